@@ -1,0 +1,83 @@
+// Shared helpers for the gfx950 kernels of libv1idx: status/error plumbing,
+// launch checks, order-preserving float keys and wave64 primitives.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include "../../include/v1idx.h"
+
+namespace v1 {
+
+// ---------------------------------------------------------------- host side
+void set_error(const char* fmt, ...);
+int hip_status(hipError_t e, const char* what);
+
+#define V1_REQUIRE(cond, ...)                  \
+    do {                                       \
+        if (!(cond)) {                         \
+            ::v1::set_error(__VA_ARGS__);      \
+            return V1_ERR_INVALID;             \
+        }                                      \
+    } while (0)
+
+// Checks the launch that was just issued (configuration errors surface here).
+#define V1_LAUNCHED(what) ::v1::hip_status(hipGetLastError(), what)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------- device side
+constexpr int kWave = 64;
+
+// Order-preserving map of an fp32 score onto uint32: a > b  <=>  key(a) > key(b).
+// -0.0 is folded onto +0.0 so that the two compare equal (IEEE semantics).
+__device__ __forceinline__ uint32_t score_key(float x) {
+    uint32_t b = __float_as_uint(x);
+    if (b == 0x80000000u) b = 0u;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_score(uint32_t k) {
+    uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(b);
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        uint32_t n = __shfl_up(v, off, kWave);
+        if (lane >= off) v += n;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t popc64(uint64_t m) { return (uint32_t)__popcll(m); }
+
+// Number of set bits of `m` strictly below this lane.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+    const uint32_t lane = __lane_id();
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    return popc64(m & below);
+}
+
+// Exact n / d whenever n * d < 2^32, with m = ceil(2^32 / d) and d >= 2
+// (d = 1 would need m = 2^32).
+__device__ __forceinline__ uint32_t small_div(uint32_t n, uint32_t m) { return __umulhi(n, m); }
+
+inline uint32_t small_div_magic(uint32_t d) {
+    return (uint32_t)((((uint64_t)1 << 32) + d - 1) / d);
+}
+
+}  // namespace v1

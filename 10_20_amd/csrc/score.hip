@@ -1,0 +1,296 @@
+// FP8 paged MQA index logits on CDNA4 MFMA (v_mfma_f32_16x16x128_f8f6f4):
+//   logits[r, j] = sum_h w[r,h] * ReLU(sum_d q[r,h,d] * k[j,d]) * s_k[j]
+// Formula: sglang/srt/layers/attention/v1_deepseek/kernels.py:248-320 and
+// experiments/fine_pool_shared_20261021/test_and_bench.py:37; the DeepGEMM
+// fp8_paged_mqa_logits call sites are runtime.py:434-444, 538-548.
+//
+// One MFMA multiplies 16 heads x 128 dims of a query by 16 keys x 128 dims:
+// lane l holds 32 FP8 bytes of head (l%16) / key (l%16) at dims 32*(l/16)..+32
+// for A / B (any consistent dim split gives the same dot product), and the
+// 16x16 fp32 result D[4*(l/16)+i][l%16] in its 4 accumulators.  The head
+// weighting is done per lane (16 heads of a 64-head query per lane group),
+// then folded across the 4 lane groups with two xor shuffles, which leaves
+// the logit of key l%16 in every lane group; the group whose index matches the
+// 16-key block keeps it, so a 64-key page ends as one logit per lane and is
+// stored with one coalesced 256-byte write.
+//
+// Shared-table rows (a prefill chunk of one request) are tiled 8 queries per
+// work-group: each 8448-byte key page is staged once in LDS (rows padded to
+// 144 bytes so that the 16-byte fragment reads are bank-conflict free) and
+// reused by 8 queries x 64 heads.  Rows with their own tables (decode) run one
+// query per work-group, each wave streaming whole pages straight from HBM.
+#include "common.h"
+
+namespace v1 {
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kKeyPitch = 144;                       // LDS bytes per staged key row
+constexpr int kPageLds = 64 * kKeyPitch + 64 * 4;    // keys + scales
+constexpr int kChunkPages = 16;                      // pages per work-group
+constexpr int kQueriesPerWave = 2;
+constexpr int kQueriesPerGroup = 4 * kQueriesPerWave;
+
+__device__ __forceinline__ v4f mfma_fp8(v8i a, v8i b) {
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
+}
+
+struct ScoreParams {
+    const uint8_t* q;
+    const uint8_t* kv;
+    int64_t kv_blocks;
+    const float* w;
+    const int32_t* ctx;
+    const int32_t* table;
+    int64_t table_stride;
+    int32_t max_blocks;
+    float* logits;
+    int64_t logits_stride;
+    int32_t max_context_len;
+    int32_t rows;
+    int32_t heads;
+    int32_t relu;
+    int32_t clean;
+};
+
+// A fragments (HB row blocks of 16 heads) of one query; zero past `heads`.
+template <int HB>
+__device__ __forceinline__ void load_q(const ScoreParams& p, int64_t row, v8i (&a)[HB]) {
+    const int l = __lane_id();
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+        const int h = hb * 16 + (l & 15);
+        if (row < p.rows && h < p.heads) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(p.q + (row * p.heads + h) * 128 + 32 * (l >> 4));
+            const u32x4 x = src[0], y = src[1];
+            a[hb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+        } else {
+            a[hb] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    }
+}
+
+// Weights of the 4 heads (per row block) whose results this lane holds.
+template <int HB>
+__device__ __forceinline__ void load_w(const ScoreParams& p, int64_t row, float (&w)[HB][4]) {
+    const int l = __lane_id();
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = hb * 16 + 4 * (l >> 4) + i;
+            w[hb][i] = (row < p.rows && h < p.heads) ? p.w[row * p.heads + h] : 0.f;
+        }
+}
+
+// Weighted head sum for the 16 keys of one B fragment; returns the logit
+// (before the key scale) of key l%16 in every lane.
+template <int HB>
+__device__ __forceinline__ float head_sum(const v8i (&a)[HB], v8i b, const float (&w)[HB][4], bool relu) {
+    float s = 0.f;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+        const v4f d = mfma_fp8(a[hb], b);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = fmaf(w[hb][i], relu ? fmaxf(d[i], 0.f) : d[i], s);
+    }
+    s += __shfl_xor(s, 16, kWave);
+    s += __shfl_xor(s, 32, kWave);
+    return s;
+}
+
+__device__ __forceinline__ int32_t page_of(const ScoreParams& p, int64_t row, int32_t blk) {
+    if (blk >= p.max_blocks) return -1;
+    const int32_t page = p.table[row * p.table_stride + blk];
+    return (page >= 0 && page < p.kv_blocks) ? page : -1;
+}
+
+__device__ __forceinline__ void store_logit(const ScoreParams& p, int64_t row, int32_t j, int32_t ctx, float v) {
+    if (row >= p.rows || j >= p.max_context_len) return;
+    if (j < ctx)
+        p.logits[row * p.logits_stride + j] = v;
+    else if (p.clean)
+        p.logits[row * p.logits_stride + j] = -__builtin_huge_valf();
+}
+
+// ------------------------------------------------------------ shared table
+template <int HB>
+__global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][kPageLds];
+    const int t = threadIdx.x, l = __lane_id(), wv = t / kWave;
+    const int64_t row0 = (int64_t)blockIdx.y * kQueriesPerGroup;
+    const int32_t chunk0 = blockIdx.x * kChunkPages;
+
+    int32_t ctx[kQueriesPerWave];
+    int32_t max_ctx = 0;
+    for (int q = 0; q < kQueriesPerGroup; ++q) {
+        const int64_t r = row0 + q;
+        if (r < p.rows) max_ctx = max(max_ctx, min(p.ctx[r], p.max_context_len));
+    }
+#pragma unroll
+    for (int q = 0; q < kQueriesPerWave; ++q) {
+        const int64_t r = row0 + wv * kQueriesPerWave + q;
+        ctx[q] = r < p.rows ? min(p.ctx[r], p.max_context_len) : 0;
+    }
+    const int32_t npages = max(0, min(kChunkPages, (max_ctx + 63) / 64 - chunk0));
+    if (npages == 0) {
+        if (p.clean) {
+            for (int q = 0; q < kQueriesPerWave; ++q) {
+                const int64_t r = row0 + wv * kQueriesPerWave + q;
+                for (int j = chunk0 * 64 + l; j < (chunk0 + kChunkPages) * 64; j += kWave) store_logit(p, r, j, ctx[q], 0.f);
+            }
+        }
+        return;
+    }
+
+    v8i a[kQueriesPerWave][HB];
+    float w[kQueriesPerWave][HB][4];
+#pragma unroll
+    for (int q = 0; q < kQueriesPerWave; ++q) {
+        const int64_t r = row0 + wv * kQueriesPerWave + q;
+        load_q<HB>(p, r, a[q]);
+        load_w<HB>(p, r, w[q]);
+    }
+
+    // staging: thread t moves 32 key bytes (key t/4, part t%4); t < 64 one scale
+    const int skey = t >> 2, spart = t & 3;
+    u32x4 st0, st1;
+    float sscale = 0.f;
+    auto fetch = [&](int32_t pg) {
+        const int32_t page = page_of(p, row0, chunk0 + pg);
+        if (page >= 0) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(p.kv + (int64_t)page * V1_PAGE_BYTES + skey * 128 + spart * 32);
+            st0 = src[0];
+            st1 = src[1];
+            if (t < 64) sscale = reinterpret_cast<const float*>(p.kv + (int64_t)page * V1_PAGE_BYTES + 8192)[t];
+        } else {
+            st0 = st1 = u32x4{0u, 0u, 0u, 0u};
+            sscale = 0.f;
+        }
+    };
+    auto stash = [&](int buf) {
+        u32x4* dst = reinterpret_cast<u32x4*>(&lds[buf][skey * kKeyPitch + spart * 32]);
+        dst[0] = st0;
+        dst[1] = st1;
+        if (t < 64) reinterpret_cast<float*>(&lds[buf][64 * kKeyPitch])[t] = sscale;
+    };
+
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int32_t pg = 0; pg < npages; ++pg) {
+        const int buf = pg & 1;
+        if (pg + 1 < npages) fetch(pg + 1);
+        float out[kQueriesPerWave];
+#pragma unroll
+        for (int q = 0; q < kQueriesPerWave; ++q) out[q] = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(&lds[buf][(kb * 16 + (l & 15)) * kKeyPitch + 32 * (l >> 4)]);
+            const u32x4 x = src[0], y = src[1];
+            const v8i b = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+#pragma unroll
+            for (int q = 0; q < kQueriesPerWave; ++q) {
+                const float s = head_sum<HB>(a[q], b, w[q], p.relu != 0);
+                if ((l >> 4) == kb) out[q] = s;
+            }
+        }
+        const float scale = reinterpret_cast<const float*>(&lds[buf][64 * kKeyPitch])[l];
+        const int32_t j = (chunk0 + pg) * 64 + l;
+#pragma unroll
+        for (int q = 0; q < kQueriesPerWave; ++q)
+            store_logit(p, row0 + wv * kQueriesPerWave + q, j, ctx[q], out[q] * scale);
+        if (pg + 1 < npages) stash(buf ^ 1);
+        __syncthreads();
+    }
+    if (p.clean) {
+        // columns of this chunk past the last staged page
+        for (int q = 0; q < kQueriesPerWave; ++q) {
+            const int64_t r = row0 + wv * kQueriesPerWave + q;
+            for (int j = (chunk0 + npages) * 64 + l; j < (chunk0 + kChunkPages) * 64; j += kWave) store_logit(p, r, j, ctx[q], 0.f);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- per row
+template <int HB>
+__global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
+    const int l = __lane_id(), wv = threadIdx.x / kWave;
+    const int64_t row = blockIdx.y;
+    const int32_t chunk0 = blockIdx.x * kChunkPages;
+    const int32_t ctx = min(p.ctx[row], p.max_context_len);
+    const int32_t npages = max(0, min(kChunkPages, (ctx + 63) / 64 - chunk0));
+    v8i a[HB];
+    float w[HB][4];
+    if (npages > 0) {
+        load_q<HB>(p, row, a);
+        load_w<HB>(p, row, w);
+    }
+    for (int32_t pg = wv; pg < kChunkPages; pg += 4) {
+        const int32_t j = (chunk0 + pg) * 64 + l;
+        if (pg >= npages) {
+            if (p.clean) store_logit(p, row, j, ctx, 0.f);
+            continue;
+        }
+        const int32_t page = page_of(p, row, chunk0 + pg);
+        float out = 0.f, scale = 0.f;
+        if (page >= 0) {
+            const uint8_t* base = p.kv + (int64_t)page * V1_PAGE_BYTES;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(base + (kb * 16 + (l & 15)) * 128 + 32 * (l >> 4));
+                const u32x4 x = src[0], y = src[1];
+                const v8i b = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+                const float s = head_sum<HB>(a, b, w, p.relu != 0);
+                if ((l >> 4) == kb) out = s;
+            }
+            scale = reinterpret_cast<const float*>(base + 8192)[l];
+        }
+        store_logit(p, row, j, ctx, out * scale);
+    }
+}
+
+}  // namespace
+}  // namespace v1
+
+using namespace v1;
+
+extern "C" int v1_score(const v1_score_args* a, void* stream) {
+    V1_REQUIRE(a != nullptr, "score: null args");
+    V1_REQUIRE(a->heads >= 1 && a->heads <= 64, "score: heads must be in [1, 64]");
+    V1_REQUIRE(a->rows >= 0 && a->max_context_len >= 0 && a->max_blocks >= 0, "score: bad shape");
+    V1_REQUIRE(a->kv_blocks > 0, "score: empty key pool");
+    V1_REQUIRE((reinterpret_cast<uintptr_t>(a->q) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->kv_pages) & 15) == 0,
+               "score: q and kv_pages must be 16-byte aligned");
+    V1_REQUIRE(a->logits_stride >= a->max_context_len, "score: logits row stride too small");
+    if (a->rows == 0 || a->max_context_len == 0) return V1_OK;
+    ScoreParams p{a->q, a->kv_pages, a->kv_blocks, a->weights, a->context_lens, a->block_table, a->block_table_stride,
+                  a->max_blocks, a->logits, a->logits_stride, a->max_context_len, a->rows, a->heads, a->relu,
+                  a->clean_logits};
+    const int hb = (a->heads + 15) / 16;
+    const uint32_t chunks = (uint32_t)cdiv(cdiv(a->max_context_len, 64), kChunkPages);
+    hipStream_t st = as_stream(stream);
+    if (a->block_table_stride == 0) {
+        const dim3 grid(chunks, (uint32_t)cdiv(a->rows, kQueriesPerGroup));
+        switch (hb) {
+            case 1: hipLaunchKernelGGL(score_shared<1>, grid, dim3(kThreads), 0, st, p); break;
+            case 2: hipLaunchKernelGGL(score_shared<2>, grid, dim3(kThreads), 0, st, p); break;
+            case 3: hipLaunchKernelGGL(score_shared<3>, grid, dim3(kThreads), 0, st, p); break;
+            default: hipLaunchKernelGGL(score_shared<4>, grid, dim3(kThreads), 0, st, p); break;
+        }
+        return V1_LAUNCHED("score_shared");
+    }
+    const dim3 grid(chunks, (uint32_t)a->rows);
+    switch (hb) {
+        case 1: hipLaunchKernelGGL(score_rows<1>, grid, dim3(kThreads), 0, st, p); break;
+        case 2: hipLaunchKernelGGL(score_rows<2>, grid, dim3(kThreads), 0, st, p); break;
+        case 3: hipLaunchKernelGGL(score_rows<3>, grid, dim3(kThreads), 0, st, p); break;
+        default: hipLaunchKernelGGL(score_rows<4>, grid, dim3(kThreads), 0, st, p); break;
+    }
+    return V1_LAUNCHED("score_rows");
+}

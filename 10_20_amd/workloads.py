@@ -1,0 +1,200 @@
+"""Deterministic synthetic inputs for the query-indexing workloads (host numpy,
+PCG64 seeded; identical on every machine).
+
+FP8 is OCP e4m3fn.  Quantisation follows the reference rule
+s = 2^ceil(log2(max(absmax, 1e-4) / 448)), x8 = e4m3(x / s)
+(sglang/srt/layers/attention/v1_native/grouping.py:41-45), with the exponent
+taken exactly from frexp rather than from a floating log2.
+
+Native page layout (8448 bytes): 64 tokens x 128 FP8 bytes, then 64 fp32
+scales (sglang/srt/layers/attention/v1_deepseek/kernels.py:1-3).
+"""
+from dataclasses import dataclass, field
+
+import numpy as np
+
+PAGE = 64
+DIM = 128
+PAGE_BYTES = 8448
+MLA_ROW_BYTES = 656  # 512 FP8 latent + 64 bf16 RoPE + fp32 scales (41 x 16 B)
+TOPK = 2048
+
+
+def rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+# ------------------------------------------------------------------- FP8
+def _e4m3_positive_values():
+    """Values of the 127 non-negative finite e4m3fn codes 0x00..0x7e, ascending."""
+    codes = np.arange(127)
+    e = codes >> 3
+    m = codes & 7
+    return np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7.0))
+
+
+_E4M3_POS = _e4m3_positive_values()
+
+
+def e4m3_encode(x):
+    """Round-to-nearest-even float -> e4m3fn byte; |x| must be <= 448."""
+    x = np.asarray(x, dtype=np.float32)
+    a = np.abs(x).astype(np.float64)
+    if a.size and float(a.max()) > 448.0:
+        raise ValueError("e4m3_encode: value beyond the e4m3fn range")
+    hi = np.clip(np.searchsorted(_E4M3_POS, a, side="left"), 0, 126)
+    lo = np.clip(hi - 1, 0, 126)
+    dl = a - _E4M3_POS[lo]
+    dh = _E4M3_POS[hi] - a
+    pick_hi = (dh < dl) | ((dh == dl) & ((hi & 1) == 0))
+    code = np.where(pick_hi, hi, lo).astype(np.uint8)
+    return code | (np.signbit(x).astype(np.uint8) << 7)
+
+
+def pow2_scale(absmax):
+    """2^ceil(log2(max(absmax, 1e-4) / 448)) in float32, exactly."""
+    v = np.maximum(np.asarray(absmax, dtype=np.float32), np.float32(1e-4)) / np.float32(448.0)
+    m, e = np.frexp(v)
+    e = np.where(m == 0.5, e - 1, e)
+    return np.ldexp(np.float32(1.0), e).astype(np.float32)
+
+
+def quantize_rows(x):
+    """Per-row (token) FP8 quantisation: returns (bytes [n, d], scale [n])."""
+    x = np.asarray(x, dtype=np.float32)
+    s = pow2_scale(np.abs(x).max(axis=-1))
+    return e4m3_encode(x / s[..., None]), s
+
+
+def pack_pages(k8, ks, n_pages=None):
+    """Native pages [n_pages, 8448] from token keys k8 [n, 128] and scales [n]."""
+    n = k8.shape[0]
+    pages = n_pages if n_pages is not None else -(-n // PAGE)
+    out = np.zeros((pages, PAGE_BYTES), dtype=np.uint8)
+    kk = np.zeros((pages * PAGE, DIM), dtype=np.uint8)
+    kk[:n] = k8
+    ss = np.zeros(pages * PAGE, dtype=np.float32)
+    ss[:n] = ks
+    out[:, :8192] = kk.reshape(pages, 8192)
+    out[:, 8192:] = ss.reshape(pages, PAGE).view(np.uint8)
+    return out
+
+
+def scatter_pages(pool_pages, logical_pages, table):
+    """Places logical page i at physical page table[i] of a zero pool."""
+    pool = np.zeros((pool_pages, logical_pages.shape[1]), dtype=np.uint8)
+    pool[table[: len(logical_pages)]] = logical_pages
+    return pool
+
+
+# --------------------------------------------------------------- configs
+@dataclass
+class Workload:
+    name: str
+    seed: int
+    arrays: dict = field(default_factory=dict)
+    params: dict = field(default_factory=dict)
+
+
+def config1(seed=19, rows=1024):
+    """The reference example shape with FP8 N(0,1) data
+    (sglang/srt/layers/attention/v1_deepseek/example_v1_query_single_head.py:11-41):
+    1024 queries x 1 head, 4097 keys in four built 1K buckets (members reversed
+    per bucket), route of 40 of 64 pages (P=128), 2688 fine candidates
+    (40 pages + 64 sink + 64 tail), query i sees candidates < 1664+i, Top-2048,
+    native table = random pages of a 4096-page pool, 656-byte row gather."""
+    g = rng(seed)
+    B, P, CAP, TAKE, N, WINDOW, SINK = rows, 128, 128, 40, 4097, 64, 64
+    POOL = 4096
+    nt_row = g.permutation(POOL)[:P].astype(np.int32)
+    rt_row = g.permutation(CAP).astype(np.int32)
+    q8, qs = quantize_rows(g.standard_normal((B, DIM), dtype=np.float32))
+    k8, ks = quantize_rows(g.standard_normal((N, DIM), dtype=np.float32))
+    # native pool: logical page i of the request at physical page nt_row[i]
+    native = scatter_pages(POOL, pack_pages(k8, ks), nt_row)
+    logical_order = np.arange(4096, dtype=np.int32).reshape(4, 1024)[:, ::-1].reshape(64, 64).copy()
+    members = np.full((CAP, 64), -1, dtype=np.int32)
+    members[rt_row[:64]] = logical_order
+    # fine pool: reordered pages at rt_row[i], then 68 tail scratch pages
+    fine = np.zeros((CAP + 68, PAGE_BYTES), dtype=np.uint8)
+    ro_k8, ro_ks = k8[logical_order.reshape(-1)], ks[logical_order.reshape(-1)]
+    fine[rt_row[:64]] = pack_pages(ro_k8, ro_ks)
+    # centers: mean of 8 consecutive reordered members, FP8 with pow2 scale
+    kf = ro_k8.astype(np.int64)
+    dq = decode_table()[ro_k8] * ro_ks[:, None]
+    mean = dq.reshape(512, 8, DIM).sum(axis=1, dtype=np.float32) / np.float32(8.0)
+    c8, cs = quantize_rows(mean)
+    centers = pack_pages(c8, cs)  # 8 pages = 512 centers
+    w = qs[:, None].astype(np.float32)  # H = 1: weight = q scale
+    fine_lens = np.minimum(2688, 1664 + np.arange(B)).astype(np.int32)
+    lat_pool = g.integers(0, 256, size=(POOL * PAGE, MLA_ROW_BYTES), dtype=np.uint8)
+    del kf
+    return Workload("config1", seed, dict(
+        q8=q8.reshape(B, 1, DIM), w=w, native=native, fine=fine, members=members, centers=centers,
+        nt=np.broadcast_to(nt_row, (B, P)).copy(), rt=np.broadcast_to(rt_row, (B, P)).copy(),
+        center_table=np.arange(8, dtype=np.int32), lens=np.full(B, N, np.int32),
+        takes=np.full(B, TAKE, np.int32), tail_rows=np.zeros(B, np.int32), fine_lens=fine_lens,
+        latent=lat_pool),
+        dict(B=B, P=P, CAP=CAP, TAKE=TAKE, N=N, WINDOW=WINDOW, SINK=SINK, TOPK=TOPK, H=1, FT_COLS=TAKE + 68,
+             WIDTH=2688))
+
+
+def config3(seed=3, rows=1024, pool_tokens=1 << 20, window_pages=512, pad=0.05):
+    """K/V slot gather: 656-byte rows of a 1M-token paged pool; each query has
+    its own 512-page request window (random pages of the pool) and 2048 ids
+    uniform over the window's 32768 tokens, 5% set to -1."""
+    g = rng(seed)
+    pool_pages = pool_tokens // PAGE
+    pool = g.integers(0, 256, size=(pool_tokens, MLA_ROW_BYTES), dtype=np.uint8)
+    table = np.stack([g.choice(pool_pages, window_pages, replace=False) for _ in range(rows)]).astype(np.int32)
+    ids = g.integers(0, window_pages * PAGE, size=(rows, TOPK), dtype=np.int64).astype(np.int32)
+    ids[g.random((rows, TOPK)) < pad] = -1
+    return Workload("config3", seed, dict(pool=pool, table=table, ids=ids),
+                    dict(rows=rows, top=TOPK, row_bytes=MLA_ROW_BYTES, page_bits=6))
+
+
+def config4(seed=4, rows=4096, ctx_tokens=32768, heads=64, first_pos=28672):
+    """DeepSeek-V3.2-style prefill indexer chunk: 4096 queries x 64 heads FP8,
+    32768 context keys FP8 in 64-token pages (random 512-page table), weights
+    U(0,1); query i at position first_pos+i sees keys <= first_pos+i; Top-2048,
+    slot mapping through the page table, 656-byte latent row gather."""
+    g = rng(seed)
+    pages = ctx_tokens // PAGE
+    q8, _ = quantize_rows(g.standard_normal((rows * heads, DIM), dtype=np.float32))
+    w = g.random((rows, heads), dtype=np.float32)
+    k8, ks = quantize_rows(g.standard_normal((ctx_tokens, DIM), dtype=np.float32))
+    table = g.permutation(pages).astype(np.int32)
+    native = scatter_pages(pages, pack_pages(k8, ks), table)
+    latent = g.integers(0, 256, size=(ctx_tokens, MLA_ROW_BYTES), dtype=np.uint8)
+    lens = (first_pos + 1 + np.arange(rows)).astype(np.int32)
+    return Workload("config4", seed, dict(q8=q8.reshape(rows, heads, DIM), w=w, native=native, table=table,
+                                          lens=lens, latent=latent),
+                    dict(rows=rows, heads=heads, ctx=ctx_tokens, topk=TOPK, row_bytes=MLA_ROW_BYTES))
+
+
+def config5(seed=5, rows=128, heads=64, pool_pages=32768, lo=4096, hi=131072):
+    """Decode batch: 128 requests x 1 query (64 heads FP8), context lengths
+    round(exp(U(ln 4K, ln 128K))), each request's pages random distinct pages of
+    a 2M-token pool; full scoring -> Top-2048 -> slots -> 656-byte row gather."""
+    g = rng(seed)
+    ctx = np.rint(np.exp(g.uniform(np.log(lo), np.log(hi), size=rows))).astype(np.int32)
+    max_pages = int(-(-ctx.max() // PAGE))
+    table = np.zeros((rows, max_pages), dtype=np.int32)
+    for r in range(rows):
+        n = -(-int(ctx[r]) // PAGE)
+        table[r, :n] = g.choice(pool_pages, n, replace=False)
+    q8, _ = quantize_rows(g.standard_normal((rows * heads, DIM), dtype=np.float32))
+    w = g.random((rows, heads), dtype=np.float32)
+    k8, ks = quantize_rows(g.standard_normal((pool_pages * PAGE, DIM), dtype=np.float32))
+    native = pack_pages(k8, ks)
+    latent_rows = pool_pages * PAGE
+    return Workload("config5", seed, dict(q8=q8.reshape(rows, heads, DIM), w=w, native=native, table=table,
+                                          lens=ctx),
+                    dict(rows=rows, heads=heads, topk=TOPK, row_bytes=MLA_ROW_BYTES, latent_rows=latent_rows,
+                         max_ctx=int(ctx.max())))
+
+
+def decode_table():
+    """float32 value of each of the 256 e4m3fn codes (NaN for 0x7f / 0xff)."""
+    vals = np.concatenate([_E4M3_POS, [np.nan]]).astype(np.float32)
+    return np.concatenate([vals, -vals]).astype(np.float32)

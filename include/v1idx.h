@@ -1,0 +1,279 @@
+/*
+ * v1idx.h -- C ABI of the MI355X (gfx950) query-indexing library `libv1idx.so`.
+ *
+ * Every entry point takes plain device pointers, element counts and strides,
+ * and a HIP stream (passed as `void*`, i.e. a `hipStream_t`).  No entry point
+ * allocates device memory, synchronises the stream or reads device data on the
+ * host, so every launch is stream ordered and can be captured in a hipGraph.
+ * Strides are in ELEMENTS of the pointed-to type unless the name ends in
+ * `_bytes`.  FP8 data is OCP e4m3fn (`torch.float8_e4m3fn`), handled as bytes.
+ *
+ * Return value: V1_OK (0) or a negative V1_ERR_* code; `v1_last_error()` then
+ * holds a message (thread local).  V1_ERR_INVALID means the arguments failed
+ * validation and nothing was launched.
+ *
+ * A "native page" is 8448 bytes: 64 tokens x 128 FP8 bytes followed by 64 fp32
+ * per-token scales (sglang/srt/layers/attention/v1_deepseek/kernels.py:1-3).
+ */
+#ifndef V1IDX_H
+#define V1IDX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define V1_OK 0
+#define V1_ERR_INVALID (-1)
+#define V1_ERR_HIP (-2)
+#define V1_ERR_UNSUPPORTED (-3)
+
+#define V1_PAGE_TOKENS 64
+#define V1_PAGE_BYTES 8448
+#define V1_HEAD_DIM 128
+#define V1_MAX_TOPK 2048
+#define V1_TAIL_SCRATCH_PAGES 68
+
+const char* v1_last_error(void);
+int v1_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * fused.route: per-row page max-of-8, stable top-`take` page selection and
+ * optional fine-page-table write.
+ * Replaces V1QueryKernel::route
+ *   sglang/kernels/jit/csrc/deepseek_v4/v1_query.cuh:155-180 (kernel :7-49).
+ * Ties between equal page maxima resolve to the lower page index.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    const float* scores;      /* [batch, score_cols], row stride score_stride */
+    int64_t score_stride;
+    int32_t batch;
+    int32_t score_cols;
+    const int32_t* lens;      /* [batch] */
+    const int32_t* takes;     /* [batch] */
+    void* selected;           /* [batch, take_stride] int32 or int64 */
+    int32_t selected_bits;    /* 32 or 64 */
+    int32_t take_stride;      /* K */
+    int32_t pages;            /* P: row length of rt */
+    const int32_t* rt;        /* [batch, pages] */
+    int32_t* ft;              /* [batch, ft_cols] */
+    int32_t ft_cols;
+    const int32_t* tail_rows; /* [batch] */
+    int32_t capacity;
+    int32_t fill_table;
+} v1_route_args;
+int v1_route(const v1_route_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * fused.topk: in-place sink/tail mask, exact Top-T (T <= 2048) over the
+ * first fine_lens[b] candidates of each row, and the raw -> logical ->
+ * physical mapping epilogue with optional x4 expansion.
+ * Replaces V1QueryKernel::topk
+ *   sglang/kernels/jit/csrc/deepseek_v4/v1_query.cuh:181-220 (kernel :62-153).
+ * Selection order: score descending, ties toward the LOWER candidate index;
+ * -0.0 equals +0.0.  Each output row lists the selected candidates in
+ * ascending candidate index, then -1 padding.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    float* scores;             /* [batch, cols], row stride score_stride; masked in place */
+    int64_t score_stride;
+    int32_t batch;
+    int32_t cols;
+    const int32_t* fine_lens;  /* [batch] */
+    const int32_t* members;    /* [member_pages, 64] */
+    int64_t member_pages;
+    const int32_t* rt;         /* [batch, pages] */
+    const int32_t* nt;         /* [batch, pages] */
+    int32_t pages;
+    const void* selected;      /* [batch, take_stride] int32 or int64 */
+    int32_t selected_bits;
+    int32_t take_stride;
+    const int32_t* lens;       /* [batch] */
+    const int32_t* takes;      /* [batch] */
+    int32_t* physical;         /* [batch, topk] (written when physical_output) */
+    int32_t* logical;          /* [batch, topk] */
+    int32_t* raw;              /* [batch, topk] (written when physical_output) */
+    int32_t topk;
+    int32_t window;
+    int32_t mask;
+    int32_t* expanded;         /* [batch, expansion_stride] or NULL */
+    int32_t expansion_stride;  /* 0 or 4*topk+64 */
+    int32_t physical_output;
+    int32_t bucket_from_rank;
+    const int32_t* fine_table; /* [batch, fine_table_cols] */
+    int32_t fine_table_cols;
+    int32_t direct_fine;
+    void* workspace;           /* rows longer than 32768 columns: >= v1_topk_workspace() bytes */
+    int64_t workspace_bytes;
+} v1_topk_args;
+int64_t v1_topk_workspace(int32_t batch, int32_t cols, int32_t topk);
+int v1_topk(const v1_topk_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Top-T with page-table transform (rows of any length, any batch):
+ *   out = raw < 0 ? -1 : (page_table[b, raw >> page_bits] << page_bits) | (raw & mask)
+ * Replaces TopKKernel::transform / topk_transform_512_v2
+ *   sglang/kernels/jit/csrc/deepseek_v4/topk_v2.cuh:352-460,
+ *   sglang/kernels/jit/include/sgl_kernel/deepseek_v4/topk_impl.cuh:156-190.
+ * Rows longer than one work-group's register tile are split over several
+ * work-groups; `workspace` (device memory, >= v1_topk_workspace() bytes)
+ * then holds the per-segment candidates.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    const float* scores;        /* [batch, cols], row stride score_stride */
+    int64_t score_stride;
+    int32_t batch;
+    int32_t cols;
+    const int32_t* seq_lens;    /* [batch] */
+    const int32_t* page_table;  /* [batch, page_table_cols], row stride page_table_stride */
+    int64_t page_table_stride;
+    int32_t page_table_cols;    /* entries past it map to -1 */
+    int32_t page_bits;
+    int32_t* page_indices;      /* [batch, topk] */
+    int32_t* raw_indices;       /* [batch, topk] or NULL */
+    int32_t topk;
+    void* workspace;
+    int64_t workspace_bytes;
+} v1_topk_transform_args;
+int v1_topk_transform(const v1_topk_transform_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * FP8 paged MQA index logits (the DeepGEMM fp8_paged_mqa_logits contract):
+ *   logits[r, j] = sum_h w[r,h] * ReLU(sum_d q[r,h,d] * k[j,d]) * s_k[j]
+ * for j < context_lens[r]; k / s_k come from native pages through
+ * block_table[r, j / 64].  block_table_stride == 0 means every row shares one
+ * table (a prefill chunk of one request); rows are then tiled together so that
+ * each key page is staged once per row tile.  Columns in
+ * [context_lens[r], max_context_len) are set to -inf when clean_logits.
+ * Formula: sglang/srt/layers/attention/v1_deepseek/kernels.py:248-320,
+ * experiments/fine_pool_shared_20261021/test_and_bench.py:37; call sites
+ * sglang/srt/layers/attention/v1_deepseek/runtime.py:434-444, 538-548.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    const uint8_t* q;            /* [rows, heads, 128] e4m3fn */
+    const uint8_t* kv_pages;     /* [blocks, 8448] */
+    int64_t kv_blocks;
+    const float* weights;        /* [rows, heads] */
+    const int32_t* context_lens; /* [rows] */
+    const int32_t* block_table;  /* [rows, max_blocks], row stride block_table_stride */
+    int64_t block_table_stride;
+    int32_t max_blocks;
+    float* logits;               /* [rows, logits_stride] */
+    int64_t logits_stride;
+    int32_t max_context_len;
+    int32_t rows;
+    int32_t heads;               /* 1..64 */
+    int32_t relu;                /* 1: DSA ReLU rule; 0: signed scores */
+    int32_t clean_logits;
+} v1_score_args;
+int v1_score(const v1_score_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * _gather_slots: logical -> req[logical] -> K and V rows of one head into
+ * contiguous [rows, top, 128] outputs; ids < 0 give zero rows.
+ * Replaces sglang/srt/layers/attention/v1_native/kernels.py:62-77 (_gather_slots)
+ * as launched by GatherWorkspace.gather (:102-111).  Strides in elements.
+ * ids >= req_len or req entries outside [0, pool_slots) give zero rows.
+ * ---------------------------------------------------------------------- */
+int v1_gather_slots(const void* k_pool, const void* v_pool, int64_t pool_slots, int32_t elem_bytes,
+                    int64_t ks0, int64_t ks1, int64_t ks2,
+                    int64_t vs0, int64_t vs1, int64_t vs2, int32_t head,
+                    const int32_t* req, int64_t req_len, const int32_t* ids, int64_t ids_stride,
+                    int32_t rows, int32_t top, void* k_out, void* v_out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Byte-row gather (the _gather_slots contract generalised to opaque rows,
+ * e.g. 656-byte MLA latent rows): for t = r*top + i, id = ids[r*ids_stride+i];
+ *   id < 0            -> out row t = zeros
+ *   map == NULL       -> physical = id
+ *   otherwise         -> physical = (map[r*map_stride + (id >> map_shift)] << map_shift)
+ *                                   | (id & ((1 << map_shift) - 1))
+ * and out[t*row_bytes ...] = pool[physical*pool_stride_bytes ...].
+ * map_stride == 0 shares one map (the reference REQ vector) across rows;
+ * map_len is the number of entries of one map row.  An id whose map entry or
+ * physical row falls outside [0, map_len) / [0, pool_rows) yields a zero row
+ * (the reference leaves such ids undefined).
+ * ---------------------------------------------------------------------- */
+int v1_gather_rows(const void* pool, int64_t pool_rows, int64_t row_bytes, int64_t pool_stride_bytes,
+                   const int32_t* map, int64_t map_len, int64_t map_stride, int32_t map_shift,
+                   const int32_t* ids, int64_t ids_stride, int32_t rows, int32_t top,
+                   void* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * _sort: per group g of n keys, out[g*n + i] = perm[g*n + pos_i] where pos
+ * orders the group's keys descending, ties by ascending position.
+ * fp32 keys (-0.0 == +0.0):  sglang/srt/layers/attention/v1_native/fused_grouping.py:64-76
+ * (only when *flag < 0; head h uses offset h*head_stride).  int64 keys are the
+ * same rule over signed 64-bit keys.  perm and out must not overlap.
+ * n is a power of two in [2, 4096].
+ * ---------------------------------------------------------------------- */
+int v1_sort_f32(const int32_t* perm, int32_t* out, const float* keys, const int32_t* flag,
+                int32_t n, int32_t groups, int32_t heads, int64_t head_stride, void* stream);
+int v1_sort_i64(const int32_t* perm, int32_t* out, const int64_t* keys, const int32_t* flag,
+                int32_t n, int32_t groups, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Page manager: sglang/srt/layers/attention/v1_deepseek/kernels.py:57-179
+ * (fingerprint 57-69, match_pages 72-113, allocate 116-131, publish 134-167,
+ * release 170-179).  Each call handles one 16-page bucket record gated by
+ * meta[2] (active); meta[1] is the lease.  page_bytes is 8448 for the
+ * reference pages.  status (int32, may be NULL) receives bit 0 when
+ * allocate finds the free stack exhausted (the reference device_assert).
+ * ---------------------------------------------------------------------- */
+int v1_fingerprint(const uint8_t* tmp, const int32_t* map, const int32_t* meta, int64_t* hash,
+                   int32_t pages, int64_t page_bytes, void* stream);
+int v1_match_pages(const uint8_t* tmp, const int32_t* map, const int64_t* hash, const int32_t* meta,
+                   const uint8_t* fine, const int32_t* members, const int64_t* hashes,
+                   const int32_t* refs, int32_t* match, int32_t pages, int32_t capacity,
+                   int64_t page_bytes, void* stream);
+int v1_allocate(const int32_t* meta, const int32_t* match, int32_t* free_stack, int32_t* count,
+                int32_t* refs, int32_t* tables, uint8_t* fresh, int32_t pages, int32_t* status,
+                void* stream);
+int v1_publish(const uint8_t* tmp, const uint8_t* centers_src, const int32_t* map, const int64_t* hash,
+               const int32_t* meta, const int32_t* tables, const uint8_t* fresh, uint8_t* fine,
+               uint8_t* centers, int32_t* members, int64_t* hashes, int32_t pages,
+               int64_t page_bytes, void* stream);
+int v1_release(const int32_t* table, int32_t* refs, int32_t* free_stack, int32_t* count,
+               int32_t pages, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Query metadata, fine page tables and shared tail staging:
+ * query_metadata    sglang/srt/layers/attention/v1_deepseek/kernels.py:568-591
+ * query_lengths     kernels.py:224-245
+ * fine_table_shared kernels.py:488-514   (tail_rows == NULL: fine_table :379-404)
+ * stage_tail_shared kernels.py:518-564   (tail_rows == NULL: stage_tail :407-441)
+ * mask_fine         kernels.py:444-472
+ * output_ids        kernels.py:323-376
+ * ---------------------------------------------------------------------- */
+int v1_query_metadata(const int32_t* lens, const int32_t* nt, int32_t* fine_lens, int32_t* takes,
+                      int32_t* dg_lens, int32_t* center_lens, int32_t* tail_rows, int32_t rows,
+                      int32_t np, int32_t topk, int32_t num, int32_t den, int32_t sink,
+                      int32_t window, void* stream);
+int v1_query_lengths(const int32_t* lens, int32_t* fine_lens, int32_t* takes, int32_t rows,
+                     int32_t topk, int32_t num, int32_t den, int32_t sink, int32_t window,
+                     void* stream);
+int v1_fine_table(const int32_t* rt, const void* selected, int32_t selected_bits,
+                  const int32_t* takes, int32_t* ft, const int32_t* tail_rows, int32_t rows,
+                  int32_t capacity, int32_t maxp, int32_t take_stride, int32_t fp,
+                  int32_t scratch, void* stream);
+int v1_stage_tail(const uint8_t* native, const int32_t* nt, const int32_t* lens, uint8_t* fine,
+                  const int32_t* tail_rows, int32_t rows, int32_t capacity, int32_t np,
+                  int32_t scratch, int32_t sink, int32_t window, int64_t native_pages,
+                  int64_t fine_pages, void* stream);
+int v1_mask_fine(float* scores, int64_t score_stride, const void* selected, int32_t selected_bits,
+                 const int32_t* rt, const int32_t* members, const int32_t* lens,
+                 const int32_t* takes, int32_t rows, int32_t maxp, int32_t take_stride,
+                 int32_t width, int32_t sink, int32_t window, void* stream);
+int v1_output_ids(const int32_t* raw, const float* scores, int64_t score_stride,
+                  const int32_t* members, const int32_t* rt, const int32_t* nt,
+                  const void* selected, int32_t selected_bits, const int32_t* lens,
+                  const int32_t* takes, int32_t* out, int32_t* logical, const int32_t* ft,
+                  int32_t rows, int32_t maxp, int32_t np, int32_t take_stride, int32_t width,
+                  int32_t topk, int32_t sink, int32_t window, int32_t map_physical,
+                  int32_t direct_fine, int32_t fp, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* V1IDX_H */

@@ -1,0 +1,443 @@
+"""Numpy restatement of the V1 query-indexing path (test infrastructure only).
+
+Integer division follows C / Triton semantics (truncation toward zero) where a
+negative operand can occur; see tdiv().
+"""
+import numpy as np
+
+NEG_INF = np.float32(-np.inf)
+
+
+def tdiv(a, b):
+    """C-style integer division (truncates toward zero)."""
+    a = np.asarray(a, dtype=np.int64)
+    q = np.abs(a) // b
+    return np.where(a < 0, -q, q)
+
+
+# ----------------------------------------------------------------- FP8
+def e4m3_decode(codes):
+    """OCP e4m3fn byte -> float32 from the bit fields (1 sign, 4 exponent with
+    bias 7, 3 mantissa; exponent 0 is subnormal; 0x7f/0xff are NaN)."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    s = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 7
+    v = np.where(e == 0, m * 2.0 ** -9, (8 + m) * 2.0 ** (e - 10.0))
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return (s * v).astype(np.float32)
+
+
+# -------------------------------------------------------------- ordering
+def score_key(x):
+    """Order-preserving uint32 key of fp32 scores; -0.0 folded onto +0.0."""
+    b = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32).copy()
+    b[b == 0x80000000] = 0
+    return np.where(b & 0x80000000, ~b, b | np.uint32(0x80000000)).astype(np.uint32)
+
+
+def top_order(values, count):
+    """Indices of the `count` largest values, value descending, ties by lower index."""
+    k = score_key(values)
+    return np.argsort(~k, kind="stable")[:count]
+
+
+def topk_select(row, L, T):
+    """Selected raw candidates of one row, ascending, -1 padded to T.
+    L <= T takes [0, L) (sglang/kernels/jit/csrc/deepseek_v4/topk_v2.cuh:136-143,
+    v1_query.cuh:109-111); otherwise the T largest of row[:L]."""
+    out = np.full(T, -1, dtype=np.int64)
+    if L <= T:
+        out[:L] = np.arange(L)
+        return out
+    out[:] = np.sort(top_order(row[:L], T))
+    return out
+
+
+# ----------------------------------------------------------------- route
+def route(scores, lens, takes, selected, pages, rt, ft, tail_rows, capacity, fill_table):
+    """sglang/kernels/jit/csrc/deepseek_v4/v1_query.cuh:7-49 (in place on
+    selected / ft).  Ties between equal page maxima go to the lower page."""
+    B = scores.shape[0]
+    K = selected.shape[1]
+    for b in range(B):
+        active = max(int(lens[b]) - 1, 0) // 1024 * 16
+        take = int(takes[b])
+        if fill_table:
+            for j in range(max(take, 0), ft.shape[1]):
+                ft[b, j] = capacity + int(tail_rows[b]) * 68 + min(j - take, 67)
+        if take >= active:
+            selected[b, :] = np.arange(K)
+            if fill_table:
+                n = max(0, min(take, K))
+                ft[b, :n] = rt[b, :n]
+            continue
+        vals = np.full(pages, NEG_INF, dtype=np.float32)
+        if active:
+            vals[:active] = np.fmax.reduce(scores[b, : 8 * active].reshape(active, 8), axis=1)
+        order = top_order(vals, pages)
+        selected[b, :] = order[:K]
+        if fill_table:
+            n = max(0, min(take, pages))
+            ft[b, :n] = rt[b, order[:n]]
+
+
+# ------------------------------------------------------------ fused topk
+def _bounds(n, window, sink_cap=64):
+    sink = min(n, sink_cap)
+    tail = max(sink, min(max(n - 1, 0) // 1024 * 1024, max(sink, n - window)))
+    return sink, tail
+
+
+def _map_row(raw, L, row_scores, take, sink, tail, n, members, rt_row, nt_row, sel_row, ft_row):
+    """raw -> (logical, physical) of one row (v1_query.cuh:121-139)."""
+    raw = np.asarray(raw, dtype=np.int64)
+    valid = (raw >= 0) & (raw < L)
+    valid &= row_scores[np.where(valid, raw, 0)] != NEG_INF
+    lg = np.full(raw.shape, -1, dtype=np.int64)
+    fm = valid & (raw < take * 64)
+    if fm.any():
+        r = raw[fm]
+        page = ft_row[r // 64] if ft_row is not None else rt_row[sel_row[r // 64]]
+        lg[fm] = members[page, r % 64]
+    tm = valid & (raw >= take * 64)
+    off = raw[tm] - take * 64
+    lg[tm] = np.where(off < sink, off, tail + off - sink)
+    ok = valid & (lg >= 0) & (lg < n)
+    safe = np.where(ok, lg, 0)
+    ph = np.where(ok, nt_row[safe // 64].astype(np.int64) * 64 + safe % 64, -1)
+    return np.where(ok, lg, -1).astype(np.int32), ph.astype(np.int32)
+
+
+def fused_topk(scores, fine_lens, members, rt, nt, selected, lens, takes, T, window, mask, expansion_stride,
+               physical_output, bucket_from_rank, fine_table, direct_fine):
+    """sglang/kernels/jit/csrc/deepseek_v4/v1_query.cuh:62-153.  Masks `scores`
+    in place; returns dict(physical, logical, raw, expanded)."""
+    B, cols = scores.shape
+    P = rt.shape[1]
+    physical = np.full((B, T), -1, dtype=np.int32)
+    logical = np.full((B, T), -1, dtype=np.int32)
+    raw_out = np.full((B, T), -1, dtype=np.int32)
+    expanded = np.full((B, expansion_stride), -1, dtype=np.int32) if expansion_stride else None
+    for b in range(B):
+        n, take = int(lens[b]), int(takes[b])
+        sink, tail = _bounds(n, window)
+        if mask:
+            for r in range(take):
+                rank = int(selected[b, r])
+                if bucket_from_rank:
+                    bucket = int(tdiv(rank, 16)) * 1024
+                else:
+                    page = int(rt[b, rank])
+                    bucket = int(tdiv(members[page, 0], 1024)) * 1024
+                if bucket < sink or bucket + 1024 > tail:
+                    page = int(rt[b, rank])
+                    lg = members[page]
+                    kill = (lg < sink) | (lg >= tail)
+                    cols_r = r * 64 + np.arange(64)
+                    ok = cols_r < cols
+                    scores[b, cols_r[kill & ok]] = NEG_INF
+        L = min(int(fine_lens[b]), cols)
+        raw = topk_select(scores[b], L, T)
+        lg, ph = _map_row(raw, L, scores[b], take, sink, tail, n, members, rt[b], nt[b], selected[b],
+                          fine_table[b] if direct_fine else None)
+        logical[b] = lg
+        if physical_output:
+            physical[b] = ph
+            raw_out[b] = raw
+        if expansion_stride:
+            ex = np.where(lg[:, None] < 0, -1, 4 * lg[:, None].astype(np.int64) + np.arange(4))
+            expanded[b, :4 * T] = ex.reshape(-1)
+    return dict(physical=physical, logical=logical, raw=raw_out, expanded=expanded)
+
+
+def transform_topk(scores, seq_lens, page_table, T, page_bits):
+    """topk_impl.cuh:156-190 transform after selection: returns (page_indices, raw)."""
+    B, cols = scores.shape
+    out = np.full((B, T), -1, dtype=np.int64)
+    raws = np.full((B, T), -1, dtype=np.int64)
+    mask = (1 << page_bits) - 1
+    for b in range(B):
+        L = min(int(seq_lens[b]), cols)
+        raw = topk_select(scores[b], L, T)
+        raws[b] = raw
+        ok = raw >= 0
+        r = raw[ok]
+        out[b, ok] = (page_table[b, r >> page_bits].astype(np.int64) << page_bits) | (r & mask)
+    return out.astype(np.int32), raws.astype(np.int32)
+
+
+# ------------------------------------------------------ unfused mask / map
+def mask_fine(scores, selected, rt, members, lens, takes, width, sink_cap, window):
+    """sglang/srt/layers/attention/v1_deepseek/kernels.py:444-472 (in place)."""
+    B = scores.shape[0]
+    j = np.arange(width)
+    for b in range(B):
+        n, take = int(lens[b]), int(takes[b])
+        sink, tail = _bounds(n, window, sink_cap)
+        count = take * 64 + sink + n - tail
+        fine = j < take * 64
+        lg = np.full(width, -1, dtype=np.int64)
+        if fine.any():
+            jj = j[fine]
+            pages = rt[b, selected[b, jj // 64]]
+            lg[fine] = members[pages, jj % 64]
+        good = (j < count) & (~fine | ((lg >= sink) & (lg < tail)))
+        scores[b, :width][~good] = NEG_INF
+
+
+def output_ids(raw, scores, members, rt, nt, selected, lens, takes, width, topk, sink_cap, window, map_physical,
+               direct_fine, ft):
+    """sglang/srt/layers/attention/v1_deepseek/kernels.py:323-376."""
+    B = raw.shape[0]
+    out = np.full((B, topk), -1, dtype=np.int32)
+    logical = np.full((B, topk), -1, dtype=np.int32)
+    for b in range(B):
+        n, take = int(lens[b]), int(takes[b])
+        sink, tail = _bounds(n, window, sink_cap)
+        for j in range(topk):
+            rw = int(raw[b, j])
+            if not (0 <= rw < width):
+                continue
+            if rw < take * 64:
+                page = int(ft[b, rw // 64]) if direct_fine else int(rt[b, int(selected[b, rw // 64])])
+                lg = int(members[page, rw % 64])
+            else:
+                off = rw - take * 64
+                lg = off if off < sink else tail + off - sink
+            if scores[b, rw] == NEG_INF or not (0 <= lg < n):
+                continue
+            logical[b, j] = lg
+            if map_physical:
+                out[b, j] = int(nt[b, lg // 64]) * 64 + lg % 64
+    return out, logical
+
+
+# -------------------------------------------------------------- metadata
+def geometry(n, topk, num, den, sink_cap, window):
+    """kernels.py:224-245, 568-582: (pages, take, sink, tail, fine)."""
+    pages = max(n - 1, 0) // 1024 * 16
+    take = min(pages, max((pages * num + den - 1) // den, -(-topk // 64)))
+    sink, tail = _bounds(n, window, sink_cap)
+    return pages, take, sink, tail, take * 64 + sink + n - tail
+
+
+def query_metadata(lens, nt, topk, num, den, sink_cap, window):
+    """kernels.py:568-591: (fine_lens, takes, dg_lens, center_lens, tail_rows)."""
+    B, NP = nt.shape
+    outs = [np.zeros(B, np.int32) for _ in range(5)]
+    for r in range(B):
+        n = int(lens[r])
+        pages, take, sink, tail, fine = geometry(n, topk, num, den, sink_cap, window)
+        outs[0][r], outs[1][r], outs[2][r], outs[3][r] = fine, take, max(fine, 1), max(pages * 8, 1)
+        same = True
+        for i in range(128):
+            page = 0 if i == 0 else tail // 64 + i - 1
+            valid = n > 0 and (i == 0 or page < (n + 63) // 64) and page < NP
+            mine = int(nt[r, page]) if valid else -1
+            first = int(nt[0, page]) if valid else -1
+            same &= mine == first
+        outs[4][r] = 0 if (n == int(lens[0]) and same) else r
+    return tuple(outs)
+
+
+def fine_table(rt, selected, takes, fp, capacity, scratch, tail_rows=None):
+    """kernels.py:379-404 (tail_rows None) and :488-514."""
+    B = rt.shape[0]
+    ft = np.zeros((B, fp), dtype=np.int32)
+    for b in range(B):
+        take = int(takes[b])
+        owner = b if tail_rows is None else int(tail_rows[b])
+        for j in range(fp):
+            if j < take:
+                ft[b, j] = rt[b, int(selected[b, j])]
+            else:
+                ft[b, j] = capacity + owner * scratch + min(max(j - take, 0), scratch - 1)
+    return ft
+
+
+def stage_tail(native, nt, lens, fine, capacity, scratch, sink_cap, window, tail_rows=None, rows=None):
+    """kernels.py:518-564 (tail_rows None: :407-441) on byte pools [pages, 8448]
+    (in place on fine)."""
+    B = nt.shape[0] if rows is None else rows
+    nat_k = native[:, :8192].reshape(-1, 64, 128)
+    nat_s = native[:, 8192:].copy().view(np.float32).reshape(-1, 64)
+    for row in range(B):
+        if tail_rows is not None and int(tail_rows[row]) != row:
+            continue
+        n = int(lens[row])
+        sink, tail = _bounds(n, window, sink_cap)
+        count = sink + n - tail
+        for p in range(scratch):
+            if not (p * 64 < count or p == 0):
+                continue
+            dst = capacity + row * scratch + p
+            kb = np.zeros((64, 128), dtype=np.uint8)
+            sb = np.zeros(64, dtype=np.float32)
+            for o in range(64):
+                i = p * 64 + o
+                if i < count:
+                    lg = i if i < sink else tail + i - sink
+                    page = int(nt[row, lg // 64])
+                    kb[o] = nat_k[page, lg % 64]
+                    sb[o] = nat_s[page, lg % 64]
+            fine[dst, :8192] = kb.reshape(-1)
+            fine[dst, 8192:] = sb.view(np.uint8)
+
+
+# ------------------------------------------------------------------ sort
+def sort_f32(perm, keys, n, groups, heads=1, head_stride=4096):
+    """sglang/srt/layers/attention/v1_native/fused_grouping.py:64-76: returns O."""
+    out = np.array(perm, copy=True)
+    for h in range(heads):
+        for g in range(groups):
+            base = h * head_stride + g * n
+            order = top_order(keys[base:base + n], n)
+            out[base:base + n] = perm[base + order]
+    return out
+
+
+def sort_i64(perm, keys, n):
+    """Same rule for signed int64 keys: descending, ties by ascending position."""
+    out = np.array(perm, copy=True)
+    for g in range(len(keys) // n):
+        k = keys[g * n:(g + 1) * n].astype(np.int64)
+        order = np.lexsort((np.arange(n), ~k))
+        out[g * n:(g + 1) * n] = perm[g * n + order]
+    return out
+
+
+# ---------------------------------------------------------- page manager
+def fingerprint(tmp, mapping):
+    """kernels.py:57-69: int64 [pages, 2] of byte and member weighted sums."""
+    pages, nbytes = tmp.shape
+    i = np.arange(nbytes, dtype=np.int64)
+    m_i = np.arange(64, dtype=np.int64)
+    out = np.zeros((pages, 2), dtype=np.int64)
+    for p in range(pages):
+        x = tmp[p].astype(np.int64)
+        m = mapping[p].astype(np.int64)
+        out[p, 0] = int((x * (i + 1)).sum()) + int(m.sum()) * 104729
+        out[p, 1] = int((x * ((i + 7) * 1000003)).sum()) + int((m * (m_i + 1) * 65537).sum())
+    return out
+
+
+def match_pages(tmp, mapping, hashes_tmp, fine, members, hashes, refs, capacity):
+    """kernels.py:72-113: lowest live page with equal fingerprints and equal
+    bytes + members, else -1."""
+    out = np.full(tmp.shape[0], -1, dtype=np.int32)
+    live = np.nonzero(refs[:capacity] > 0)[0]
+    for p in range(tmp.shape[0]):
+        for j in live:
+            if hashes[j, 0] == hashes_tmp[p, 0] and hashes[j, 1] == hashes_tmp[p, 1]:
+                if np.array_equal(fine[j], tmp[p]) and np.array_equal(members[j], mapping[p]):
+                    out[p] = j
+                    break
+    return out
+
+
+def allocate(lease, match, free, count, refs, tables):
+    """kernels.py:116-131 (in place on free-stack count / refs / tables).
+    Returns (new_count, fresh) or raises on exhaustion (the reference asserts)."""
+    fresh = match < 0
+    rank = np.cumsum(fresh) - 1
+    needed = int(fresh.sum())
+    if count < needed:
+        raise RuntimeError("V1 DeepSeek page arena exhausted")
+    pages = len(match)
+    dst = np.where(fresh, free[np.clip(count - 1 - rank, 0, None)], match)
+    np.add.at(refs, dst, 1)
+    tables[lease * pages:(lease + 1) * pages] = dst
+    return count - needed, fresh
+
+
+def publish(lease, tmp, centers_tmp, mapping, hash_tmp, tables, fresh, fine, centers, members, hashes):
+    """kernels.py:134-167 (in place).  Centers: 8 per page, 128 FP8 bytes plus
+    one fp32 scale each, to center index lease*pages*8 + p*8 + g."""
+    pages = len(fresh)
+    for p in range(pages):
+        if fresh[p]:
+            dst = int(tables[lease * pages + p])
+            fine[dst] = tmp[p]
+            members[dst] = mapping[p]
+            hashes[dst] = hash_tmp[p]
+        for g in range(8):
+            sc = p * 8 + g
+            dc = lease * pages * 8 + sc
+            centers[dc // 64, (dc % 64) * 128:(dc % 64) * 128 + 128] = \
+                centers_tmp[sc // 64, (sc % 64) * 128:(sc % 64) * 128 + 128]
+            centers[dc // 64, 8192 + 4 * (dc % 64):8192 + 4 * (dc % 64) + 4] = \
+                centers_tmp[sc // 64, 8192 + 4 * (sc % 64):8192 + 4 * (sc % 64) + 4]
+
+
+def release(table, refs, free, count):
+    """kernels.py:170-179, decrements in table order; returns the new count."""
+    dead = []
+    for page in table:
+        old = int(refs[page])
+        refs[page] = old - 1
+        if old == 1:
+            dead.append(int(page))
+    free[count:count + len(dead)] = dead
+    return count + len(dead)
+
+
+# ---------------------------------------------------------------- gather
+def gather_slots(k_pool, v_pool, req, ids, head):
+    """sglang/srt/layers/attention/v1_native/kernels.py:62-77 -> (kg, vg) [rows, top, 1, 128]."""
+    valid = ids >= 0
+    slots = req[np.where(valid, ids, 0)]
+    kg = np.where(valid[..., None], k_pool[slots, head], 0).astype(k_pool.dtype)
+    vg = np.where(valid[..., None], v_pool[slots, head], 0).astype(v_pool.dtype)
+    return kg[:, :, None, :], vg[:, :, None, :]
+
+
+def physical_rows(ids, table=None, page_bits=0):
+    """ids -> physical rows (-1 stays -1); table None / shared 1-D / per-row."""
+    ids = np.asarray(ids, dtype=np.int64)
+    if table is None:
+        return ids
+    valid = ids >= 0
+    e = np.where(valid, ids >> page_bits, 0)
+    t = table[e] if table.ndim == 1 else np.take_along_axis(table, e, axis=1)
+    phys = (t.astype(np.int64) << page_bits) | (ids & ((1 << page_bits) - 1))
+    return np.where(valid, phys, -1)
+
+
+def gather_rows(pool, ids, table=None, page_bits=0):
+    phys = physical_rows(ids, table, page_bits)
+    out = pool[np.where(phys >= 0, phys, 0)]
+    out[phys < 0] = 0
+    return out
+
+
+# ---------------------------------------------------------------- score
+def paged_logits(q8, w, native, block_table, lens, max_len, relu=True, clean=True, magnitude=False):
+    """Dequantised reference of the FP8 paged index logits (fp64 accumulation):
+    logit[r,j] = sum_h w[r,h] * relu(q[r,h] . k[j]) * s_k[j] for j < lens[r]
+    (sglang/srt/layers/attention/v1_deepseek/kernels.py:310-313; weighted
+    head sum, then the key scale).  Columns >= lens[r] are -inf (clean).
+    magnitude=True returns sum_h |w| sum_d |q k| s_k instead: the scale of the
+    terms, which bounds the rounding of any fp32 accumulation order."""
+    rows, H, D = q8.shape
+    qf = e4m3_decode(q8).astype(np.float64)
+    kk = native[:, :8192].reshape(-1, 64, 128)
+    ks = native[:, 8192:].copy().view(np.float32).reshape(-1, 64)
+    out = np.full((rows, max_len), -np.inf if clean else 0.0, dtype=np.float64)
+    for r in range(rows):
+        n = min(int(lens[r]), max_len)
+        if n <= 0:
+            continue
+        tab = block_table[r] if block_table.ndim == 2 else block_table
+        j = np.arange(n)
+        pages = tab[j // 64]
+        k = e4m3_decode(kk[pages, j % 64]).astype(np.float64)
+        s = ks[pages, j % 64].astype(np.float64)
+        if magnitude:
+            out[r, :n] = (np.abs(w[r].astype(np.float64))[:, None] * (np.abs(qf[r]) @ np.abs(k).T)).sum(axis=0) * s
+            continue
+        dots = qf[r] @ k.T  # [H, n]
+        if relu:
+            dots = np.maximum(dots, 0.0)
+        out[r, :n] = (w[r].astype(np.float64)[:, None] * dots).sum(axis=0) * s
+    return out

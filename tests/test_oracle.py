@@ -1,0 +1,408 @@
+"""Pins the CPU oracle against the reference's own known answers, closed forms
+and brute force (CPU only)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import v1 as O
+from conftest import pkg
+import refexample as RX
+
+W = pkg("workloads")
+
+
+def test_fp8_decode_matches_torch_every_code():
+    codes = np.arange(256, dtype=np.uint8)
+    ours = O.e4m3_decode(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(ours[ok], ref[ok])
+    assert np.array_equal(np.signbit(ours[ok]), np.signbit(ref[ok]))
+
+
+def test_fp8_encode_matches_torch_cast():
+    g = np.random.default_rng(0)
+    x = np.concatenate([g.standard_normal(20000).astype(np.float32) * s for s in (1e-3, 0.1, 1, 30, 200)])
+    x = np.clip(x, -448, 448)
+    # exact ties between neighbouring codes (round-half-even) and subnormals
+    vals = W.decode_table()[:127].astype(np.float64)
+    mids = ((vals[1:] + vals[:-1]) / 2).astype(np.float32)
+    x = np.concatenate([x, mids, -mids, np.float32([0.0, -0.0, 2 ** -10, 3 * 2 ** -10, 448.0])])
+    ours = W.e4m3_encode(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ours, ref)
+
+
+def test_pow2_scale_is_exact_ceiling():
+    for m in [1e-6, 1e-4, 0.5, 448.0, 448.0001, 896.0, 3.7, 1000.0]:
+        s = float(W.pow2_scale(np.float32(m)))
+        v = float(np.float32(max(np.float32(m), np.float32(1e-4))) / np.float32(448))
+        assert s >= v and s / 2 < v and s == 2.0 ** round(np.log2(s))
+
+
+# ------------------------------------------------------------------ topk
+def _brute(row, L, T):
+    if L <= T:
+        return list(range(L)) + [-1] * (T - L)
+    key = [(0.0 if v == 0 else v) for v in row[:L]]  # -0.0 == +0.0
+    order = sorted(range(L), key=lambda i: (-key[i], i))[:T]
+    return sorted(order)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_topk_select_brute_force_with_ties(seed):
+    g = np.random.default_rng(seed)
+    L = int(g.integers(1, 300))
+    T = int(g.integers(1, 64))
+    row = g.choice(np.float32([0.0, -0.0, 1.0, -1.0, 2.5, -np.inf, np.inf, 7.0]), size=L)
+    row = np.where(g.random(L) < 0.3, g.standard_normal(L).astype(np.float32), row).astype(np.float32)
+    assert list(O.topk_select(row, L, T)) == _brute(row, L, T)
+
+
+def test_topk_select_short_row_takes_all_even_neg_inf():
+    row = np.float32([-np.inf, 3, -np.inf])
+    assert list(O.topk_select(row, 3, 5)) == [0, 1, 2, -1, -1]
+
+
+def test_score_key_orders_like_floats():
+    v = np.float32([-np.inf, -3.5, -1e-30, -0.0, 0.0, 1e-30, 2.0, np.inf])
+    k = O.score_key(v)
+    assert k[3] == k[4]
+    assert all(int(k[i]) < int(k[i + 1]) for i in (0, 1, 2, 4, 5, 6))
+
+
+# ------------------------------------------------------------------ sort
+def test_sort_kat(kats):
+    kat = kats["sort_stable_signed_zero"]
+    vals = np.float32([float(v) for v in kat["values"]])
+    assert np.signbit(vals[4])
+    out = O.sort_f32(np.int32(kat["ids"]), vals, 16, 1)
+    assert out.tolist() == kat["expected"]
+
+
+def test_sort_split_chain_kat(kats):
+    kat = kats["sort_split_chain"]
+    # dots / anchors of test_fused_grouping_small.py:101-115 on unit[:,0] = [1,-1]*8
+    u = np.float32(kat["unit0"])
+    perm = np.int32(kat["perm"])
+    s0 = u[perm - 100] * u[perm[0] - 100]
+    a0 = int(perm[int(np.argmin(s0))])
+    s1 = u[perm - 100] * u[a0 - 100]
+    a1 = int(perm[int(np.argmin(s1))])
+    s2 = u[perm - 100] * u[a1 - 100] - s1
+    assert [a0, a1] == kat["anchor"]
+    assert O.sort_f32(perm, s2.astype(np.float32), 16, 1).tolist() == kat["expected"]
+
+
+@pytest.mark.parametrize("n", [16, 64, 1024])
+def test_sort_special_values_vs_sorted(kats, n):
+    kat = kats["sort_special_pattern"]
+    vals = np.float32([float(v) for v in kat["pattern"]] * kat["repeat"])
+    perm = np.random.default_rng(n).permutation(4096).astype(np.int32)
+    out = O.sort_f32(perm, vals, n, 4096 // n)
+    for g in range(4096 // n):
+        seg = vals[g * n:(g + 1) * n]
+        exp = [perm[g * n + i] for i in sorted(range(n), key=lambda i: (-(0.0 if seg[i] == 0 else seg[i]), i))]
+        assert out[g * n:(g + 1) * n].tolist() == exp
+
+
+def test_sort_i64_matches_sorted():
+    g = np.random.default_rng(3)
+    keys = g.integers(-5, 5, size=256).astype(np.int64)
+    keys[:3] = [np.iinfo(np.int64).min, np.iinfo(np.int64).max, 0]
+    perm = np.arange(256, dtype=np.int32) + 1000
+    out = O.sort_i64(perm, keys, 64)
+    for s in range(4):
+        k = keys[s * 64:(s + 1) * 64].tolist()
+        exp = [1000 + s * 64 + i for i in sorted(range(64), key=lambda i: (-k[i], i))]
+        assert out[s * 64:(s + 1) * 64].tolist() == exp
+
+
+# ---------------------------------------------------------- page manager
+def test_fingerprint_hand_kat(kats):
+    kat = kats["fingerprint_hand"]
+    tmp = np.zeros((1, 8448), np.uint8)
+    tmp[0, :2] = kat["bytes_head"]
+    m = np.zeros((1, 64), np.int32)
+    m[0, :2] = kat["members_head"]
+    assert O.fingerprint(tmp, m)[0].tolist() == kat["hash"]
+
+
+def test_fingerprint_word_identity(kats):
+    kat = kats["fingerprint_words"]
+    b = kat["word_bytes"]
+    i = 0
+    assert sum(b) * (4 * i + 1) + b[1] + 2 * b[2] + 3 * b[3] == kat["weighted"]
+    tmp = np.zeros((1, 8448), np.uint8)
+    tmp[0, :4] = b
+    assert O.fingerprint(tmp, np.zeros((1, 64), np.int32))[0, 0] == kat["weighted"]
+
+
+def lifecycle_state(cap=16):
+    tmp = np.repeat(np.arange(16, dtype=np.uint8)[:, None], 8448, axis=1)
+    mapping = np.arange(1024, dtype=np.int32).reshape(16, 64)
+    centers = np.zeros((2, 8448), np.uint8)
+    centers[:, :8192] = 7
+    centers[:, 8192:] = np.full((2, 64), 1.25, np.float32).view(np.uint8)
+    return dict(tmp=tmp, mapping=mapping, centers=centers, fine=np.zeros_like(tmp),
+                members=np.full_like(mapping, -1), live_hash=np.zeros((16, 2), np.int64),
+                refs=np.zeros(cap, np.int32), free=np.arange(cap, dtype=np.int32), count=cap,
+                tables=np.full(32, -1, np.int32), center_pool=np.zeros((4, 8448), np.uint8))
+
+
+def test_page_lifecycle_kat(kats):
+    kat = kats["page_lifecycle"]
+    s = lifecycle_state(kat["capacity"])
+    h = O.fingerprint(s["tmp"], s["mapping"])
+    look = lambda: O.match_pages(s["tmp"], s["mapping"], h, s["fine"], s["members"], s["live_hash"], s["refs"], 16)
+    assert (look() == -1).all()
+    count, fresh = O.allocate(0, look(), s["free"], s["count"], s["refs"], s["tables"])
+    O.publish(0, s["tmp"], s["centers"], s["mapping"], h, s["tables"], fresh, s["fine"], s["center_pool"],
+              s["members"], s["live_hash"])
+    s["count"] = count
+    t0 = s["tables"][:16].copy()
+    assert t0.tolist() == kat["first_table"] and count == kat["count_after_first"] and fresh.all()
+    assert (s["fine"][t0] == s["tmp"]).all() and (s["members"][t0] == s["mapping"]).all()
+    assert (s["center_pool"][:2] == s["centers"]).all() and (s["refs"] == kat["refs_after_first"]).all()
+    s["tmp"][0, 0] = 99
+    h2 = O.fingerprint(s["tmp"], s["mapping"])
+    assert O.match_pages(s["tmp"], s["mapping"], h2, s["fine"], s["members"], s["live_hash"], s["refs"], 16)[0] == -1
+    s["tmp"][0, 0] = 0
+    s["mapping"][0, 0] = 9999
+    h3 = O.fingerprint(s["tmp"], s["mapping"])
+    assert O.match_pages(s["tmp"], s["mapping"], h3, s["fine"], s["members"], s["live_hash"], s["refs"], 16)[0] == -1
+    s["mapping"][0, 0] = 0
+    m = look()
+    assert m.tolist() == t0.tolist()
+    count, fresh = O.allocate(1, m, s["free"], s["count"], s["refs"], s["tables"])
+    O.publish(1, s["tmp"], s["centers"], s["mapping"], h, s["tables"], fresh, s["fine"], s["center_pool"],
+              s["members"], s["live_hash"])
+    assert s["tables"][16:].tolist() == t0.tolist() and not fresh.any() and count == 0
+    assert (s["refs"] == kat["refs_after_second"]).all() and (s["center_pool"][2:] == s["centers"]).all()
+    count = O.release(t0, s["refs"], s["free"], count)
+    assert count == 0 and (s["refs"] == kat["refs_after_release_a"]).all()
+    count = O.release(s["tables"][16:], s["refs"], s["free"], count)
+    assert count == kat["count_after_release_b"] and (s["refs"] == 0).all()
+    assert sorted(s["free"].tolist()) == list(range(16))
+
+
+@pytest.mark.parametrize("mode", ["miss", "hit", "collision"])
+def test_match_modes(mode):
+    g = np.random.default_rng(77)
+    cap = 32
+    tmp = g.integers(0, 256, (16, 8448), dtype=np.uint8)
+    mp = g.integers(-1, 262144, (16, 64)).astype(np.int32)
+    h = O.fingerprint(tmp, mp)
+    fine = g.integers(0, 256, (cap, 8448), dtype=np.uint8)
+    members = np.zeros((cap, 64), np.int32)
+    hashes = np.zeros((cap, 2), np.int64)
+    refs = np.zeros(cap, np.int32)
+    if mode != "miss":
+        fine[1:17], members[1:17], hashes[1:17], refs[1:17] = tmp, mp, h, 1
+    if mode == "collision":
+        fine[0], members[0], hashes[0], refs[0] = tmp[0], mp[0], h[0], 1
+        fine[0, 0] ^= 1
+    m = O.match_pages(tmp, mp, h, fine, members, hashes, refs, cap)
+    exp = [-1] * 16 if mode == "miss" else list(range(1, 17))
+    assert m.tolist() == exp
+
+
+def test_release_duplicates_in_table_order():
+    refs = np.int32([2, 1, 1, 0])
+    free = np.full(8, -9, np.int32)
+    count = O.release(np.int32([0, 1, 0, 2]), refs, free, 3)
+    assert count == 6 and free[3:6].tolist() == [1, 0, 2] and refs.tolist() == [0, 0, 0, 0]
+
+
+def shared_tail_inputs(kat):
+    rows, np_, cap, scratch = kat["rows"], kat["np"], kat["cap"], kat["scratch"]
+    native = np.zeros((np_, 8448), np.uint8)
+    for page in range(np_):
+        native[page, :8192] = W.e4m3_encode(np.float32([page + 1]))[0]
+        native[page, 8192:] = (np.arange(64, dtype=np.float32) + 1).view(np.uint8)
+    nt = np.repeat(np.arange(np_ - 1, -1, -1, dtype=np.int32)[None], rows, axis=0)
+    return native, nt
+
+
+def test_shared_tail_kat(kats):
+    kat = kats["shared_tail"]
+    native, nt = shared_tail_inputs(kat)
+    rows, cap, scratch = kat["rows"], kat["cap"], kat["scratch"]
+    lens, owners = np.int32(kat["lens"]), np.int32(kat["owners"])
+    out = np.full((cap + rows * scratch, 8448), 255, np.uint8)
+    O.stage_tail(native, nt, lens, out, cap, scratch, 64, 64, tail_rows=owners)
+    for row, n in ((0, 1100), (2, 1101)):
+        ids = list(range(64)) + list(range(1024, n))
+        exp = np.zeros((scratch, 8448), np.uint8)
+        for j, lg in enumerate(ids):
+            page = nt[row, lg // 64]
+            exp[j // 64, (j % 64) * 128:(j % 64) * 128 + 128] = native[page, (lg % 64) * 128:(lg % 64) * 128 + 128]
+            exp[j // 64, 8192 + 4 * (j % 64):8192 + 4 * (j % 64) + 4] = native[page, 8192 + 4 * (lg % 64):8192 + 4 * (lg % 64) + 4]
+        assert (out[cap + row * scratch:cap + (row + 1) * scratch] == exp).all()
+    for row in (1, 3):
+        assert (out[cap + row * scratch:cap + (row + 1) * scratch] == 255).all()
+    assert (out[0] == 255).all()
+    ft = O.fine_table(np.zeros((rows, kat["np"]), np.int32), np.zeros((rows, 1), np.int32), np.zeros(rows, np.int32),
+                      scratch, cap, scratch, tail_rows=owners)
+    assert ft.tolist() == kat["fine_table"]
+
+
+def test_query_metadata_tail_sharing():
+    nt = np.tile(np.arange(64, dtype=np.int32), (4, 1))
+    nt[3, 20] = 999  # row 3 differs in a tail page
+    lens = np.int32([1100, 1100, 1200, 1100])
+    fl, tk, dg, cl, tr = O.query_metadata(lens, nt, 2048, 1, 2, 64, 64)
+    assert tr.tolist() == [0, 0, 2, 0]  # row 3's differing page 20 is not a tail page of n=1100
+    nt[3, 16] = 999  # page 16 = tail // 64 (tail = min(1024, 1100 - 64) = 1024) is
+    assert O.query_metadata(lens, nt, 2048, 1, 2, 64, 64)[4].tolist() == [0, 0, 2, 3]
+    pages, take, sink, tail, fine = O.geometry(1100, 2048, 1, 2, 64, 64)
+    assert (pages, take, sink, tail) == (16, 16, 64, 1024) and fine == 16 * 64 + 64 + 1100 - 1024
+    assert fl[0] == fine and tk[0] == take and cl[0] == 128
+
+
+# ------------------------------------------------------------------ gather
+def test_gather_kat(kats):
+    kat = kats["gather_small"]
+    x = np.arange(8 * 2 * 128, dtype=np.float32).reshape(8, 2, 128)
+    k, v = x, -x - 16
+    req = np.int32(kat["req"])
+    ids = np.int32(kat["ids"])
+    for head in (0, 1):
+        kg, vg = O.gather_slots(k, v, req, ids, head)
+        for r in range(2):
+            for i in range(3):
+                p = kat["physical"][r][i]
+                assert (kg[r, i, 0] == (k[p, head] if p >= 0 else 0)).all()
+                assert (vg[r, i, 0] == (v[p, head] if p >= 0 else 0)).all()
+
+
+def test_gather_rows_paged_table():
+    pool = np.arange(40 * 16, dtype=np.int64).astype(np.uint8).reshape(40, 16)
+    table = np.int32([[3, 1], [0, 2]])
+    ids = np.int32([[0, 5, -1], [7, 4, 2]])
+    out = O.gather_rows(pool, ids, table, page_bits=2)
+    phys = [[12, 5, -1], [11, 8, 2]]
+    for r in range(2):
+        for i in range(3):
+            p = phys[r][i]
+            assert (out[r, i] == (pool[p] if p >= 0 else 0)).all()
+
+
+# ------------------------------------------------------------------- route
+def test_route_reference_example(kats):
+    kat = kats["route_example"]
+    d = RX.route_inputs()
+    B = RX.B
+    sel = np.full((B, RX.TAKE), -1, np.int32)
+    ft = np.full((B, RX.TAKE + 68), -1, np.int32)
+    O.route(d["scores"].numpy(), d["lens"].numpy(), d["takes"].numpy(), sel, RX.P, d["rt"].numpy(), ft,
+            d["tail_rows"].numpy(), RX.CAP, True)
+    ref_pages = d["scores"][:, :512].view(B, 64, 8).amax(-1).topk(RX.TAKE, dim=-1).indices.numpy()
+    assert (sel == ref_pages).all()
+    assert sel[0, :8].tolist() == kat["first_selected"]
+    assert (ft[:, :RX.TAKE] == np.take_along_axis(d["rt"].numpy(), ref_pages, 1)).all()
+    assert (ft[:, RX.TAKE:] == RX.CAP + np.arange(68)).all()
+
+
+def test_route_ties_to_lower_page_and_trivial_branch():
+    B, P = 3, 64
+    scores = np.full((B, 8 * P), -np.inf, np.float32)
+    scores[:, :8 * 32] = 1.0  # all 32 active pages tie
+    scores[1, 8 * 5 + 3] = 2.0
+    lens = np.int32([2049, 2049, 1025])  # active 32, 32, 16
+    takes = np.int32([4, 4, 20])
+    sel = np.zeros((B, 6), np.int32)
+    rt = np.arange(B * P, dtype=np.int32).reshape(B, P)
+    ft = np.zeros((B, 10), np.int32)
+    O.route(scores, lens, takes, sel, P, rt, ft, np.int32([0, 1, 2]), 500, True)
+    assert sel[0].tolist() == [0, 1, 2, 3, 4, 5]
+    assert sel[1].tolist() == [5, 0, 1, 2, 3, 4]
+    assert sel[2].tolist() == [0, 1, 2, 3, 4, 5]  # take >= active: identity
+    assert ft[1, :4].tolist() == [rt[1, 5], rt[1, 0], rt[1, 1], rt[1, 2]]
+    assert ft[1, 4:].tolist() == [500 + 68 + j for j in range(6)]
+    # the identity branch writes ft[i] only for i < take_stride (v1_query.cuh:17-19)
+    assert ft[2, :6].tolist() == rt[2, :6].tolist() and ft[2, 6:].tolist() == [0, 0, 0, 0]
+
+
+# -------------------------------------------------------------- fused topk
+@pytest.fixture(scope="module")
+def example_after_route():
+    d = RX.route_inputs()
+    B = RX.B
+    sel = np.full((B, RX.TAKE), -1, np.int32)
+    ft = np.full((B, RX.TAKE + 68), -1, np.int32)
+    O.route(d["scores"].numpy(), d["lens"].numpy(), d["takes"].numpy(), sel, RX.P, d["rt"].numpy(), ft,
+            d["tail_rows"].numpy(), RX.CAP, True)
+    f = RX.fine_inputs(d, torch.from_numpy(ft))
+    return d, sel, ft, f
+
+
+@pytest.mark.parametrize("direct", [False, True])
+def test_fused_topk_reference_example(example_after_route, direct):
+    d, sel, ft, f = example_after_route
+    work = f["fine_scores"].numpy().copy()
+    out = O.fused_topk(work, f["fine_lens"].numpy(), d["members"].numpy(), d["rt"].numpy(), d["nt"].numpy(), sel,
+                       d["lens"].numpy(), d["takes"].numpy(), RX.TOP, RX.WINDOW, True, 0, True, True, ft, direct)
+    ref = f["reference_scores"]
+    exp_raw = ref.topk(RX.TOP, dim=-1).indices
+    cand = f["candidate_ids"].numpy()
+    raw = out["raw"]
+    assert (np.sort(raw, 1) == exp_raw.sort(1).values.numpy()).all()
+    assert (out["logical"] == np.take_along_axis(cand, raw.astype(np.int64), 1)).all()
+    nt = d["nt"].numpy()
+    lg = out["logical"]
+    assert (out["physical"] == np.take_along_axis(nt, lg // 64, 1) * 64 + lg % 64).all()
+    s = np.sort(lg, 1)
+    assert (s[:, 1:] != s[:, :-1]).all()
+    assert np.array_equal(work, ref.numpy())
+
+
+def test_unfused_mask_and_map_equal_fused(example_after_route):
+    d, sel, ft, f = example_after_route
+    rows = 64
+    args = lambda a: a[:rows]
+    w1 = f["fine_scores"].numpy()[:rows].copy()
+    w2 = w1.copy()
+    fl = f["fine_lens"].numpy()[:rows]
+    out = O.fused_topk(w1, fl, d["members"].numpy(), args(d["rt"].numpy()), args(d["nt"].numpy()), args(sel),
+                       args(d["lens"].numpy()), args(d["takes"].numpy()), RX.TOP, RX.WINDOW, True, 0, True, False,
+                       args(ft), False)
+    O.mask_fine(w2, args(sel), args(d["rt"].numpy()), d["members"].numpy(), args(d["lens"].numpy()),
+                args(d["takes"].numpy()), w2.shape[1], 64, RX.WINDOW)
+    assert np.array_equal(w1, w2)
+    raw = np.stack([O.topk_select(w2[b], int(fl[b]), RX.TOP) for b in range(rows)]).astype(np.int32)
+    phys, lg = O.output_ids(raw, w2, d["members"].numpy(), args(d["rt"].numpy()), args(d["nt"].numpy()), args(sel),
+                            args(d["lens"].numpy()), args(d["takes"].numpy()), w2.shape[1], RX.TOP, 64, RX.WINDOW,
+                            True, False, args(ft))
+    assert np.array_equal(phys, out["physical"]) and np.array_equal(lg, out["logical"])
+
+
+def test_transform_closed_form():
+    g = np.random.default_rng(5)
+    scores = g.standard_normal((3, 300)).astype(np.float32)
+    lens = np.int32([300, 10, 200])
+    table = g.permutation(64).astype(np.int32)[None].repeat(3, 0)
+    out, raw = O.transform_topk(scores, lens, table, 16, 6)
+    for b in range(3):
+        r = raw[b]
+        ok = r >= 0
+        assert (out[b][ok] == table[b, r[ok] >> 6] * 64 + (r[ok] & 63)).all() and (out[b][~ok] == -1).all()
+    assert raw[1].tolist() == list(range(10)) + [-1] * 6
+
+
+# ------------------------------------------------------------------- score
+def test_score_formula_order_by_hand():
+    # one query, 2 heads, one key: q0.k = 2, q1.k = -3 -> w0*relu(2) + w1*relu(-3) = 0.5*2; times s_k = 0.25
+    q8 = np.zeros((1, 2, 128), np.uint8)
+    q8[0, 0, 0] = W.e4m3_encode(np.float32([1.0]))[0]
+    q8[0, 1, 0] = W.e4m3_encode(np.float32([-1.5]))[0]
+    native = np.zeros((1, 8448), np.uint8)
+    native[0, 0] = W.e4m3_encode(np.float32([2.0]))[0]
+    native[0, 8192:8196] = np.float32([0.25]).view(np.uint8)
+    w = np.float32([[0.5, 7.0]])
+    out = O.paged_logits(q8, w, native, np.int32([[0]]), np.int32([1]), 4)
+    assert out[0, 0] == pytest.approx(0.5 * 2 * 0.25)
+    assert np.isneginf(out[0, 1:]).all()
+    signed = O.paged_logits(q8, w, native, np.int32([[0]]), np.int32([1]), 1, relu=False)
+    assert signed[0, 0] == pytest.approx((0.5 * 2 - 7.0 * 3) * 0.25)
