@@ -22,6 +22,8 @@ FLAGS = [
     "-Wno-unused-variable", "-Wno-unused-but-set-variable",
     # packed FP32 VALU ops are kept out of every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the epilogues read every accumulator with VALU ops
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -46,14 +46,16 @@ __device__ __forceinline__ float key_score(uint32_t k) {
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave, on DPP lane moves:
+// row_shr 1/2/4/8 scans each 16-lane row, then row_bcast15 / row_bcast31 carry
+// the row totals into rows 1,3 and 2,3.
 __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
-    const int lane = __lane_id();
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        uint32_t n = __shfl_up(v, off, kWave);
-        if (lane >= off) v += n;
-    }
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);  // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);  // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);  // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);  // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31
     return v;
 }
 

@@ -88,20 +88,42 @@ __device__ __forceinline__ void load_w(const ScoreParams& p, int64_t row, float 
         }
 }
 
-// Weighted head sum for the 16 keys of one B fragment; returns the logit
-// (before the key scale) of key l%16 in every lane.
-template <int HB>
-__device__ __forceinline__ float head_sum(const v8i (&a)[HB], v8i b, const float (&w)[HB][4], bool relu) {
-    float s = 0.f;
+// ReLU as an integer max on the bit pattern: negative floats (and -0.0) have
+// the sign bit set and compare below 0 as int32; no NaN canonicalisation.
+__device__ __forceinline__ float relu(float x) {
+    return __builtin_bit_cast(float, max(__builtin_bit_cast(int, x), 0));
+}
+
+// Per-lane partial logits of one query for the 4 key blocks of a page:
+// s[kb] = sum over this lane's 4 heads per row block of w * relu(q . k).
+template <int HB, bool RELU>
+__device__ __forceinline__ void page_partials(const v8i (&a)[HB], const v8i (&b)[4], const float (&w)[HB][4],
+                                              float (&s)[4]) {
 #pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
-        const v4f d = mfma_fp8(a[hb], b);
+    for (int kb = 0; kb < 4; ++kb) {
+        float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s = fmaf(w[hb][i], relu ? fmaxf(d[i], 0.f) : d[i], s);
+        for (int hb = 0; hb < HB; ++hb) {
+            const v4f d = mfma_fp8(a[hb], b[kb]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = fmaf(w[hb][i], RELU ? relu(d[i]) : d[i], acc);
+        }
+        s[kb] = acc;
     }
-    s += __shfl_xor(s, 16, kWave);
-    s += __shfl_xor(s, 32, kWave);
-    return s;
+}
+
+// Reduce-scatter over the four 16-lane groups: lane g*16+c returns
+// sum over groups of s[g] at column c, i.e. the full head sum of key g*16+c.
+// permlane32_swap(x, y) exchanges the upper half of x with the lower half of
+// y; adding both results folds the two halves.  permlane16_swap does the same
+// between 16-lane rows 0/1 and 2/3.
+__device__ __forceinline__ float reduce_scatter4(const float (&s)[4]) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(s[0]), __float_as_uint(s[2]), false, false);
+    const float ta = __uint_as_float(p[0]) + __uint_as_float(p[1]);  // rows 0,1: sum s0; rows 2,3: sum s2
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(s[1]), __float_as_uint(s[3]), false, false);
+    const float tb = __uint_as_float(q[0]) + __uint_as_float(q[1]);  // rows 0,1: sum s1; rows 2,3: sum s3
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(ta), __float_as_uint(tb), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ int32_t page_of(const ScoreParams& p, int64_t row, int32_t blk) {
@@ -119,7 +141,7 @@ __device__ __forceinline__ void store_logit(const ScoreParams& p, int64_t row, i
 }
 
 // ------------------------------------------------------------ shared table
-template <int HB>
+template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[2][kPageLds];
     const int t = threadIdx.x, l = __lane_id(), wv = t / kWave;
@@ -186,19 +208,19 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     for (int32_t pg = 0; pg < npages; ++pg) {
         const int buf = pg & 1;
         if (pg + 1 < npages) fetch(pg + 1);
-        float out[kQueriesPerWave];
-#pragma unroll
-        for (int q = 0; q < kQueriesPerWave; ++q) out[q] = 0.f;
+        v8i b[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             const u32x4* src = reinterpret_cast<const u32x4*>(&lds[buf][(kb * 16 + (l & 15)) * kKeyPitch + 32 * (l >> 4)]);
             const u32x4 x = src[0], y = src[1];
-            const v8i b = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+            b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+        }
+        float out[kQueriesPerWave];
 #pragma unroll
-            for (int q = 0; q < kQueriesPerWave; ++q) {
-                const float s = head_sum<HB>(a[q], b, w[q], p.relu != 0);
-                if ((l >> 4) == kb) out[q] = s;
-            }
+        for (int q = 0; q < kQueriesPerWave; ++q) {
+            float part[4];
+            page_partials<HB, RELU>(a[q], b, w[q], part);
+            out[q] = reduce_scatter4(part);
         }
         const float scale = reinterpret_cast<const float*>(&lds[buf][64 * kKeyPitch])[l];
         const int32_t j = (chunk0 + pg) * 64 + l;
@@ -218,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
 }
 
 // ---------------------------------------------------------------- per row
-template <int HB>
+template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
     const int l = __lane_id(), wv = threadIdx.x / kWave;
     const int64_t row = blockIdx.y;
@@ -241,17 +263,50 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
         float out = 0.f, scale = 0.f;
         if (page >= 0) {
             const uint8_t* base = p.kv + (int64_t)page * V1_PAGE_BYTES;
+            v8i b[4];
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
                 const u32x4* src = reinterpret_cast<const u32x4*>(base + (kb * 16 + (l & 15)) * 128 + 32 * (l >> 4));
                 const u32x4 x = src[0], y = src[1];
-                const v8i b = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
-                const float s = head_sum<HB>(a, b, w, p.relu != 0);
-                if ((l >> 4) == kb) out = s;
+                b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
             }
+            float part[4];
+            page_partials<HB, RELU>(a, b, w, part);
+            out = reduce_scatter4(part);
             scale = reinterpret_cast<const float*>(base + 8192)[l];
         }
         store_logit(p, row, j, ctx, out * scale);
+    }
+}
+
+struct Shared {
+    template <int HB, bool RELU>
+    static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
+        hipLaunchKernelGGL((score_shared<HB, RELU>), g, dim3(kThreads), 0, st, p);
+    }
+};
+struct Rows {
+    template <int HB, bool RELU>
+    static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
+        hipLaunchKernelGGL((score_rows<HB, RELU>), g, dim3(kThreads), 0, st, p);
+    }
+};
+
+template <typename K, int HB>
+void launch_relu(bool relu, dim3 g, hipStream_t st, const ScoreParams& p) {
+    if (relu)
+        K::template launch<HB, true>(g, st, p);
+    else
+        K::template launch<HB, false>(g, st, p);
+}
+
+template <typename K>
+void launch_hb(int hb, bool relu, dim3 g, hipStream_t st, const ScoreParams& p) {
+    switch (hb) {
+        case 1: launch_relu<K, 1>(relu, g, st, p); break;
+        case 2: launch_relu<K, 2>(relu, g, st, p); break;
+        case 3: launch_relu<K, 3>(relu, g, st, p); break;
+        default: launch_relu<K, 4>(relu, g, st, p); break;
     }
 }
 
@@ -277,20 +332,10 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
     hipStream_t st = as_stream(stream);
     if (a->block_table_stride == 0) {
         const dim3 grid(chunks, (uint32_t)cdiv(a->rows, kQueriesPerGroup));
-        switch (hb) {
-            case 1: hipLaunchKernelGGL(score_shared<1>, grid, dim3(kThreads), 0, st, p); break;
-            case 2: hipLaunchKernelGGL(score_shared<2>, grid, dim3(kThreads), 0, st, p); break;
-            case 3: hipLaunchKernelGGL(score_shared<3>, grid, dim3(kThreads), 0, st, p); break;
-            default: hipLaunchKernelGGL(score_shared<4>, grid, dim3(kThreads), 0, st, p); break;
-        }
+        launch_hb<Shared>(hb, a->relu != 0, grid, st, p);
         return V1_LAUNCHED("score_shared");
     }
     const dim3 grid(chunks, (uint32_t)a->rows);
-    switch (hb) {
-        case 1: hipLaunchKernelGGL(score_rows<1>, grid, dim3(kThreads), 0, st, p); break;
-        case 2: hipLaunchKernelGGL(score_rows<2>, grid, dim3(kThreads), 0, st, p); break;
-        case 3: hipLaunchKernelGGL(score_rows<3>, grid, dim3(kThreads), 0, st, p); break;
-        default: hipLaunchKernelGGL(score_rows<4>, grid, dim3(kThreads), 0, st, p); break;
-    }
+    launch_hb<Rows>(hb, a->relu != 0, grid, st, p);
     return V1_LAUNCHED("score_rows");
 }

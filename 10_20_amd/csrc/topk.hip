@@ -8,17 +8,23 @@
 // candidates take every candidate (sglang/kernels/jit/csrc/deepseek_v4/
 // topk_v2.cuh:136-143).
 //
-// Design (one 1024-thread work-group per row, wave64):
-//  * the row is loaded once, as order-preserving uint32 keys, into registers
-//    (striped float4 loads: element j = c*4096 + 4*t + e);
-//  * three LDS radix-histogram passes (12/10/10 bits) locate the T-th largest
-//    key `tau` and how many tau-valued elements must be taken (`r`);
-//  * one block-wide packed (greater | equal << 16) prefix scan in index order
-//    gives every chosen element its output slot: gt_before + min(eq_before, r).
-//    The output is therefore ascending and deterministic without a sort.
-// Rows longer than 32768 columns are cut into 32768-column segments: one
-// work-group selects each segment's Top-T into a workspace (ascending index),
-// and a merge work-group selects the row's Top-T from the concatenation.
+// Design: one 1024-thread work-group selects over up to 32768 positions and
+// keeps little state per thread, so two work-groups share a CU and one row's
+// HBM stream overlaps another's selection.
+//  1. 4096 sampled keys give a pivot that about 1.5*T of the row's keys exceed.
+//  2. One streaming pass, wave-independent (no barriers), sends every key at or
+//     above the pivot to an LDS candidate buffer (wave-aggregated slot
+//     allocation) and keeps the row's key statistics.
+//  3. LDS radix passes over the candidates (the first digit starts where the
+//     largest and smallest candidate differ) give the T-th largest key tau and
+//     the number r of tau-valued keys to take.
+//  4. Position bitmaps of "> tau" and "== tau" plus a block prefix of their
+//     popcounts give each winner its output slot: (> tau before it) +
+//     min(== tau before it, r).  No sort is needed and the order is exact.
+// When the pivot misses (fewer than T or more than kCandMax keys at or above
+// it) the same steps run on the whole row, streamed again from cache.
+// Rows longer than 32768 columns are cut into 32768-column segments whose
+// Top-T land in a workspace; a merge work-group selects from their union.
 #include "common.h"
 
 namespace v1 {
@@ -26,62 +32,96 @@ namespace {
 
 constexpr int kBlock = 1024;
 constexpr int kWaves = kBlock / kWave;  // 16
-constexpr int kChunk = 4 * kBlock;      // elements per striped chunk
-constexpr int kSegment = 32768;         // columns per work-group
+constexpr int kSpan = 32768;            // positions one work-group selects over
+constexpr int kWords = kSpan / 32;      // position bitmap words, one per thread
+constexpr int kCandMax = 5120;
+constexpr int kCandPerThread = kCandMax / kBlock;  // 5
 constexpr uint32_t kNegInfKey = 0x007fffffu;
 constexpr uint32_t kInfBit = 0x80000000u;
 
 struct SelSmem {
-    uint32_t hist[4096];
-    uint32_t wtot[kWaves];
-    uint32_t ctot[8 * kWaves];
-    uint32_t cbase[8 * kWaves];
-    uint32_t bc[2];
+    uint32_t hist[4096];       // radix histograms; bitmap word prefixes
+    uint32_t cand_key[kCandMax];
+    uint16_t cand_pos[kCandMax];
+    uint32_t gt_bits[kWords];  // positions with key > tau
+    uint32_t eq_bits[kWords];  // positions with key == tau
     int32_t sel[V1_MAX_TOPK];  // chosen positions (| kInfBit when the score is -inf)
-    int32_t maskpage[512];     // V1 mask: page per selected rank, -1 when unmasked
+    uint32_t selkey[V1_MAX_TOPK];
+    uint32_t red[4 * kWaves];
+    uint32_t bc[4];
+    uint32_t ncand;
+    int32_t maskpage[kSpan / 64];  // V1 mask: page per selected rank, -1 when unmasked
 };
+
+__device__ __forceinline__ uint32_t readlane(uint32_t v, int lane) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
 
 __device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, SelSmem& sm) {
     const int w = threadIdx.x / kWave;
     const uint32_t x = wave_inclusive_sum(v);
-    if (__lane_id() == kWave - 1) sm.wtot[w] = x;
+    if (__lane_id() == kWave - 1) sm.red[w] = x;
     __syncthreads();
     uint32_t base = 0;
-    for (int k = 0; k < w; ++k) base += sm.wtot[k];
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) base += k < w ? sm.red[k] : 0u;
+    __syncthreads();
     return base + x;
 }
 
-// One radix pass: histogram the digit (key >> SHIFT) & (BINS-1) of every key
-// matching `prefix` under `pmask`, then locate the bin holding the
-// `remaining`-th largest such key.
-template <int ITEMS, int BINS, int SHIFT>
-__device__ __forceinline__ void radix_pass(const uint32_t (&key)[ITEMS], uint32_t& prefix,
-                                           uint32_t& pmask, uint32_t& remaining, SelSmem& sm) {
-    const int t = threadIdx.x;
-    for (int i = t; i < BINS; i += kBlock) sm.hist[i] = 0;
-    __syncthreads();
+// Block-wide max / min / count; every thread gets the result.
+__device__ __forceinline__ void block_stats(uint32_t& mx, uint32_t& mn, uint32_t& n, SelSmem& sm) {
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-        const uint32_t k = key[i];
-        if ((k & pmask) == prefix) atomicAdd(&sm.hist[(k >> SHIFT) & (BINS - 1)], 1u);
+    for (int off = 32; off > 0; off >>= 1) {
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, kWave));
+        mn = min(mn, (uint32_t)__shfl_xor((int)mn, off, kWave));
+        n += (uint32_t)__shfl_xor((int)n, off, kWave);
+    }
+    const int w = threadIdx.x / kWave;
+    if (__lane_id() == 0) {
+        sm.red[w] = mx;
+        sm.red[kWaves + w] = mn;
+        sm.red[2 * kWaves + w] = n;
     }
     __syncthreads();
-    constexpr int BPT = BINS / kBlock;
-    uint32_t h[BPT];
+    mx = 0u;
+    mn = 0xffffffffu;
+    n = 0u;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) {
+        mx = max(mx, sm.red[k]);
+        mn = min(mn, sm.red[kWaves + k]);
+        n += sm.red[2 * kWaves + k];
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void key_stats(uint32_t k, uint32_t& mx, uint32_t& mn, uint32_t& n) {
+    const bool real = k > kNegInfKey;
+    mx = real ? max(mx, k) : mx;
+    mn = real ? min(mn, k) : mn;
+    n += real ? 1u : 0u;
+}
+
+// Descending scan of hist[0..4096): the bin holding the `rank`-th largest
+// counted key, and the count above it.  Ends with a barrier.
+__device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& bin, uint32_t& above) {
+    const int t = threadIdx.x;
+    uint32_t h[4];
     uint32_t local = 0;
 #pragma unroll
-    for (int b = 0; b < BPT; ++b) {
-        h[b] = sm.hist[BINS - 1 - (BPT * t + b)];
+    for (int b = 0; b < 4; ++b) {  // thread t owns bins 4095-4t .. 4092-4t
+        h[b] = sm.hist[4095 - (4 * t + b)];
         local += h[b];
     }
     const uint32_t incl = block_incl_scan(local, sm);
     const uint32_t excl = incl - local;
-    if (excl < remaining && remaining <= incl) {
+    if (excl < rank && rank <= incl) {
         uint32_t acc = excl;
 #pragma unroll
-        for (int b = 0; b < BPT; ++b) {
-            if (acc + h[b] >= remaining) {
-                sm.bc[0] = BINS - 1 - (BPT * t + b);
+        for (int b = 0; b < 4; ++b) {
+            if (acc + h[b] >= rank) {
+                sm.bc[0] = 4095 - (4 * t + b);
                 sm.bc[1] = acc;
                 break;
             }
@@ -89,100 +129,317 @@ __device__ __forceinline__ void radix_pass(const uint32_t (&key)[ITEMS], uint32_
         }
     }
     __syncthreads();
-    remaining -= sm.bc[1];
-    prefix |= sm.bc[0] << SHIFT;
-    pmask |= (uint32_t)(BINS - 1) << SHIFT;
+    bin = sm.bc[0];
+    above = sm.bc[1];
+    __syncthreads();
 }
 
-// Selects the T largest keys (ties -> lower position) of a register tile and
-// writes their positions, ascending, to sm.sel[0..T) and their keys to
-// sm.hist[0..T) (the histogram is free once the radix passes are done).
-// Requires more than T keys above the padding key 0.  Position of item i of
-// thread t: (i/4)*kChunk + 4*t + i%4.  Ends with a barrier.
-template <int ITEMS>
-__device__ void select_top(const uint32_t (&key)[ITEMS], uint32_t T, SelSmem& sm) {
-    uint32_t prefix = 0, pmask = 0, remaining = T;
-    radix_pass<ITEMS, 4096, 20>(key, prefix, pmask, remaining, sm);
-    radix_pass<ITEMS, 1024, 10>(key, prefix, pmask, remaining, sm);
-    radix_pass<ITEMS, 1024, 0>(key, prefix, pmask, remaining, sm);
-    const uint32_t tau = prefix, r = remaining;
+__device__ __forceinline__ void clear_hist(SelSmem& sm) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm.hist[threadIdx.x + i * kBlock] = 0;
+}
 
-    constexpr int NC = ITEMS / 4;
-    const int t = threadIdx.x, w = t / kWave, lane = __lane_id();
-    uint32_t cnt[NC], incl[NC];
+// Digit window of a pass: bits [shift, shift+bits) under the fixed prefix.
+struct Radix {
+    uint32_t prefix, pmask, remaining;
+    int shift;  // bits still unresolved below the prefix
+    __device__ __forceinline__ void start(uint32_t mx, uint32_t mn, uint32_t T) {
+        const int hb = 31 - __builtin_clz(mx ^ mn);
+        pmask = hb == 31 ? 0u : ~((2u << hb) - 1u);
+        prefix = mx & pmask;
+        remaining = T;
+        shift = hb + 1;
+    }
+    __device__ __forceinline__ int bits() const { return shift < 12 ? shift : 12; }
+    __device__ __forceinline__ bool counts(uint32_t k, bool real_only) const {
+        return (k & pmask) == prefix && (!real_only || k > kNegInfKey);
+    }
+    __device__ __forceinline__ uint32_t digit(uint32_t k) const {
+        return (k >> (shift - bits())) & ((1u << bits()) - 1u);
+    }
+    // after the histogram of this pass is in sm.hist
+    __device__ __forceinline__ void finish(SelSmem& sm) {
+        uint32_t bin, above;
+        find_bin(remaining, sm, bin, above);
+        const int b = bits();
+        shift -= b;
+        remaining -= above;
+        prefix |= bin << shift;
+        pmask |= ((1u << b) - 1u) << shift;
+    }
+};
+
+// Position ranks of the winners: builds the "> tau" / "== tau" bitmaps from
+// `mark(emit)` and the block prefix of their packed popcounts; `place(emit)`
+// then visits each marked item again and writes it to its slot.
+struct Ranker {
+    __device__ __forceinline__ static void clear(SelSmem& sm) {
+        sm.gt_bits[threadIdx.x] = 0;
+        sm.eq_bits[threadIdx.x] = 0;
+    }
+    __device__ __forceinline__ static void mark(SelSmem& sm, uint32_t pos, bool gt, bool eq) {
+        if (gt) atomicOr(&sm.gt_bits[pos >> 5], 1u << (pos & 31));
+        if (eq) atomicOr(&sm.eq_bits[pos >> 5], 1u << (pos & 31));
+    }
+    // word prefixes: hist[w] = packed (gt | eq << 16) count before word w;
+    // wave 0 scans the 1024 words, 16 per lane
+    __device__ __forceinline__ static void scan(SelSmem& sm) {
+        if (threadIdx.x < kWave) {
+            const int lane = threadIdx.x;
+            uint32_t c[16];
+            uint32_t local = 0;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        uint32_t n = 0;
+            for (int i = 0; i < 16; ++i) {
+                const int wd = 16 * lane + i;
+                c[i] = (uint32_t)__popc(sm.gt_bits[wd]) | ((uint32_t)__popc(sm.eq_bits[wd]) << 16);
+                local += c[i];
+            }
+            uint32_t run = wave_inclusive_sum(local) - local;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t k = key[4 * c + e];
-            n += k > tau ? 1u : (k == tau ? 0x10000u : 0u);
+            for (int i = 0; i < 16; ++i) {
+                sm.hist[16 * lane + i] = run;
+                run += c[i];
+            }
         }
-        cnt[c] = n;
-        incl[c] = wave_inclusive_sum(n);
+        __syncthreads();
     }
-    if (lane == kWave - 1) {
+    // output slot of a marked position, or -1 for an eq item past the first r
+    __device__ __forceinline__ static int32_t slot(const SelSmem& sm, uint32_t pos, bool gt, uint32_t r) {
+        const uint32_t w = pos >> 5, below = (1u << (pos & 31)) - 1u;
+        const uint32_t pre = sm.hist[w];
+        const uint32_t g = (pre & 0xffffu) + (uint32_t)__popc(sm.gt_bits[w] & below);
+        const uint32_t e = (pre >> 16) + (uint32_t)__popc(sm.eq_bits[w] & below);
+        if (gt) return (int32_t)(g + min(e, r));
+        return e < r ? (int32_t)(g + e) : -1;
+    }
+};
+
+__device__ __forceinline__ void put(SelSmem& sm, int32_t at, uint32_t pos, uint32_t k) {
+    sm.sel[at] = (int32_t)pos | (k == kNegInfKey ? (int32_t)kInfBit : 0);
+    sm.selkey[at] = k;
+}
+
+// Selects the T largest keys of positions [0, n) of `src` (n > T, n <= kSpan;
+// ties toward the lower position) into sm.sel / sm.selkey [0, T), ascending by
+// position.  src.load4(p, k) returns the keys of positions p..p+3 (p % 4 == 0),
+// key 0 past n.  Ends with a barrier.
+template <class Src>
+__device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm) {
+    const int t = threadIdx.x, w = t / kWave, lane = __lane_id();
+    const int32_t n = src.n;
+    // 1. pivot from 4096 sampled keys
+    uint32_t sk[4];
+    src.load4((int32_t)(((int64_t)t * n / kBlock) & ~3ll), sk);
+    uint32_t smax = 0, smin = 0xffffffffu, scnt = 0;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) sm.ctot[c * kWaves + w] = incl[c];
+    for (int e = 0; e < 4; ++e) key_stats(sk[e], smax, smin, scnt);
+    if (t == 0) sm.ncand = 0;
+    block_stats(smax, smin, scnt, sm);
+    uint32_t pivot = kNegInfKey + 1;
+    if (scnt > 0 && smax == smin) {
+        pivot = smin;
+    } else if (scnt > 0) {
+        Radix rx;
+        rx.start(smax, smin, 1);
+        const int lo = rx.shift > 12 ? rx.shift - 12 : 0;
+        clear_hist(sm);
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (sk[e] > kNegInfKey) atomicAdd(&sm.hist[(sk[e] >> lo) & 0xfffu], 1u);
+        __syncthreads();
+        const uint64_t want = (uint64_t)scnt * T * 3 / (2ull * (uint64_t)n) + 16ull;
+        uint32_t bin, above;
+        find_bin((uint32_t)min((uint64_t)scnt, want), sm, bin, above);
+        pivot = max(rx.prefix | (bin << lo), kNegInfKey + 1);
+    }
+    // 2. stream: candidates >= pivot into LDS, row statistics on the side.
+    //    Each wave keeps kBatch 1 KB loads in flight.
+    uint32_t rmax = 0, rmin = 0xffffffffu, rcnt = 0;
+    const int32_t steps = (n + 255) / 256;
+    constexpr int kBatch = 4;
+    for (int32_t s0 = w; s0 < steps; s0 += kWaves * kBatch) {
+        uint32_t k[kBatch][4];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int32_t s = s0 + u * kWaves;
+            if (s < steps) {
+                src.load4(s * 256 + 4 * lane, k[u]);
+            } else {
+                k[u][0] = k[u][1] = k[u][2] = k[u][3] = 0u;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int32_t p = (s0 + u * kWaves) * 256 + 4 * lane;
+            uint32_t c = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                key_stats(k[u][e], rmax, rmin, rcnt);
+                c += k[u][e] >= pivot ? 1u : 0u;
+            }
+            const uint32_t incl = wave_inclusive_sum(c);
+            const uint32_t total = readlane(incl, kWave - 1);
+            if (total == 0) continue;
+            uint32_t base = 0;
+            if (lane == kWave - 1) base = atomicAdd(&sm.ncand, total);
+            uint32_t at = readlane(base, kWave - 1) + incl - c;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (k[u][e] >= pivot) {
+                    if (at < (uint32_t)kCandMax) {
+                        sm.cand_key[at] = k[u][e];
+                        sm.cand_pos[at] = (uint16_t)(p + e);
+                    }
+                    ++at;
+                }
+            }
+        }
     }
     __syncthreads();
-    if (w == 0) {
-        // exclusive scan over (chunk, wave) in index order; 2 entries per lane
-        const int q0 = 2 * lane, q1 = 2 * lane + 1;
-        const uint32_t a = q0 < NC * kWaves ? sm.ctot[q0] : 0u;
-        const uint32_t b = q1 < NC * kWaves ? sm.ctot[q1] : 0u;
-        const uint32_t s = wave_inclusive_sum(a + b);
-        if (q0 < NC * kWaves) sm.cbase[q0] = s - a - b;
-        if (q1 < NC * kWaves) sm.cbase[q1] = s - b;
+    const uint32_t ncand = sm.ncand;
+    block_stats(rmax, rmin, rcnt, sm);
+    Ranker::clear(sm);
+    __syncthreads();
+    if (ncand >= T && ncand <= (uint32_t)kCandMax) {
+        // 3. radix select on the candidates (5 per thread, slot q = i*kBlock + t)
+        uint32_t ck[kCandPerThread];
+        uint32_t cmax = 0, cmin = 0xffffffffu, cc = 0;
+#pragma unroll
+        for (int i = 0; i < kCandPerThread; ++i) {
+            const uint32_t q = i * kBlock + t;
+            ck[i] = q < ncand ? sm.cand_key[q] : 0u;
+            key_stats(ck[i], cmax, cmin, cc);
+        }
+        block_stats(cmax, cmin, cc, sm);
+        uint32_t tau = cmax, r = T;
+        if (cmax != cmin) {
+            Radix rx;
+            rx.start(cmax, cmin, T);
+            while (rx.shift > 0) {
+                clear_hist(sm);
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < kCandPerThread; ++i)
+                    if (rx.counts(ck[i], true)) atomicAdd(&sm.hist[rx.digit(ck[i])], 1u);
+                __syncthreads();
+                rx.finish(sm);
+            }
+            tau = rx.prefix;
+            r = rx.remaining;
+        }
+        // 4. position ranks
+#pragma unroll
+        for (int i = 0; i < kCandPerThread; ++i) {
+            const uint32_t q = i * kBlock + t;
+            if (q < ncand) Ranker::mark(sm, sm.cand_pos[q], ck[i] > tau, ck[i] == tau);
+        }
+        __syncthreads();
+        Ranker::scan(sm);
+#pragma unroll
+        for (int i = 0; i < kCandPerThread; ++i) {
+            const uint32_t q = i * kBlock + t;
+            if (q < ncand && ck[i] >= tau) {
+                const uint32_t pos = sm.cand_pos[q];
+                const int32_t at = Ranker::slot(sm, pos, ck[i] > tau, r);
+                if (at >= 0) put(sm, at, pos, ck[i]);
+            }
+        }
+        __syncthreads();
+        return;
+    }
+    // fallback: the same steps on the whole row, streamed again
+    uint32_t tau, r;
+    if (rcnt >= T) {
+        if (rmax == rmin) {
+            tau = rmax;
+            r = T;
+        } else {
+            Radix rx;
+            rx.start(rmax, rmin, T);
+            while (rx.shift > 0) {
+                clear_hist(sm);
+                __syncthreads();
+                for (int32_t s = w; s < steps; s += kWaves) {
+                    uint32_t k[4];
+                    src.load4(s * 256 + 4 * lane, k);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (rx.counts(k[e], true)) atomicAdd(&sm.hist[rx.digit(k[e])], 1u);
+                }
+                __syncthreads();
+                rx.finish(sm);
+            }
+            tau = rx.prefix;
+            r = rx.remaining;
+        }
+    } else {
+        // fewer than T keys above -inf: every key counts (-inf, NaN, padding)
+        Radix rx;
+        rx.prefix = 0;
+        rx.pmask = 0;
+        rx.remaining = T;
+        rx.shift = 32;
+        while (rx.shift > 0) {
+            clear_hist(sm);
+            __syncthreads();
+            for (int32_t s = w; s < steps; s += kWaves) {
+                uint32_t k[4];
+                src.load4(s * 256 + 4 * lane, k);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (s * 256 + 4 * lane + e < n && rx.counts(k[e], false)) atomicAdd(&sm.hist[rx.digit(k[e])], 1u);
+            }
+            __syncthreads();
+            rx.finish(sm);
+        }
+        tau = rx.prefix;
+        r = rx.remaining;
+    }
+    for (int32_t s = w; s < steps; s += kWaves) {
+        const int32_t p = s * 256 + 4 * lane;
+        uint32_t k[4];
+        src.load4(p, k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (p + e < n) Ranker::mark(sm, p + e, k[e] > tau, k[e] == tau);
     }
     __syncthreads();
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const uint32_t before = sm.cbase[c * kWaves + w] + incl[c] - cnt[c];
-        uint32_t gt = before & 0xffffu, eq = before >> 16;
+    Ranker::scan(sm);
+    for (int32_t s = w; s < steps; s += kWaves) {
+        const int32_t p = s * 256 + 4 * lane;
+        uint32_t k[4];
+        src.load4(p, k);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint32_t k = key[4 * c + e];
-            const int32_t j = c * kChunk + 4 * t + e;
-            const int32_t tag = k == kNegInfKey ? (int32_t)kInfBit : 0;
-            if (k > tau) {
-                const uint32_t at = gt + min(eq, r);
-                sm.sel[at] = j | tag;
-                sm.hist[at] = k;
-                ++gt;
-            } else if (k == tau) {
-                if (eq < r) {
-                    sm.sel[gt + eq] = j | tag;
-                    sm.hist[gt + eq] = k;
-                }
-                ++eq;
+            if (p + e < n && k[e] >= tau) {
+                const int32_t at = Ranker::slot(sm, p + e, k[e] > tau, r);
+                if (at >= 0) put(sm, at, p + e, k[e]);
             }
         }
     }
     __syncthreads();
 }
 
-// Loads columns [0, n) of one row (n <= ITEMS*1024) as keys; others get key 0.
-template <int ITEMS>
-__device__ __forceinline__ void load_keys(const float* __restrict__ rowp, int32_t n, uint32_t (&key)[ITEMS]) {
-    constexpr int NC = ITEMS / 4;
-    const int t = threadIdx.x;
-    const bool vec = (reinterpret_cast<uintptr_t>(rowp) & 15) == 0;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int32_t j = c * kChunk + 4 * t;
-        if (vec && j + 3 < n) {
-            const float4 v = *reinterpret_cast<const float4*>(rowp + j);
-            key[4 * c + 0] = score_key(v.x);
-            key[4 * c + 1] = score_key(v.y);
-            key[4 * c + 2] = score_key(v.z);
-            key[4 * c + 3] = score_key(v.w);
+// ------------------------------------------------------------ key sources
+// Columns [lo, lo + n) of one fp32 score row.
+struct RowSrc {
+    const float* row;  // already offset by lo
+    int32_t n;
+    bool vec;
+    __device__ __forceinline__ void load4(int32_t p, uint32_t (&k)[4]) const {
+        if (vec && p + 3 < n) {
+            const float4 v = *reinterpret_cast<const float4*>(row + p);
+            k[0] = score_key(v.x);
+            k[1] = score_key(v.y);
+            k[2] = score_key(v.z);
+            k[3] = score_key(v.w);
         } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) key[4 * c + e] = j + e < n ? score_key(rowp[j + e]) : 0u;
+            for (int e = 0; e < 4; ++e) k[e] = p + e < n ? score_key(row[p + e]) : 0u;
         }
     }
-}
+};
 
 // ------------------------------------------------------------------ V1 map
 struct V1Params {
@@ -252,39 +509,6 @@ __device__ __forceinline__ int32_t v1_mask_page(const V1Params& p, int64_t row, 
     if (!(bucket < ri.sink || bucket + 1024 > ri.tail)) return -1;
     if (page < 0 || page >= p.member_pages) return -1;
     return page;
-}
-
-// Applies the sink/tail mask to columns [lo, hi) of the row: writes -inf in
-// place and, for columns held in registers, turns their key into the -inf key.
-template <int ITEMS>
-__device__ void v1_apply_mask(const V1Params& p, int64_t row, const RowInfo& ri, int32_t lo, int32_t hi,
-                              uint32_t (&key)[ITEMS], int32_t reg_n, SelSmem& sm) {
-    const int t = threadIdx.x;
-    const int32_t limit = min(hi, min(ri.take * 64, p.cols));
-    const int32_t r0 = lo / 64, r1 = limit > lo ? (limit + 63) / 64 : r0;  // ranks touching [lo, limit)
-    for (int32_t r = r0 + t; r < r1; r += kBlock) sm.maskpage[r - r0] = v1_mask_page(p, row, r, ri);
-    __syncthreads();
-    float* rowp = p.scores + row * p.score_stride;
-    constexpr int NC = ITEMS / 4;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int32_t jl = c * kChunk + 4 * t + e;  // position inside the tile
-            const int32_t j = lo + jl;
-            if (j < limit) {
-                const int32_t page = sm.maskpage[j / 64 - r0];
-                if (page >= 0) {
-                    const int32_t lg = p.members[(int64_t)page * 64 + (j & 63)];
-                    if (lg < ri.sink || lg >= ri.tail) {
-                        rowp[j] = -__builtin_huge_valf();
-                        if (jl < reg_n) key[4 * c + e] = kNegInfKey;
-                    }
-                }
-            }
-        }
-    }
-    __syncthreads();
 }
 
 // raw -> logical -> physical for one output slot.
@@ -358,44 +582,99 @@ __device__ __forceinline__ void transform_emit(const TransformParams& p, int64_t
     if (p.raw_indices) p.raw_indices[dst] = raw;
 }
 
+// A V1 row with the sink/tail mask applied on the fly: positions of masked
+// pages (sm.maskpage) whose member lies outside [sink, tail) read as -inf.
+struct V1Src {
+    RowSrc base;
+    const int32_t* members;
+    const int32_t* maskpage;  // LDS, indexed by (position - segment start) / 64
+    int32_t masked_end;       // positions below it may be masked (take * 64 - lo)
+    int32_t sink, tail;
+    int32_t n;
+    __device__ __forceinline__ void load4(int32_t p, uint32_t (&k)[4]) const {
+        base.load4(p, k);
+        if (p < masked_end) {
+            const int32_t page = maskpage[p >> 6];
+            if (page >= 0) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (p + e < n) {
+                        const int32_t lg = members[(int64_t)page * 64 + ((p + e) & 63)];
+                        if (lg < sink || lg >= tail) k[e] = kNegInfKey;
+                    }
+                }
+            }
+        }
+    }
+};
+
+// Sets sm.maskpage for the ranks touching [lo, lo + kSpan) and writes -inf in
+// place for every masked position below min(take * 64, cols) in that range.
+// sglang/kernels/jit/csrc/deepseek_v4/v1_query.cuh:71-107.  Ends with a barrier.
+__device__ void v1_prepare_mask(const V1Params& p, int64_t row, const RowInfo& ri, int32_t lo, SelSmem& sm,
+                                int32_t& masked_end) {
+    const int t = threadIdx.x;
+    const int32_t limit = min(lo + kSpan, min(ri.take * 64, p.cols));
+    masked_end = p.mask ? max(0, limit - lo) : 0;
+    const int32_t nranks = (masked_end + 63) / 64;
+    for (int32_t r = t; r < nranks; r += kBlock) sm.maskpage[r] = v1_mask_page(p, row, lo / 64 + r, ri);
+    __syncthreads();
+    float* rowp = p.scores + row * p.score_stride + lo;
+    for (int32_t j = t; j < masked_end; j += kBlock) {
+        const int32_t page = sm.maskpage[j >> 6];
+        if (page >= 0) {
+            const int32_t lg = p.members[(int64_t)page * 64 + (j & 63)];
+            if (lg < ri.sink || lg >= ri.tail) rowp[j] = -__builtin_huge_valf();
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ V1Src v1_source(const V1Params& p, int64_t row, const RowInfo& ri, int32_t lo, int32_t n,
+                                           int32_t masked_end, const SelSmem& sm) {
+    const float* rp = p.scores + row * p.score_stride + lo;
+    V1Src s;
+    s.base = RowSrc{rp, n, (reinterpret_cast<uintptr_t>(rp) & 15) == 0};
+    s.members = p.members;
+    s.maskpage = sm.maskpage;
+    s.masked_end = masked_end;
+    s.sink = ri.sink;
+    s.tail = ri.tail;
+    s.n = n;
+    return s;
+}
+
 // --------------------------------------------------------- single pass
-template <int ITEMS>
-__global__ __launch_bounds__(kBlock) void v1_topk_rows(V1Params p) {
+__global__ __launch_bounds__(kBlock, 8) void v1_topk_rows(V1Params p) {
     __shared__ SelSmem sm;
     const int64_t row = blockIdx.x;
     const RowInfo ri = v1_row_info(p, row);
     const int32_t L = max(0, min(p.fine_lens[row], p.cols));
-    uint32_t key[ITEMS];
-    load_keys<ITEMS>(p.scores + row * p.score_stride, L, key);
-    if (p.mask) v1_apply_mask<ITEMS>(p, row, ri, 0, p.cols, key, L, sm);
+    int32_t masked_end;
+    v1_prepare_mask(p, row, ri, 0, sm, masked_end);
+    const V1Src src = v1_source(p, row, ri, 0, L, masked_end, sm);
     const int32_t T = p.topk;
-    int32_t nsel;
     if (L <= T) {
-        // every candidate; -inf status needs the key of position tx
-        constexpr int NC = ITEMS / 4;
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int32_t j = c * kChunk + 4 * threadIdx.x + e;
-                if (j < L) sm.sel[j] = j | (key[4 * c + e] == kNegInfKey ? (int32_t)kInfBit : 0);
+        for (int tx = threadIdx.x; tx < T; tx += kBlock) {
+            bool inf = false;
+            if (tx < L) {
+                uint32_t k[4];
+                src.load4(tx & ~3, k);
+                inf = k[tx & 3] == kNegInfKey;
             }
-        __syncthreads();
-        nsel = L;
+            v1_emit(p, row, ri, tx, tx < L ? tx : -1, inf);
+        }
     } else {
-        select_top<ITEMS>(key, (uint32_t)T, sm);
-        nsel = T;
-    }
-    for (int tx = threadIdx.x; tx < T; tx += kBlock) {
-        const int32_t s = tx < nsel ? sm.sel[tx] : -1;
-        const bool inf = s != -1 && (s & (int32_t)kInfBit);
-        v1_emit(p, row, ri, tx, s == -1 ? -1 : (s & 0x7fffffff), inf);
+        select_stream(src, (uint32_t)T, sm);
+        for (int tx = threadIdx.x; tx < T; tx += kBlock) {
+            const int32_t s = sm.sel[tx];
+            v1_emit(p, row, ri, tx, s & 0x7fffffff, (s & (int32_t)kInfBit) != 0);
+        }
     }
     v1_pad_expansion(p, row);
 }
 
-template <int ITEMS>
-__global__ __launch_bounds__(kBlock) void transform_rows(TransformParams p) {
+__global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
     __shared__ SelSmem sm;
     const int64_t row = blockIdx.x;
     const int32_t L = max(0, min(p.seq_lens[row], p.cols));
@@ -404,9 +683,9 @@ __global__ __launch_bounds__(kBlock) void transform_rows(TransformParams p) {
         for (int tx = threadIdx.x; tx < T; tx += kBlock) transform_emit(p, row, tx, tx < L ? tx : -1);
         return;
     }
-    uint32_t key[ITEMS];
-    load_keys<ITEMS>(p.scores + row * p.score_stride, L, key);
-    select_top<ITEMS>(key, (uint32_t)T, sm);
+    const float* rp = p.scores + row * p.score_stride;
+    const RowSrc src{rp, L, (reinterpret_cast<uintptr_t>(rp) & 15) == 0};
+    select_stream(src, (uint32_t)T, sm);
     for (int tx = threadIdx.x; tx < T; tx += kBlock) transform_emit(p, row, tx, sm.sel[tx] & 0x7fffffff);
 }
 
@@ -422,13 +701,13 @@ struct Workspace {
 };
 
 inline int64_t workspace_bytes(int32_t batch, int32_t cols, int32_t topk) {
-    const int64_t nseg = cdiv(cols, kSegment);
+    const int64_t nseg = cdiv(cols, kSpan);
     return (int64_t)batch * nseg * ((int64_t)topk * 8 + 4);
 }
 
 inline Workspace make_workspace(void* base, int32_t batch, int32_t cols, int32_t topk) {
     Workspace ws;
-    ws.nseg = (int32_t)cdiv(cols, kSegment);
+    ws.nseg = (int32_t)cdiv(cols, kSpan);
     ws.T = topk;
     const int64_t pairs = (int64_t)batch * ws.nseg;
     ws.keys = static_cast<uint32_t*>(base);
@@ -437,85 +716,85 @@ inline Workspace make_workspace(void* base, int32_t batch, int32_t cols, int32_t
     return ws;
 }
 
-// Segment s of a row: the segment's Top-T (all of it when shorter) into the
-// workspace in ascending position.  Keys are forced >= 1 so that the merge's
-// padding key 0 stays strictly below every real candidate.
-__device__ void segment_select(const uint32_t (&key)[32], int32_t n, int32_t lo, int32_t T, const Workspace& ws,
-                               int64_t row, int32_t s, SelSmem& sm) {
+// Segment s of a row: its Top-T (all of it when shorter) into the workspace in
+// ascending position.  Keys are forced >= 1 so that the merge's padding key 0
+// stays strictly below every real candidate.
+template <class Src>
+__device__ __forceinline__ void segment_select(const Src& src, int32_t lo, int32_t T, const Workspace& ws, int64_t row,
+                                               int32_t s, SelSmem& sm) {
     const int64_t at = ws.at(row, s);
+    const int32_t n = src.n;
     if (n <= T) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
+        for (int32_t j = 4 * threadIdx.x; j < n; j += 4 * kBlock) {
+            uint32_t k[4];
+            src.load4(j, k);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int32_t j = c * kChunk + 4 * threadIdx.x + e;
-                if (j < n) {
-                    ws.keys[at + j] = max(key[4 * c + e], 1u);
-                    ws.pos[at + j] = lo + j;
+                if (j + e < n) {
+                    ws.keys[at + j + e] = max(k[e], 1u);
+                    ws.pos[at + j + e] = lo + j + e;
                 }
             }
-        if (threadIdx.x == 0) ws.count[row * ws.nseg + s] = max(n, 0);
+        }
+        if (threadIdx.x == 0) ws.count[row * ws.nseg + s] = n;
         return;
     }
-    select_top<32>(key, (uint32_t)T, sm);
+    select_stream(src, (uint32_t)T, sm);
     for (int tx = threadIdx.x; tx < T; tx += kBlock) {
-        ws.keys[at + tx] = max(sm.hist[tx], 1u);
+        ws.keys[at + tx] = max(sm.selkey[tx], 1u);
         ws.pos[at + tx] = lo + (sm.sel[tx] & 0x7fffffff);
     }
     if (threadIdx.x == 0) ws.count[row * ws.nseg + s] = T;
 }
 
-__global__ __launch_bounds__(kBlock) void v1_topk_segments(V1Params p, Workspace ws) {
+__global__ __launch_bounds__(kBlock, 8) void v1_topk_segments(V1Params p, Workspace ws) {
     __shared__ SelSmem sm;
     const int32_t s = blockIdx.x;
     const int64_t row = blockIdx.y;
     const RowInfo ri = v1_row_info(p, row);
     const int32_t L = max(0, min(p.fine_lens[row], p.cols));
-    const int32_t lo = s * kSegment;
-    const int32_t n = max(0, min(L - lo, kSegment));
-    uint32_t key[32];
-    load_keys<32>(p.scores + row * p.score_stride + lo, n, key);
-    if (p.mask) v1_apply_mask<32>(p, row, ri, lo, lo + kSegment, key, n, sm);
+    const int32_t lo = s * kSpan;
+    int32_t masked_end;
+    v1_prepare_mask(p, row, ri, lo, sm, masked_end);
     if (L <= p.topk) return;  // the merge kernel takes every candidate
-    segment_select(key, n, lo, p.topk, ws, row, s, sm);
+    const int32_t n = max(0, min(L - lo, kSpan));
+    segment_select(v1_source(p, row, ri, lo, n, masked_end, sm), lo, p.topk, ws, row, s, sm);
 }
 
-__global__ __launch_bounds__(kBlock) void transform_segments(TransformParams p, Workspace ws) {
+__global__ __launch_bounds__(kBlock, 8) void transform_segments(TransformParams p, Workspace ws) {
     __shared__ SelSmem sm;
     const int32_t s = blockIdx.x;
     const int64_t row = blockIdx.y;
     const int32_t L = max(0, min(p.seq_lens[row], p.cols));
     if (L <= p.topk) return;
-    const int32_t lo = s * kSegment;
-    const int32_t n = max(0, min(L - lo, kSegment));
-    uint32_t key[32];
-    load_keys<32>(p.scores + row * p.score_stride + lo, n, key);
-    segment_select(key, n, lo, p.topk, ws, row, s, sm);
+    const int32_t lo = s * kSpan;
+    const int32_t n = max(0, min(L - lo, kSpan));
+    const float* rp = p.scores + row * p.score_stride + lo;
+    segment_select(RowSrc{rp, n, (reinterpret_cast<uintptr_t>(rp) & 15) == 0}, lo, p.topk, ws, row, s, sm);
 }
 
-// Loads the concatenated segment candidates of a row: position q = s*T + k.
-template <int ITEMS>
-__device__ __forceinline__ void load_candidates(const Workspace& ws, int64_t row, uint32_t (&key)[ITEMS]) {
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int c = 0; c < ITEMS / 4; ++c)
+// The concatenated segment candidates of a row: position q = s*T + k.
+struct CandSrc {
+    const uint32_t* keys;  // workspace keys of this row
+    const int32_t* count;  // per segment
+    int32_t T;
+    int32_t nseg;
+    int32_t n;
+    __device__ __forceinline__ void load4(int32_t q, uint32_t (&k)[4]) const {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int32_t q = c * kChunk + 4 * t + e;
-            const int32_t s = q / ws.T, k = q - s * ws.T;
-            uint32_t v = 0u;
-            if (s < ws.nseg && k < ws.count[row * ws.nseg + s]) v = ws.keys[ws.at(row, s) + k];
-            key[4 * c + e] = v;
+            const int32_t qq = q + e;
+            const int32_t s = qq / T, j = qq - s * T;
+            k[e] = (s < nseg && j < count[s]) ? keys[qq] : 0u;
         }
+    }
+};
+
+__device__ __forceinline__ CandSrc cand_source(const Workspace& ws, int64_t row) {
+    return CandSrc{ws.keys + ws.at(row, 0), ws.count + row * ws.nseg, ws.T, ws.nseg, ws.nseg * ws.T};
 }
 
-__device__ __forceinline__ int32_t candidate_pos(const Workspace& ws, int64_t row, int32_t q) {
-    const int32_t s = q / ws.T, k = q - s * ws.T;
-    return ws.pos[ws.at(row, s) + k];
-}
-
-template <int ITEMS>
-__global__ __launch_bounds__(kBlock) void v1_topk_merge(V1Params p, Workspace ws) {
+__global__ __launch_bounds__(kBlock, 8) void v1_topk_merge(V1Params p, Workspace ws) {
     __shared__ SelSmem sm;
     const int64_t row = blockIdx.x;
     const RowInfo ri = v1_row_info(p, row);
@@ -529,19 +808,17 @@ __global__ __launch_bounds__(kBlock) void v1_topk_merge(V1Params p, Workspace ws
             v1_emit(p, row, ri, tx, ok ? tx : -1, inf);
         }
     } else {
-        uint32_t key[ITEMS];
-        load_candidates<ITEMS>(ws, row, key);
-        select_top<ITEMS>(key, (uint32_t)T, sm);
+        select_stream(cand_source(ws, row), (uint32_t)T, sm);
+        const int32_t* pos = ws.pos + ws.at(row, 0);
         for (int tx = threadIdx.x; tx < T; tx += kBlock) {
             const int32_t q = sm.sel[tx];
-            v1_emit(p, row, ri, tx, candidate_pos(ws, row, q & 0x7fffffff), (q & (int32_t)kInfBit) != 0);
+            v1_emit(p, row, ri, tx, pos[q & 0x7fffffff], (q & (int32_t)kInfBit) != 0);
         }
     }
     v1_pad_expansion(p, row);
 }
 
-template <int ITEMS>
-__global__ __launch_bounds__(kBlock) void transform_merge(TransformParams p, Workspace ws) {
+__global__ __launch_bounds__(kBlock, 8) void transform_merge(TransformParams p, Workspace ws) {
     __shared__ SelSmem sm;
     const int64_t row = blockIdx.x;
     const int32_t L = max(0, min(p.seq_lens[row], p.cols));
@@ -550,11 +827,9 @@ __global__ __launch_bounds__(kBlock) void transform_merge(TransformParams p, Wor
         for (int tx = threadIdx.x; tx < T; tx += kBlock) transform_emit(p, row, tx, tx < L ? tx : -1);
         return;
     }
-    uint32_t key[ITEMS];
-    load_candidates<ITEMS>(ws, row, key);
-    select_top<ITEMS>(key, (uint32_t)T, sm);
-    for (int tx = threadIdx.x; tx < T; tx += kBlock)
-        transform_emit(p, row, tx, candidate_pos(ws, row, sm.sel[tx] & 0x7fffffff));
+    select_stream(cand_source(ws, row), (uint32_t)T, sm);
+    const int32_t* pos = ws.pos + ws.at(row, 0);
+    for (int tx = threadIdx.x; tx < T; tx += kBlock) transform_emit(p, row, tx, pos[sm.sel[tx] & 0x7fffffff]);
 }
 
 // ------------------------------------------------------ unfused mask/map
@@ -626,29 +901,24 @@ __global__ void output_ids_kernel(const int32_t* raw_in, const float* scores, in
     logical_out[dst] = valid ? logical : -1;
 }
 
-template <typename P>
-int launch_single(void (*k4)(P), void (*k8)(P), void (*k16)(P), void (*k32)(P), int32_t cols, int32_t batch,
-                  const P& p, hipStream_t st, const char* name) {
-    auto kern = cols <= 4096 ? k4 : cols <= 8192 ? k8 : cols <= 16384 ? k16 : k32;
-    hipLaunchKernelGGL(kern, dim3(batch), dim3(kBlock), 0, st, p);
-    return V1_LAUNCHED(name);
-}
 
 template <typename P>
-int launch_segmented(void (*seg)(P, Workspace), void (*m8)(P, Workspace), void (*m16)(P, Workspace),
-                     void (*m32)(P, Workspace), int32_t cols, int32_t batch, int32_t topk, void* wsp,
-                     int64_t ws_bytes, const P& p, hipStream_t st, const char* name) {
+int launch_topk(void (*single)(P), void (*seg)(P, Workspace), void (*merge)(P, Workspace), int32_t cols,
+                int32_t batch, int32_t topk, void* wsp, int64_t ws_bytes, const P& p, hipStream_t st,
+                const char* name) {
+    if (cols <= kSpan) {
+        hipLaunchKernelGGL(single, dim3(batch), dim3(kBlock), 0, st, p);
+        return V1_LAUNCHED(name);
+    }
     V1_REQUIRE(wsp != nullptr && ws_bytes >= workspace_bytes(batch, cols, topk),
-               "%s: rows longer than %d columns need a workspace of %lld bytes", name, kSegment,
+               "%s: rows longer than %d columns need a workspace of %lld bytes", name, kSpan,
                (long long)workspace_bytes(batch, cols, topk));
     const Workspace ws = make_workspace(wsp, batch, cols, topk);
-    const int64_t cand = (int64_t)ws.nseg * topk;
-    V1_REQUIRE(cand <= 32 * kBlock, "%s: %d columns exceed the %lld supported at topk %d", name, cols,
-               (long long)(32 * kBlock / topk) * kSegment, topk);
+    V1_REQUIRE((int64_t)ws.nseg * topk <= kSpan, "%s: %d columns exceed the %lld supported at topk %d", name, cols,
+               (long long)(kSpan / topk) * kSpan, topk);
     hipLaunchKernelGGL(seg, dim3(ws.nseg, batch), dim3(kBlock), 0, st, p, ws);
     int rc = V1_LAUNCHED(name);
     if (rc != V1_OK) return rc;
-    auto merge = cand <= 8192 ? m8 : cand <= 16384 ? m16 : m32;
     hipLaunchKernelGGL(merge, dim3(batch), dim3(kBlock), 0, st, p, ws);
     return V1_LAUNCHED(name);
 }
@@ -659,7 +929,7 @@ int launch_segmented(void (*seg)(P, Workspace), void (*m8)(P, Workspace), void (
 using namespace v1;
 
 extern "C" int64_t v1_topk_workspace(int32_t batch, int32_t cols, int32_t topk) {
-    if (cols <= kSegment || batch <= 0 || topk <= 0) return 0;
+    if (cols <= kSpan || batch <= 0 || topk <= 0) return 0;
     return workspace_bytes(batch, cols, topk);
 }
 
@@ -677,13 +947,8 @@ extern "C" int v1_topk(const v1_topk_args* a, void* stream) {
                a->pages, a->selected, a->selected_bits == 64, a->take_stride, a->lens, a->takes, a->physical,
                a->logical, a->raw, a->topk, a->window, a->mask, a->expanded, a->expansion_stride,
                a->physical_output, a->bucket_from_rank, a->fine_table, a->fine_table_cols, a->direct_fine};
-    hipStream_t st = as_stream(stream);
-    if (a->cols <= kSegment)
-        return launch_single<V1Params>(v1_topk_rows<4>, v1_topk_rows<8>, v1_topk_rows<16>, v1_topk_rows<32>,
-                                       a->cols, a->batch, p, st, "v1_topk");
-    return launch_segmented<V1Params>(v1_topk_segments, v1_topk_merge<8>, v1_topk_merge<16>, v1_topk_merge<32>,
-                                      a->cols, a->batch, a->topk, a->workspace, a->workspace_bytes, p, st,
-                                      "v1_topk");
+    return launch_topk<V1Params>(v1_topk_rows, v1_topk_segments, v1_topk_merge, a->cols, a->batch, a->topk,
+                                 a->workspace, a->workspace_bytes, p, as_stream(stream), "v1_topk");
 }
 
 extern "C" int v1_topk_transform(const v1_topk_transform_args* a, void* stream) {
@@ -694,13 +959,9 @@ extern "C" int v1_topk_transform(const v1_topk_transform_args* a, void* stream) 
     if (a->batch == 0) return V1_OK;
     TransformParams p{a->scores, a->score_stride, a->cols, a->seq_lens, a->page_table, a->page_table_stride,
                       a->page_table_cols, a->page_bits, a->page_indices, a->raw_indices, a->topk};
-    hipStream_t st = as_stream(stream);
-    if (a->cols <= kSegment)
-        return launch_single<TransformParams>(transform_rows<4>, transform_rows<8>, transform_rows<16>,
-                                              transform_rows<32>, a->cols, a->batch, p, st, "topk_transform");
-    return launch_segmented<TransformParams>(transform_segments, transform_merge<8>, transform_merge<16>,
-                                             transform_merge<32>, a->cols, a->batch, a->topk, a->workspace,
-                                             a->workspace_bytes, p, st, "topk_transform");
+    return launch_topk<TransformParams>(transform_rows, transform_segments, transform_merge, a->cols, a->batch,
+                                        a->topk, a->workspace, a->workspace_bytes, p, as_stream(stream),
+                                        "topk_transform");
 }
 
 extern "C" int v1_mask_fine(float* scores, int64_t score_stride, const void* selected, int32_t selected_bits,

@@ -33,11 +33,28 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=4, choices=[1, 3, 4, 5])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES bytes (HBM counter calibration) and exit")
     return ap.parse_args()
+
+
+def copy_calibration(nbytes):
+    """A plain copy kernel of known size: its FETCH_SIZE / WRITE_SIZE counters
+    give the scale between the counters and bytes moved."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 3}), flush=True)
 
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)

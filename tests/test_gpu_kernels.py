@@ -589,3 +589,43 @@ def assert_scores_close(got, ref, bound):
         i = int(np.argmax(err - tol))
         raise AssertionError(f"{int(bad.sum())} scores out of tolerance; worst got={got[fin][i]!r} "
                              f"ref={ref[fin][i]!r} magnitude={bound[fin][i]!r}")
+
+
+def _adversarial_rows(kind, g, cols):
+    if kind == "plateau":  # one value everywhere but a few larger ones: candidate count >> cap
+        r = np.full(cols, 3.0, np.float32)
+        r[g.choice(cols, 500, replace=False)] = g.random(500).astype(np.float32) + 4
+        return r
+    if kind == "ascending":  # strided sample sees a uniform ramp; the top is one contiguous run
+        return np.linspace(-1, 1, cols).astype(np.float32)
+    if kind == "descending":
+        return np.linspace(1, -1, cols).astype(np.float32)
+    if kind == "neg_inf_heavy":  # fewer real keys than T
+        r = np.full(cols, -np.inf, np.float32)
+        r[g.choice(cols, 1500, replace=False)] = g.standard_normal(1500).astype(np.float32)
+        return r
+    if kind == "two_values":
+        return np.where(g.random(cols) < 0.5, 1.0, 2.0).astype(np.float32)
+    if kind == "tiny_spread":  # keys differ only in the lowest mantissa bits
+        return (np.float32(1.0) + g.integers(0, 64, cols).astype(np.float32) * np.float32(2 ** -23)).astype(np.float32)
+    if kind == "signed_zero":
+        return np.where(g.random(cols) < 0.5, np.float32(0.0), np.float32(-0.0)).astype(np.float32)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["plateau", "ascending", "descending", "neg_inf_heavy", "two_values", "tiny_spread",
+                                  "signed_zero"])
+@pytest.mark.parametrize("cols", [2049, 9000, 32768, 100000])
+def test_topk_adversarial_rows(dev, kind, cols):
+    g = np.random.default_rng(cols)
+    B = 4
+    stride = -(-cols // 4) * 4  # the reference requires a row stride that is a multiple of 4
+    scores = np.zeros((B, stride), np.float32)
+    scores[:, :cols] = np.stack([_adversarial_rows(kind, g, cols) for _ in range(B)])
+    lens = np.int32([cols, cols - 1, 2049, min(cols, 2048)])
+    table = np.arange((cols + 63) // 64, dtype=np.int32)[None].repeat(B, 0)
+    out = torch.empty((B, 2048), device=dev, dtype=torch.int32)
+    raw = torch.empty_like(out)
+    TK.topk_transform_512_v2(T(scores, dev)[:, :cols], T(lens, dev), T(table, dev), out, 64, None, raw)
+    e_out, e_raw = O.transform_topk(scores[:, :cols], lens, table, 2048, 6)
+    assert np.array_equal(H(raw), e_raw) and np.array_equal(H(out), e_out)
