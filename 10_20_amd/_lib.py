@@ -55,7 +55,7 @@ class ScoreArgs(ctypes.Structure):
         ("q", _vp), ("kv_pages", _vp), ("kv_blocks", _c_i64), ("weights", _vp), ("context_lens", _vp),
         ("block_table", _vp), ("block_table_stride", _c_i64), ("max_blocks", _c_i32), ("logits", _vp),
         ("logits_stride", _c_i64), ("max_context_len", _c_i32), ("rows", _c_i32), ("heads", _c_i32),
-        ("relu", _c_i32), ("clean_logits", _c_i32),
+        ("relu", _c_i32), ("clean_logits", _c_i32), ("workspace", _vp), ("workspace_bytes", _c_i64),
     ]
 
 
@@ -68,6 +68,7 @@ _SIGNATURES = {
     "v1_topk_workspace": (_c_i64, [_c_i32, _c_i32, _c_i32]),
     "v1_topk_transform": (_c_i32, [ctypes.POINTER(TopkTransformArgs), _vp]),
     "v1_score": (_c_i32, [ctypes.POINTER(ScoreArgs), _vp]),
+    "v1_score_workspace": (_c_i64, [_c_i32]),
     "v1_gather_slots": (_c_i32, [_vp, _vp, _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32,
                                  _vp, _c_i64, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp]),
     "v1_gather_rows": (_c_i32, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i32, _vp, _c_i64, _c_i32,

@@ -8,11 +8,12 @@ _lock = threading.Lock()
 _buffers = {}
 
 
-def workspace(device, nbytes):
-    """(pointer, size) of a device buffer of at least nbytes, or (0, 0)."""
+def workspace(device, nbytes, tag="default"):
+    """(pointer, size) of a device buffer of at least nbytes, or (0, 0).
+    One buffer per (device, tag); calls that use one tag must not overlap."""
     if nbytes <= 0:
         return 0, 0
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device(), tag)
     with _lock:
         buf = _buffers.get(key)
         if buf is None or buf.numel() < nbytes:

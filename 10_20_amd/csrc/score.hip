@@ -56,7 +56,76 @@ struct ScoreParams {
     int32_t heads;
     int32_t relu;
     int32_t clean;
+    const uint8_t* pieces;  // linear-term pieces per row (shared-table ReLU path)
 };
+
+// ---------------------------------------------------------- linear term
+// relu(x) = (x + |x|) / 2, so  sum_h w_h relu(q_h . k)
+//   = 1/2 (sum_h w_h q_h) . k  +  1/2 sum_h w_h |q_h . k|.
+// The first term is one more dot product per query: q' = sum_h w_h q_h is
+// split into kPieces FP8 (e4m3fn) vectors with power-of-two scales,
+// q' ~= sum_p s_p u_p, each piece taking the residual of the previous ones
+// (every piece shrinks the residual at least 16x, so the last one leaves
+// less than 16^-8 of max|q'|), and those pieces ride in an MFMA row block.
+constexpr int kPieces = 8;
+constexpr int64_t kPieceRowBytes = kPieces * 128 + kPieces * 4;  // bytes + scales per query
+
+__device__ __forceinline__ float e4m3_value(uint32_t c) {
+    const uint32_t e = (c >> 3) & 15, m = c & 7;
+    const float v = e == 0 ? (float)m * 0.001953125f : __builtin_ldexpf((float)(8 + m), (int)e - 10);
+    return (c & 0x80) ? -v : v;
+}
+
+// Round-to-nearest-even encoding of |x| <= 448 as OCP e4m3fn.
+__device__ __forceinline__ uint32_t e4m3_code(float x) {
+    const float a = fabsf(x);
+    uint32_t code;
+    if (a < 0.015625f) {  // below 2^-6: subnormal quanta of 2^-9 (8 quanta = the first normal)
+        code = (uint32_t)rintf(a * 512.0f);
+    } else {
+        int e;
+        frexpf(a, &e);  // a = f * 2^e, f in [0.5, 1)
+        e -= 1;         // a in [2^e, 2^(e+1))
+        const uint32_t m = (uint32_t)rintf(__builtin_ldexpf(a, -e) * 8.0f - 8.0f);  // 0..8
+        code = (uint32_t)((e + 7) << 3) + m;  // m == 8 carries into the exponent
+    }
+    return code | (x < 0.f ? 0x80u : 0u);
+}
+
+// One wave per query row: q' and its pieces.  Output per row: kPieces x 128
+// FP8 bytes, then kPieces fp32 scales.
+__global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float* w, int32_t rows, int32_t heads,
+                                                  uint8_t* out) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    const int l = __lane_id();
+    if (row >= rows) return;
+    // lane l owns dims 2l, 2l+1
+    float a0 = 0.f, a1 = 0.f;
+    for (int h = 0; h < heads; ++h) {
+        const float wh = w[row * heads + h];
+        const uint32_t b = *reinterpret_cast<const uint16_t*>(q + (row * heads + h) * 128 + 2 * l);
+        a0 = fmaf(wh, e4m3_value(b & 0xff), a0);
+        a1 = fmaf(wh, e4m3_value(b >> 8), a1);
+    }
+    uint8_t* dst = out + row * kPieceRowBytes;
+    for (int pc = 0; pc < kPieces; ++pc) {
+        float m = fmaxf(fabsf(a0), fabsf(a1));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+        // scale: smallest power of two >= m / 448 (1 when the residual is zero)
+        float sc = 1.f;
+        if (m > 0.f) {
+            int e;
+            const float f = frexpf(m / 448.f, &e);  // m/448 = f * 2^e
+            sc = __builtin_ldexpf(1.f, f == 0.5f ? e - 1 : e);
+        }
+        const uint32_t c0 = e4m3_code(a0 / sc), c1 = e4m3_code(a1 / sc);
+        *reinterpret_cast<uint16_t*>(dst + pc * 128 + 2 * l) = (uint16_t)(c0 | (c1 << 8));
+        if (l == 0) reinterpret_cast<float*>(dst + kPieces * 128)[pc] = sc;
+        a0 -= sc * e4m3_value(c0);
+        a1 -= sc * e4m3_value(c1);
+    }
+}
 
 // A fragments (HB row blocks of 16 heads) of one query; zero past `heads`.
 template <int HB>
@@ -178,36 +247,65 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         load_q<HB>(p, r, a[q]);
         load_w<HB>(p, r, w[q]);
     }
+    // ReLU path: linear-term fragment (rows 0-7: query 0's pieces, 8-15: query 1's)
+    // and per-lane coefficients of the rows this lane holds in the MFMA result.
+    v8i alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    float coef[kQueriesPerWave][4];
+    if (RELU) {
+        const int64_t rq = row0 + wv * kQueriesPerWave + ((l & 15) >> 3);
+        if (rq < p.rows) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(p.pieces + rq * kPieceRowBytes + (l & 7) * 128 + 32 * (l >> 4));
+            const u32x4 x = src[0], y = src[1];
+            alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+        }
+#pragma unroll
+        for (int q = 0; q < kQueriesPerWave; ++q) {
+            const int64_t r = row0 + wv * kQueriesPerWave + q;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int mrow = 4 * (l >> 4) + i;
+                coef[q][i] = ((mrow >> 3) == q && r < p.rows)
+                                 ? 0.5f * reinterpret_cast<const float*>(p.pieces + r * kPieceRowBytes + kPieces * 128)[mrow & 7]
+                                 : 0.f;
+            }
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[q][hb][i] *= 0.5f;
+        }
+    }
 
-    // staging: thread t moves 32 key bytes (key t/4, part t%4); t < 64 one scale
+    // staging: thread t moves 32 key bytes (key t/4, part t%4); t < 64 one
+    // scale.  A page is fetched into registers three iterations before it is
+    // computed and written to LDS one iteration before.
     const int skey = t >> 2, spart = t & 3;
-    u32x4 st0, st1;
-    float sscale = 0.f;
+    struct Stage {
+        u32x4 a, b;
+        float s;
+    };
     auto fetch = [&](int32_t pg) {
-        const int32_t page = page_of(p, row0, chunk0 + pg);
+        Stage st{u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, 0.f};
+        const int32_t page = pg < npages ? page_of(p, row0, chunk0 + pg) : -1;
         if (page >= 0) {
             const u32x4* src = reinterpret_cast<const u32x4*>(p.kv + (int64_t)page * V1_PAGE_BYTES + skey * 128 + spart * 32);
-            st0 = src[0];
-            st1 = src[1];
-            if (t < 64) sscale = reinterpret_cast<const float*>(p.kv + (int64_t)page * V1_PAGE_BYTES + 8192)[t];
-        } else {
-            st0 = st1 = u32x4{0u, 0u, 0u, 0u};
-            sscale = 0.f;
+            st.a = src[0];
+            st.b = src[1];
+            if (t < 64) st.s = reinterpret_cast<const float*>(p.kv + (int64_t)page * V1_PAGE_BYTES + 8192)[t];
         }
+        return st;
     };
-    auto stash = [&](int buf) {
+    auto stash = [&](int buf, const Stage& st) {
         u32x4* dst = reinterpret_cast<u32x4*>(&lds[buf][skey * kKeyPitch + spart * 32]);
-        dst[0] = st0;
-        dst[1] = st1;
-        if (t < 64) reinterpret_cast<float*>(&lds[buf][64 * kKeyPitch])[t] = sscale;
+        dst[0] = st.a;
+        dst[1] = st.b;
+        if (t < 64) reinterpret_cast<float*>(&lds[buf][64 * kKeyPitch])[t] = st.s;
     };
 
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    for (int32_t pg = 0; pg < npages; ++pg) {
+    // Three fixed stage registers (no copies between them, so the compiler's
+    // memory waits cover exactly the page being written to LDS): the page
+    // computed in one step was fetched three steps earlier.
+    auto step = [&](int32_t pg, Stage& sreg) {
         const int buf = pg & 1;
-        if (pg + 1 < npages) fetch(pg + 1);
         v8i b[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
@@ -216,19 +314,51 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
             b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
         }
         float out[kQueriesPerWave];
+        if (RELU) {
+            float part[kQueriesPerWave][4];
 #pragma unroll
-        for (int q = 0; q < kQueriesPerWave; ++q) {
-            float part[4];
-            page_partials<HB, RELU>(a[q], b, w[q], part);
-            out[q] = reduce_scatter4(part);
+            for (int kb = 0; kb < 4; ++kb) {
+                const v4f dl = mfma_fp8(alin, b[kb]);
+#pragma unroll
+                for (int q = 0; q < kQueriesPerWave; ++q) {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc = fmaf(coef[q][i], dl[i], acc);
+#pragma unroll
+                    for (int hb = 0; hb < HB; ++hb) {
+                        const v4f d = mfma_fp8(a[q][hb], b[kb]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc = fmaf(w[q][hb][i], fabsf(d[i]), acc);
+                    }
+                    part[q][kb] = acc;
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kQueriesPerWave; ++q) out[q] = reduce_scatter4(part[q]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < kQueriesPerWave; ++q) {
+                float part[4];
+                page_partials<HB, false>(a[q], b, w[q], part);
+                out[q] = reduce_scatter4(part);
+            }
         }
         const float scale = reinterpret_cast<const float*>(&lds[buf][64 * kKeyPitch])[l];
         const int32_t j = (chunk0 + pg) * 64 + l;
 #pragma unroll
         for (int q = 0; q < kQueriesPerWave; ++q)
             store_logit(p, row0 + wv * kQueriesPerWave + q, j, ctx[q], out[q] * scale);
-        if (pg + 1 < npages) stash(buf ^ 1);
+        if (pg + 1 < npages) stash(buf ^ 1, sreg);
+        sreg = fetch(pg + 4);
         __syncthreads();
+    };
+    stash(0, fetch(0));
+    Stage sa = fetch(1), sb = fetch(2), sc = fetch(3);
+    __syncthreads();
+    for (int32_t pg = 0; pg < npages; pg += 3) {
+        step(pg, sa);
+        if (pg + 1 < npages) step(pg + 1, sb);
+        if (pg + 2 < npages) step(pg + 2, sc);
     }
     if (p.clean) {
         // columns of this chunk past the last staged page
@@ -315,6 +445,8 @@ void launch_hb(int hb, bool relu, dim3 g, hipStream_t st, const ScoreParams& p) 
 
 using namespace v1;
 
+extern "C" int64_t v1_score_workspace(int32_t rows) { return rows > 0 ? (int64_t)rows * kPieceRowBytes : 0; }
+
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
     V1_REQUIRE(a != nullptr, "score: null args");
     V1_REQUIRE(a->heads >= 1 && a->heads <= 64, "score: heads must be in [1, 64]");
@@ -326,11 +458,20 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
     if (a->rows == 0 || a->max_context_len == 0) return V1_OK;
     ScoreParams p{a->q, a->kv_pages, a->kv_blocks, a->weights, a->context_lens, a->block_table, a->block_table_stride,
                   a->max_blocks, a->logits, a->logits_stride, a->max_context_len, a->rows, a->heads, a->relu,
-                  a->clean_logits};
+                  a->clean_logits, nullptr};
     const int hb = (a->heads + 15) / 16;
     const uint32_t chunks = (uint32_t)cdiv(cdiv(a->max_context_len, 64), kChunkPages);
     hipStream_t st = as_stream(stream);
     if (a->block_table_stride == 0) {
+        if (a->relu) {
+            V1_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= (int64_t)a->rows * kPieceRowBytes,
+                       "score: workspace of %lld bytes required", (long long)((int64_t)a->rows * kPieceRowBytes));
+            p.pieces = static_cast<const uint8_t*>(a->workspace);
+            hipLaunchKernelGGL(score_prep, dim3((uint32_t)cdiv(a->rows, 4)), dim3(256), 0, st, a->q, a->weights, a->rows,
+                               a->heads, static_cast<uint8_t*>(a->workspace));
+            const int rc = V1_LAUNCHED("score_prep");
+            if (rc != V1_OK) return rc;
+        }
         const dim3 grid(chunks, (uint32_t)cdiv(a->rows, kQueriesPerGroup));
         launch_hb<Shared>(hb, a->relu != 0, grid, st, p);
         return V1_LAUNCHED("score_shared");

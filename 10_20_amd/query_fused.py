@@ -90,7 +90,7 @@ class V1QueryModule:
         _need(es == 0 or es == T * 4 + 64, "Invalid expansion buffer")
         _need(es == 0 or expanded.is_contiguous(), "expanded must be contiguous")
         _need(B > 512 and 0 < T <= 2048 and 0 <= window <= 4096, "Unsupported fused V1 TopK")
-        ws, ws_bytes = workspace(scores.device, _lib.lib().v1_topk_workspace(B, L, T))
+        ws, ws_bytes = workspace(scores.device, _lib.lib().v1_topk_workspace(B, L, T), "topk")
         a = _lib.TopkArgs(
             _lib.ptr(scores), S, B, L, _lib.ptr(fine_lens), _lib.ptr(members), members.shape[0], _lib.ptr(rt),
             _lib.ptr(nt), P, _lib.ptr(selected), bits, K, _lib.ptr(lens), _lib.ptr(takes), _lib.ptr(physical),

@@ -44,7 +44,7 @@ def topk_transform_512_v2(scores, seq_lens, page_table, page_indices, page_size,
     if raw_indices is not None and (tuple(raw_indices.shape) != (B, T) or raw_indices.dtype != torch.int32
                                     or not raw_indices.is_contiguous()):
         raise RuntimeError("raw_indices must be contiguous int32 [batch, topk]")
-    ws, ws_bytes = workspace(scores.device, _lib.lib().v1_topk_workspace(B, L, T))
+    ws, ws_bytes = workspace(scores.device, _lib.lib().v1_topk_workspace(B, L, T), "topk")
     a = _lib.TopkTransformArgs(_lib.ptr(scores), scores.stride(0), B, L, _lib.ptr(seq_lens), _lib.ptr(page_table),
                                page_table.stride(0), page_table.shape[1], int(page_size).bit_length() - 1,
                                _lib.ptr(page_indices), _lib.ptr(raw_indices), T, ws, ws_bytes)

@@ -166,7 +166,10 @@ typedef struct {
     int32_t heads;               /* 1..64 */
     int32_t relu;                /* 1: DSA ReLU rule; 0: signed scores */
     int32_t clean_logits;
+    void* workspace;             /* >= v1_score_workspace(rows) bytes */
+    int64_t workspace_bytes;
 } v1_score_args;
+int64_t v1_score_workspace(int32_t rows);
 int v1_score(const v1_score_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
