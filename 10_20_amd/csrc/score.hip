@@ -15,9 +15,9 @@
 // stored with one coalesced 256-byte write.
 //
 // Shared-table rows (a prefill chunk of one request) are tiled 8 queries per
-// work-group: each 8448-byte key page is staged once in LDS (rows padded to
-// 144 bytes so that the 16-byte fragment reads are bank-conflict free) and
-// reused by 8 queries x 64 heads.  Rows with their own tables (decode) run one
+// work-group: each 8448-byte key page is staged once in LDS (chunks of each
+// key row swizzled so that the 16-byte fragment reads are bank-conflict free)
+// and reused by 8 queries x 64 heads.  Rows with their own tables (decode) run one
 // query per work-group, each wave streaming whole pages straight from HBM.
 #include "common.h"
 
@@ -29,8 +29,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int kKeyPitch = 144;                       // LDS bytes per staged key row
-constexpr int kPageLds = 64 * kKeyPitch + 64 * 4;    // keys + scales
 constexpr int kChunkPages = 16;                      // pages per work-group
 constexpr int kQueriesPerWave = 2;
 constexpr int kQueriesPerGroup = 4 * kQueriesPerWave;
@@ -56,7 +54,7 @@ struct ScoreParams {
     int32_t heads;
     int32_t relu;
     int32_t clean;
-    const uint8_t* pieces;  // linear-term pieces per row (shared-table ReLU path)
+    const uint8_t* pieces;  // per-query records from score_prep (shared-table kernel)
 };
 
 // ---------------------------------------------------------- linear term
@@ -68,7 +66,15 @@ struct ScoreParams {
 // (every piece shrinks the residual at least 16x, so the last one leaves
 // less than 16^-8 of max|q'|), and those pieces ride in an MFMA row block.
 constexpr int kPieces = 8;
-constexpr int64_t kPieceRowBytes = kPieces * 128 + kPieces * 4;  // bytes + scales per query
+// Per-query record written by score_prep for the shared-table kernel:
+//   [0, 1024)     kPieces x 128 FP8 piece bytes
+//   [1024, 1056)  kPieces fp32 piece scales, times 1/2 (the linear-term factor)
+//   [1056, 1312)  64 fp32 head weights, times 1/2 on the ReLU path, zero past `heads`
+// so the kernel reads everything with unconditional 16-byte loads.
+constexpr int kRecScales = kPieces * 128;
+constexpr int kRecWeights = kRecScales + kPieces * 4;
+constexpr int64_t kPieceRowBytes = kRecWeights + 64 * 4;
+static_assert(kRecWeights % 16 == 0 && kPieceRowBytes % 16 == 0, "16-byte aligned record fields");
 
 __device__ __forceinline__ float e4m3_value(uint32_t c) {
     const uint32_t e = (c >> 3) & 15, m = c & 7;
@@ -92,10 +98,10 @@ __device__ __forceinline__ uint32_t e4m3_code(float x) {
     return code | (x < 0.f ? 0x80u : 0u);
 }
 
-// One wave per query row: q' and its pieces.  Output per row: kPieces x 128
-// FP8 bytes, then kPieces fp32 scales.
+// One wave per query row: q' = sum_h w_h q_h split into its pieces, and the
+// record described above.
 __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float* w, int32_t rows, int32_t heads,
-                                                  uint8_t* out) {
+                                                  int32_t relu, uint8_t* out) {
     const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
     const int l = __lane_id();
     if (row >= rows) return;
@@ -121,26 +127,30 @@ __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float*
         }
         const uint32_t c0 = e4m3_code(a0 / sc), c1 = e4m3_code(a1 / sc);
         *reinterpret_cast<uint16_t*>(dst + pc * 128 + 2 * l) = (uint16_t)(c0 | (c1 << 8));
-        if (l == 0) reinterpret_cast<float*>(dst + kPieces * 128)[pc] = sc;
+        if (l == 0) reinterpret_cast<float*>(dst + kRecScales)[pc] = 0.5f * sc;
         a0 -= sc * e4m3_value(c0);
         a1 -= sc * e4m3_value(c1);
     }
+    reinterpret_cast<float*>(dst + kRecWeights)[l] = l < heads ? (relu ? 0.5f : 1.f) * w[row * heads + l] : 0.f;
 }
+
+// Prologue loads are issued unconditionally, from indices clamped into range,
+// and zeroed afterwards by a select: a load inside a branch is waited for
+// before the branch joins, which would serialise every one of them.
 
 // A fragments (HB row blocks of 16 heads) of one query; zero past `heads`.
 template <int HB>
 __device__ __forceinline__ void load_q(const ScoreParams& p, int64_t row, v8i (&a)[HB]) {
     const int l = __lane_id();
+    const int64_t rc = min(row, (int64_t)p.rows - 1);
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
         const int h = hb * 16 + (l & 15);
-        if (row < p.rows && h < p.heads) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(p.q + (row * p.heads + h) * 128 + 32 * (l >> 4));
-            const u32x4 x = src[0], y = src[1];
-            a[hb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
-        } else {
-            a[hb] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-        }
+        const bool ok = (row < p.rows) & (h < p.heads);
+        const u32x4* src = reinterpret_cast<const u32x4*>(p.q + (rc * p.heads + min(h, p.heads - 1)) * 128 + 32 * (l >> 4));
+        const u32x4 x = src[0], y = src[1];
+        a[hb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+        if (!ok) a[hb] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
     }
 }
 
@@ -148,12 +158,14 @@ __device__ __forceinline__ void load_q(const ScoreParams& p, int64_t row, v8i (&
 template <int HB>
 __device__ __forceinline__ void load_w(const ScoreParams& p, int64_t row, float (&w)[HB][4]) {
     const int l = __lane_id();
+    const int64_t rc = min(row, (int64_t)p.rows - 1);
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int h = hb * 16 + 4 * (l >> 4) + i;
-            w[hb][i] = (row < p.rows && h < p.heads) ? p.w[row * p.heads + h] : 0.f;
+            const float v = p.w[rc * p.heads + min(h, p.heads - 1)];
+            w[hb][i] = ((row < p.rows) & (h < p.heads)) ? v : 0.f;
         }
 }
 
@@ -196,9 +208,9 @@ __device__ __forceinline__ float reduce_scatter4(const float (&s)[4]) {
 }
 
 __device__ __forceinline__ int32_t page_of(const ScoreParams& p, int64_t row, int32_t blk) {
-    if (blk >= p.max_blocks) return -1;
-    const int32_t page = p.table[row * p.table_stride + blk];
-    return (page >= 0 && page < p.kv_blocks) ? page : -1;
+    if (p.max_blocks <= 0) return -1;
+    const int32_t page = p.table[row * p.table_stride + min(max(blk, 0), p.max_blocks - 1)];
+    return ((blk < p.max_blocks) & (page >= 0) & (page < p.kv_blocks)) ? page : -1;
 }
 
 __device__ __forceinline__ void store_logit(const ScoreParams& p, int64_t row, int32_t j, int32_t ctx, float v) {
@@ -210,24 +222,83 @@ __device__ __forceinline__ void store_logit(const ScoreParams& p, int64_t row, i
 }
 
 // ------------------------------------------------------------ shared table
+// Key pages are moved HBM -> LDS by buffer loads with the LDS destination
+// (one 16-byte chunk per lane, 1 KiB per wave instruction) into a ring of
+// kStages page buffers.  A page's MFMA B fragments are read from LDS into
+// registers one step before the page is computed, so its buffer is refilled
+// kStages pages ahead.  In LDS a page keeps its 128-byte key rows but chunk c
+// of key k sits in slot c ^ key_swizzle(k): any 8 (and any 16 aligned)
+// consecutive keys of one chunk then hit distinct 16-byte bank groups, for
+// both 128- and 256-byte bank rows.  Invalid pages use a buffer descriptor of
+// zero length, which makes every load return zeros.
+constexpr int kStages = 4;
+constexpr int kDmaPerPage = 3;  // per wave: two 1 KiB key chunks + 64 bytes of scales
+
+__device__ __forceinline__ int key_swizzle(int k) { return (k ^ (k >> 3)) & 7; }
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor over one native page (stride 0, 32-bit dwords).
+__device__ __forceinline__ i32x4 page_rsrc(const uint8_t* kv, int32_t page) {
+    const uint64_t base = reinterpret_cast<uint64_t>(kv + (int64_t)max(page, 0) * V1_PAGE_BYTES);
+    return i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)(base >> 32) & 0xffff, page >= 0 ? V1_PAGE_BYTES : 0,
+                 0x00020000};
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>((lds_ptr)(const_cast<void*>(p)));
+}
+
+// Buffer loads whose data goes to LDS at M0 + 16 (or 4) * lane.  Issued as
+// inline assembly so that the compiler keeps no bookkeeping of its own for
+// them: every wait on them is the explicit one before the page barrier.
+// The descriptor and LDS address are wave-uniform; readfirstlane pins them
+// to scalar registers.  No other code in these kernels uses M0.
+__device__ __forceinline__ i32x4 uniform(const i32x4& v) {
+    return i32x4{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                 __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
+}
+__device__ __forceinline__ void dma16(const i32x4& rs, int32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :: "v"(voff), "s"(uniform(rs)), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const i32x4& rs, int32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+                 :: "v"(voff), "s"(uniform(rs)), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+
+// Waits until this wave has at most `pending` page loads in flight (so the
+// older page has landed), drains its LDS traffic, then joins the work-group
+// barrier.  The memory clobber keeps the compiler from moving LDS accesses
+// across it; no fence is used, as a fence would drain every load.
+#define V1_PAGE_BARRIER(pending) \
+    asm volatile("s_waitcnt vmcnt(" #pending ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
 template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][kPageLds];
-    const int t = threadIdx.x, l = __lane_id(), wv = t / kWave;
+    __shared__ __attribute__((aligned(16))) uint8_t st0[V1_PAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t st1[V1_PAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t st2[V1_PAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t st3[V1_PAGE_BYTES];
+    __shared__ float olds[kQueriesPerGroup][kChunkPages][64];
+    const int l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int64_t row0 = (int64_t)blockIdx.y * kQueriesPerGroup;
     const int32_t chunk0 = blockIdx.x * kChunkPages;
 
+    // lane q (mod 8) holds the clamped length of query row0 + q: one load
+    int32_t lane_ctx;
+    {
+        const int64_t r = row0 + (l & (kQueriesPerGroup - 1));
+        const int32_t c = min(p.ctx[min(r, (int64_t)p.rows - 1)], p.max_context_len);
+        lane_ctx = r < p.rows ? c : 0;
+    }
     int32_t ctx[kQueriesPerWave];
     int32_t max_ctx = 0;
-    for (int q = 0; q < kQueriesPerGroup; ++q) {
-        const int64_t r = row0 + q;
-        if (r < p.rows) max_ctx = max(max_ctx, min(p.ctx[r], p.max_context_len));
-    }
 #pragma unroll
-    for (int q = 0; q < kQueriesPerWave; ++q) {
-        const int64_t r = row0 + wv * kQueriesPerWave + q;
-        ctx[q] = r < p.rows ? min(p.ctx[r], p.max_context_len) : 0;
-    }
+    for (int q = 0; q < kQueriesPerGroup; ++q) max_ctx = max(max_ctx, __builtin_amdgcn_readlane(lane_ctx, q));
+#pragma unroll
+    for (int q = 0; q < kQueriesPerWave; ++q) ctx[q] = __builtin_amdgcn_readlane(lane_ctx, wv * kQueriesPerWave + q);
     const int32_t npages = max(0, min(kChunkPages, (max_ctx + 63) / 64 - chunk0));
     if (npages == 0) {
         if (p.clean) {
@@ -238,81 +309,86 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         }
         return;
     }
+    // lane i < npages holds the pool page of chunk page i (-1: invalid)
+    int32_t lane_page = page_of(p, row0, chunk0 + (l & (kChunkPages - 1)));
+    lane_page = l < npages ? lane_page : -1;
 
+    // per-lane load offsets (into the page) of this wave's three loads
+    int32_t voff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int s = (2 * wv + i) * 64 + l;  // 16-byte LDS slot
+        const int key = s >> 3;
+        voff[i] = key * 128 + (((s & 7) ^ key_swizzle(key & 15)) << 4);
+    }
+    const int32_t soff = 8192 + 64 * wv + 4 * l;
+    auto issue = [&](uint8_t* buf, int32_t pg) {
+        const int32_t page = pg < npages ? __builtin_amdgcn_readlane(lane_page, pg) : -1;
+        const i32x4 rs = page_rsrc(p.kv, page);
+        const uint32_t base = lds_addr(buf);
+        dma16(rs, voff[0], base + (2 * wv) * 1024);
+        dma16(rs, voff[1], base + (2 * wv + 1) * 1024);
+        if (l < 16) dma4(rs, soff, base + 8192 + 64 * wv);
+    };
+    issue(st0, 0);
+    issue(st1, 1);
+    issue(st2, 2);
+    issue(st3, 3);
+
+    // Query fragments, weights and linear-term coefficients.  Rows past the
+    // end read the last row (their logits are never stored).
     v8i a[kQueriesPerWave][HB];
     float w[kQueriesPerWave][HB][4];
+    float coef[kQueriesPerWave][4];
+    v8i alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int q = 0; q < kQueriesPerWave; ++q) {
         const int64_t r = row0 + wv * kQueriesPerWave + q;
         load_q<HB>(p, r, a[q]);
-        load_w<HB>(p, r, w[q]);
+        const uint8_t* rec = p.pieces + min(r, (int64_t)p.rows - 1) * kPieceRowBytes;
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            const v4f x = *reinterpret_cast<const v4f*>(rec + kRecWeights + (hb * 16 + 4 * (l >> 4)) * 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[q][hb][i] = x[i];
+        }
+        if (RELU) {
+            // result row 4*(l/16)+i holds piece (row & 7) of query (row >> 3)
+            const v4f x = *reinterpret_cast<const v4f*>(rec + kRecScales + 16 * ((l >> 4) & 1));
+            const float mine = (l >> 5) == q ? 1.f : 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) coef[q][i] = x[i] * mine;
+        }
     }
-    // ReLU path: linear-term fragment (rows 0-7: query 0's pieces, 8-15: query 1's)
-    // and per-lane coefficients of the rows this lane holds in the MFMA result.
-    v8i alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-    float coef[kQueriesPerWave][4];
     if (RELU) {
-        const int64_t rq = row0 + wv * kQueriesPerWave + ((l & 15) >> 3);
-        if (rq < p.rows) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(p.pieces + rq * kPieceRowBytes + (l & 7) * 128 + 32 * (l >> 4));
-            const u32x4 x = src[0], y = src[1];
-            alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
-        }
-#pragma unroll
-        for (int q = 0; q < kQueriesPerWave; ++q) {
-            const int64_t r = row0 + wv * kQueriesPerWave + q;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int mrow = 4 * (l >> 4) + i;
-                coef[q][i] = ((mrow >> 3) == q && r < p.rows)
-                                 ? 0.5f * reinterpret_cast<const float*>(p.pieces + r * kPieceRowBytes + kPieces * 128)[mrow & 7]
-                                 : 0.f;
-            }
-#pragma unroll
-            for (int hb = 0; hb < HB; ++hb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) w[q][hb][i] *= 0.5f;
-        }
+        // MFMA row block: rows 0-7 are query 0's pieces, rows 8-15 query 1's
+        const int64_t rq = min(row0 + wv * kQueriesPerWave + ((l & 15) >> 3), (int64_t)p.rows - 1);
+        const u32x4* src = reinterpret_cast<const u32x4*>(p.pieces + rq * kPieceRowBytes + (l & 7) * 128 + 32 * (l >> 4));
+        const u32x4 x = src[0], y = src[1];
+        alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
     }
 
-    // staging: thread t moves 32 key bytes (key t/4, part t%4); t < 64 one
-    // scale.  A page is fetched into registers three iterations before it is
-    // computed and written to LDS one iteration before.
-    const int skey = t >> 2, spart = t & 3;
-    struct Stage {
-        u32x4 a, b;
-        float s;
-    };
-    auto fetch = [&](int32_t pg) {
-        Stage st{u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, 0.f};
-        const int32_t page = pg < npages ? page_of(p, row0, chunk0 + pg) : -1;
-        if (page >= 0) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(p.kv + (int64_t)page * V1_PAGE_BYTES + skey * 128 + spart * 32);
-            st.a = src[0];
-            st.b = src[1];
-            if (t < 64) st.s = reinterpret_cast<const float*>(p.kv + (int64_t)page * V1_PAGE_BYTES + 8192)[t];
-        }
-        return st;
-    };
-    auto stash = [&](int buf, const Stage& st) {
-        u32x4* dst = reinterpret_cast<u32x4*>(&lds[buf][skey * kKeyPitch + spart * 32]);
-        dst[0] = st.a;
-        dst[1] = st.b;
-        if (t < 64) reinterpret_cast<float*>(&lds[buf][64 * kKeyPitch])[t] = st.s;
-    };
-
-    // Three fixed stage registers (no copies between them, so the compiler's
-    // memory waits cover exactly the page being written to LDS): the page
-    // computed in one step was fetched three steps earlier.
-    auto step = [&](int32_t pg, Stage& sreg) {
-        const int buf = pg & 1;
+    // B fragment of key block kb: key kb*16 + l%16, chunks 2*(l/16) and +1;
+    // plus the scale of key l
+    const int swz = key_swizzle(l & 15);
+    const int boff0 = (l & 15) * 128 + (((2 * (l >> 4)) ^ swz) << 4);
+    const int boff1 = (l & 15) * 128 + (((2 * (l >> 4) + 1) ^ swz) << 4);
+    struct Frag {
         v8i b[4];
+        float scale;
+    };
+    auto load_frag = [&](const uint8_t* buf, Frag& f) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(&lds[buf][(kb * 16 + (l & 15)) * kKeyPitch + 32 * (l >> 4)]);
-            const u32x4 x = src[0], y = src[1];
-            b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+            const u32x4 x = *reinterpret_cast<const u32x4*>(buf + kb * 2048 + boff0);
+            const u32x4 y = *reinterpret_cast<const u32x4*>(buf + kb * 2048 + boff1);
+            f.b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
         }
+        f.scale = reinterpret_cast<const float*>(buf + 8192)[l];
+    };
+
+    auto compute = [&](const Frag& f, int32_t pg) {
+        const v8i (&b)[4] = f.b;
         float out[kQueriesPerWave];
         if (RELU) {
             float part[kQueriesPerWave][4];
@@ -343,28 +419,44 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
                 out[q] = reduce_scatter4(part);
             }
         }
-        const float scale = reinterpret_cast<const float*>(&lds[buf][64 * kKeyPitch])[l];
-        const int32_t j = (chunk0 + pg) * 64 + l;
 #pragma unroll
-        for (int q = 0; q < kQueriesPerWave; ++q)
-            store_logit(p, row0 + wv * kQueriesPerWave + q, j, ctx[q], out[q] * scale);
-        if (pg + 1 < npages) stash(buf ^ 1, sreg);
-        sreg = fetch(pg + 4);
-        __syncthreads();
+        for (int q = 0; q < kQueriesPerWave; ++q) olds[wv * kQueriesPerWave + q][pg][l] = out[q] * f.scale;
     };
-    stash(0, fetch(0));
-    Stage sa = fetch(1), sb = fetch(2), sc = fetch(3);
-    __syncthreads();
-    for (int32_t pg = 0; pg < npages; pg += 3) {
-        step(pg, sa);
-        if (pg + 1 < npages) step(pg + 1, sb);
-        if (pg + 2 < npages) step(pg + 2, sc);
+
+    // Step pg (page pg's fragments already in registers): page pg+1 is
+    // complete once only pages pg+2 and pg+3 are still in flight.  After the
+    // barrier every wave has read page pg out of LDS, so its buffer receives
+    // page pg+4; then page pg+1's fragments are read while page pg is
+    // computed.  Loads past the chunk read zeros, so every wave always has
+    // the same number of loads in flight.
+    static_assert(kStages == 4 && kDmaPerPage * (kStages - 2) == 6, "barrier wait count");
+    Frag fa, fb;
+    // Compiler-visible full wait: the query fragments, weights and records
+    // loaded above are complete before the loop, so no wait for them is
+    // placed inside it.  (It also covers the first pages.)
+    __builtin_amdgcn_s_waitcnt(0);
+    V1_PAGE_BARRIER(0);
+    load_frag(st0, fa);
+    auto step = [&](int32_t pg, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn) {
+        V1_PAGE_BARRIER(6);
+        issue(cur, pg + kStages);
+        load_frag(next, fn);
+        if (pg < npages) compute(fc, pg);
+    };
+    for (int32_t pg = 0; pg < npages; pg += kStages) {
+        step(pg, st0, st1, fa, fb);
+        step(pg + 1, st1, st2, fb, fa);
+        step(pg + 2, st2, st3, fa, fb);
+        step(pg + 3, st3, st0, fb, fa);
     }
-    if (p.clean) {
-        // columns of this chunk past the last staged page
-        for (int q = 0; q < kQueriesPerWave; ++q) {
-            const int64_t r = row0 + wv * kQueriesPerWave + q;
-            for (int j = (chunk0 + npages) * 64 + l; j < (chunk0 + kChunkPages) * 64; j += kWave) store_logit(p, r, j, ctx[q], 0.f);
+    V1_PAGE_BARRIER(0);
+
+#pragma unroll
+    for (int q = 0; q < kQueriesPerWave; ++q) {
+        const int64_t r = row0 + wv * kQueriesPerWave + q;
+        for (int pg = 0; pg < kChunkPages; ++pg) {
+            const int32_t j = (chunk0 + pg) * 64 + l;
+            store_logit(p, r, j, ctx[q], pg < npages ? olds[wv * kQueriesPerWave + q][pg][l] : 0.f);
         }
     }
 }
@@ -463,15 +555,13 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
     const uint32_t chunks = (uint32_t)cdiv(cdiv(a->max_context_len, 64), kChunkPages);
     hipStream_t st = as_stream(stream);
     if (a->block_table_stride == 0) {
-        if (a->relu) {
-            V1_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= (int64_t)a->rows * kPieceRowBytes,
-                       "score: workspace of %lld bytes required", (long long)((int64_t)a->rows * kPieceRowBytes));
-            p.pieces = static_cast<const uint8_t*>(a->workspace);
-            hipLaunchKernelGGL(score_prep, dim3((uint32_t)cdiv(a->rows, 4)), dim3(256), 0, st, a->q, a->weights, a->rows,
-                               a->heads, static_cast<uint8_t*>(a->workspace));
-            const int rc = V1_LAUNCHED("score_prep");
-            if (rc != V1_OK) return rc;
-        }
+        V1_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= (int64_t)a->rows * kPieceRowBytes,
+                   "score: workspace of %lld bytes required", (long long)((int64_t)a->rows * kPieceRowBytes));
+        p.pieces = static_cast<const uint8_t*>(a->workspace);
+        hipLaunchKernelGGL(score_prep, dim3((uint32_t)cdiv(a->rows, 4)), dim3(256), 0, st, a->q, a->weights, a->rows,
+                           a->heads, a->relu, static_cast<uint8_t*>(a->workspace));
+        const int rc = V1_LAUNCHED("score_prep");
+        if (rc != V1_OK) return rc;
         const dim3 grid(chunks, (uint32_t)cdiv(a->rows, kQueriesPerGroup));
         launch_hb<Shared>(hb, a->relu != 0, grid, st, p);
         return V1_LAUNCHED("score_shared");
