@@ -24,6 +24,27 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
+# HBM traffic per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE on this
+# workload (calibrated against a plain copy), kept with the kernel trace.
+TRAFFIC_PROFILE = ROOT / "profiles" / "prefill_chunk_4096x32k.md"
+STAGE_KERNELS = {"score": ("score_prep", "score_shared"), "topk": ("transform_rows",), "gather": ("gather_rows16",)}
+
+
+def measured_traffic(stage):
+    """HBM bytes per step of a stage's kernels from the committed counter
+    summary, or None when the summary does not list them."""
+    if not TRAFFIC_PROFILE.exists():
+        return None
+    per_kernel = {}
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
+        if len(cells) == 6 and cells[0] and not cells[0].startswith("-"):
+            try:
+                per_kernel[cells[0].split("<")[0]] = float(cells[5])
+            except ValueError:
+                continue
+    vals = [per_kernel.get(k) for k in STAGE_KERNELS[stage]]
+    return None if any(v is None for v in vals) else sum(vals)
 
 
 def parse():
@@ -160,7 +181,7 @@ def main():
                    "global_batch": rows, "seq_len": ctx, "parallelism": "single GPU"},
         "stages": stage_info,
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": None},
+                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(dom)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
