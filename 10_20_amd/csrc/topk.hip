@@ -8,10 +8,11 @@
 // candidates take every candidate (sglang/kernels/jit/csrc/deepseek_v4/
 // topk_v2.cuh:136-143).
 //
-// Design: one 1024-thread work-group selects over up to 32768 positions and
-// keeps little state per thread, so two work-groups share a CU and one row's
-// HBM stream overlaps another's selection.
-//  1. 4096 sampled keys give a pivot that about 1.5*T of the row's keys exceed.
+// Design: one 512-thread work-group selects over up to 32768 positions with
+// under 40 KiB of LDS, so four work-groups (rows) share a CU and the HBM
+// streams of some rows overlap the LDS selection of others.
+//  1. 2048 keys sampled in 256 runs of 8 (a few percent of the row's cache
+//     lines) give a pivot that about 1.3*T of the row's keys exceed.
 //  2. One streaming pass, wave-independent (no barriers), sends every key at or
 //     above the pivot to an LDS candidate buffer (wave-aggregated slot
 //     allocation) and keeps the row's key statistics.
@@ -20,7 +21,8 @@
 //     the number r of tau-valued keys to take.
 //  4. Position bitmaps of "> tau" and "== tau" plus a block prefix of their
 //     popcounts give each winner its output slot: (> tau before it) +
-//     min(== tau before it, r).  No sort is needed and the order is exact.
+//     min(== tau before it, r).  No sort is needed and the order is exact;
+//     each winner is written straight to its output slot.
 // When the pivot misses (fewer than T or more than kCandMax keys at or above
 // it) the same steps run on the whole row, streamed again from cache.
 // Rows longer than 32768 columns are cut into 32768-column segments whose
@@ -30,28 +32,31 @@
 namespace v1 {
 namespace {
 
-constexpr int kBlock = 1024;
-constexpr int kWaves = kBlock / kWave;  // 16
+constexpr int kBlock = 512;
+constexpr int kWaves = kBlock / kWave;  // 8
 constexpr int kSpan = 32768;            // positions one work-group selects over
-constexpr int kWords = kSpan / 32;      // position bitmap words, one per thread
-constexpr int kCandMax = 5120;
-constexpr int kCandPerThread = kCandMax / kBlock;  // 5
+constexpr int kWords = kSpan / 32;      // position bitmap words
+constexpr int kDigitBits = 11;          // radix digit width
+constexpr int kHist = 1 << kDigitBits;  // histogram bins, 4 per thread
+constexpr int kCandMax = 3584;
+constexpr int kCandPerThread = kCandMax / kBlock;  // 7
+constexpr int kSampleRuns = 256;                   // pivot sample: runs of 8 keys
 constexpr uint32_t kNegInfKey = 0x007fffffu;
-constexpr uint32_t kInfBit = 0x80000000u;
+static_assert(kHist == 4 * kBlock && kWords % kBlock == 0 && kCandMax % kBlock == 0, "work split");
+static_assert(kSampleRuns * 8 == 4 * kBlock, "two threads per sample run");
 
 struct SelSmem {
-    uint32_t hist[4096];       // radix histograms; bitmap word prefixes
+    uint32_t hist[kHist];      // radix histograms; bitmap word prefixes
     uint32_t cand_key[kCandMax];
     uint16_t cand_pos[kCandMax];
     uint32_t gt_bits[kWords];  // positions with key > tau
     uint32_t eq_bits[kWords];  // positions with key == tau
-    int32_t sel[V1_MAX_TOPK];  // chosen positions (| kInfBit when the score is -inf)
-    uint32_t selkey[V1_MAX_TOPK];
     uint32_t red[4 * kWaves];
     uint32_t bc[4];
     uint32_t ncand;
     int32_t maskpage[kSpan / 64];  // V1 mask: page per selected rank, -1 when unmasked
 };
+static_assert(sizeof(SelSmem) <= 40 * 1024, "four work-groups per CU");
 
 __device__ __forceinline__ uint32_t readlane(uint32_t v, int lane) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
@@ -103,15 +108,15 @@ __device__ __forceinline__ void key_stats(uint32_t k, uint32_t& mx, uint32_t& mn
     n += real ? 1u : 0u;
 }
 
-// Descending scan of hist[0..4096): the bin holding the `rank`-th largest
+// Descending scan of hist[0..kHist): the bin holding the `rank`-th largest
 // counted key, and the count above it.  Ends with a barrier.
 __device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& bin, uint32_t& above) {
     const int t = threadIdx.x;
     uint32_t h[4];
     uint32_t local = 0;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {  // thread t owns bins 4095-4t .. 4092-4t
-        h[b] = sm.hist[4095 - (4 * t + b)];
+    for (int b = 0; b < 4; ++b) {  // thread t owns bins kHist-1-4t .. kHist-4-4t
+        h[b] = sm.hist[kHist - 1 - (4 * t + b)];
         local += h[b];
     }
     const uint32_t incl = block_incl_scan(local, sm);
@@ -121,7 +126,7 @@ __device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& b
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             if (acc + h[b] >= rank) {
-                sm.bc[0] = 4095 - (4 * t + b);
+                sm.bc[0] = kHist - 1 - (4 * t + b);
                 sm.bc[1] = acc;
                 break;
             }
@@ -150,7 +155,7 @@ struct Radix {
         remaining = T;
         shift = hb + 1;
     }
-    __device__ __forceinline__ int bits() const { return shift < 12 ? shift : 12; }
+    __device__ __forceinline__ int bits() const { return shift < kDigitBits ? shift : kDigitBits; }
     __device__ __forceinline__ bool counts(uint32_t k, bool real_only) const {
         return (k & pmask) == prefix && (!real_only || k > kNegInfKey);
     }
@@ -174,8 +179,11 @@ struct Radix {
 // then visits each marked item again and writes it to its slot.
 struct Ranker {
     __device__ __forceinline__ static void clear(SelSmem& sm) {
-        sm.gt_bits[threadIdx.x] = 0;
-        sm.eq_bits[threadIdx.x] = 0;
+#pragma unroll
+        for (int i = 0; i < kWords / kBlock; ++i) {
+            sm.gt_bits[threadIdx.x + i * kBlock] = 0;
+            sm.eq_bits[threadIdx.x + i * kBlock] = 0;
+        }
     }
     __device__ __forceinline__ static void mark(SelSmem& sm, uint32_t pos, bool gt, bool eq) {
         if (gt) atomicOr(&sm.gt_bits[pos >> 5], 1u << (pos & 31));
@@ -214,22 +222,20 @@ struct Ranker {
     }
 };
 
-__device__ __forceinline__ void put(SelSmem& sm, int32_t at, uint32_t pos, uint32_t k) {
-    sm.sel[at] = (int32_t)pos | (k == kNegInfKey ? (int32_t)kInfBit : 0);
-    sm.selkey[at] = k;
-}
-
 // Selects the T largest keys of positions [0, n) of `src` (n > T, n <= kSpan;
-// ties toward the lower position) into sm.sel / sm.selkey [0, T), ascending by
-// position.  src.load4(p, k) returns the keys of positions p..p+3 (p % 4 == 0),
-// key 0 past n.  Ends with a barrier.
-template <class Src>
-__device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm) {
+// ties toward the lower position).  emit(slot[], position[], key[]) takes a
+// thread's batch of items (arrays of one length; slot -1 = not selected):
+// every slot in [0, T) is delivered exactly once, the slots ascending by
+// position.  Batches let the emitter issue all of a thread's output loads
+// before its stores.  src.load4(p, k) returns the keys of positions p..p+3
+// (p % 4 == 0), key 0 past n.  Ends with a barrier.
+template <class Src, class Emit>
+__device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emit& emit) {
     const int t = threadIdx.x, w = t / kWave, lane = __lane_id();
     const int32_t n = src.n;
-    // 1. pivot from 4096 sampled keys
+    // 1. pivot from 2048 sampled keys: threads 2r, 2r+1 read run r of 8 keys
     uint32_t sk[4];
-    src.load4((int32_t)(((int64_t)t * n / kBlock) & ~3ll), sk);
+    src.load4((int32_t)((((int64_t)(t >> 1) * n / kSampleRuns) & ~7ll) + 4 * (t & 1)), sk);
     uint32_t smax = 0, smin = 0xffffffffu, scnt = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) key_stats(sk[e], smax, smin, scnt);
@@ -241,17 +247,40 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm) {
     } else if (scnt > 0) {
         Radix rx;
         rx.start(smax, smin, 1);
-        const int lo = rx.shift > 12 ? rx.shift - 12 : 0;
+        const int lo = rx.shift > kDigitBits ? rx.shift - kDigitBits : 0;
         clear_hist(sm);
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            if (sk[e] > kNegInfKey) atomicAdd(&sm.hist[(sk[e] >> lo) & 0xfffu], 1u);
+            if (sk[e] > kNegInfKey) atomicAdd(&sm.hist[(sk[e] >> lo) & (kHist - 1u)], 1u);
         __syncthreads();
-        const uint64_t want = (uint64_t)scnt * T * 3 / (2ull * (uint64_t)n) + 16ull;
+        const uint32_t want = (uint32_t)min((uint64_t)scnt, (uint64_t)scnt * T * 13 / (10ull * (uint64_t)n) + 16ull);
         uint32_t bin, above;
-        find_bin((uint32_t)min((uint64_t)scnt, want), sm, bin, above);
-        pivot = max(rx.prefix | (bin << lo), kNegInfKey + 1);
+        find_bin(want, sm, bin, above);
+        // Expected candidates with the pivot at the bin's lower edge (every
+        // sample of the bin passes) or just above the bin (none passes).
+        const uint32_t inbin = sm.hist[bin];
+        const uint64_t est_lo = (uint64_t)(above + inbin) * n / scnt, est_hi = (uint64_t)above * n / scnt;
+        if (est_lo <= (uint64_t)kCandMax * 7 / 8 || lo == 0) {
+            pivot = rx.prefix | (bin << lo);
+        } else if (est_hi >= (uint64_t)T * 9 / 8 && bin + 1 < (uint32_t)kHist) {
+            pivot = rx.prefix | ((bin + 1) << lo);
+        } else {
+            // refine inside the bin on the next digit
+            const int lo2 = lo > kDigitBits ? lo - kDigitBits : 0;
+            __syncthreads();
+            clear_hist(sm);
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (sk[e] > kNegInfKey && ((sk[e] >> lo) & (kHist - 1u)) == bin && (sk[e] & rx.pmask) == rx.prefix)
+                    atomicAdd(&sm.hist[(sk[e] >> lo2) & ((1u << (lo - lo2)) - 1u)], 1u);
+            __syncthreads();
+            uint32_t bin2, above2;
+            find_bin(want - above, sm, bin2, above2);
+            pivot = rx.prefix | (bin << lo) | (bin2 << lo2);
+        }
+        pivot = max(pivot, kNegInfKey + 1);
     }
     // 2. stream: candidates >= pivot into LDS, row statistics on the side.
     //    Each wave keeps kBatch 1 KB loads in flight.
@@ -302,7 +331,7 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm) {
     Ranker::clear(sm);
     __syncthreads();
     if (ncand >= T && ncand <= (uint32_t)kCandMax) {
-        // 3. radix select on the candidates (5 per thread, slot q = i*kBlock + t)
+        // 3. radix select on the candidates (kCandPerThread per thread, slot q = i*kBlock + t)
         uint32_t ck[kCandPerThread];
         uint32_t cmax = 0, cmin = 0xffffffffu, cc = 0;
 #pragma unroll
@@ -336,15 +365,15 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm) {
         }
         __syncthreads();
         Ranker::scan(sm);
+        int32_t at[kCandPerThread];
+        uint32_t cp[kCandPerThread];
 #pragma unroll
         for (int i = 0; i < kCandPerThread; ++i) {
             const uint32_t q = i * kBlock + t;
-            if (q < ncand && ck[i] >= tau) {
-                const uint32_t pos = sm.cand_pos[q];
-                const int32_t at = Ranker::slot(sm, pos, ck[i] > tau, r);
-                if (at >= 0) put(sm, at, pos, ck[i]);
-            }
+            cp[i] = q < ncand ? (uint32_t)sm.cand_pos[q] : 0u;
+            at[i] = (q < ncand && ck[i] >= tau) ? Ranker::slot(sm, cp[i], ck[i] > tau, r) : -1;
         }
+        emit(at, cp, ck);
         __syncthreads();
         return;
     }
@@ -408,15 +437,15 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm) {
     Ranker::scan(sm);
     for (int32_t s = w; s < steps; s += kWaves) {
         const int32_t p = s * 256 + 4 * lane;
-        uint32_t k[4];
+        uint32_t k[4], pp[4];
+        int32_t at[4];
         src.load4(p, k);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            if (p + e < n && k[e] >= tau) {
-                const int32_t at = Ranker::slot(sm, p + e, k[e] > tau, r);
-                if (at >= 0) put(sm, at, p + e, k[e]);
-            }
+            pp[e] = (uint32_t)(p + e);
+            at[e] = (p + e < n && k[e] >= tau) ? Ranker::slot(sm, p + e, k[e] > tau, r) : -1;
         }
+        emit(at, pp, k);
     }
     __syncthreads();
 }
@@ -582,6 +611,25 @@ __device__ __forceinline__ void transform_emit(const TransformParams& p, int64_t
     if (p.raw_indices) p.raw_indices[dst] = raw;
 }
 
+// A batch of selected items: every table entry is loaded (from a clamped
+// index) before any store, so a thread's lookups overlap.  The restrict
+// parameters state that the table and the outputs do not alias.
+template <int N>
+__device__ __forceinline__ void transform_emit_batch(const int32_t* __restrict__ table, int32_t table_cols, int bits,
+                                                     int32_t* __restrict__ indices, int32_t* __restrict__ raws,
+                                                     const int32_t (&at)[N], const int32_t (&raw)[N]) {
+    int32_t entry[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) entry[i] = table_cols > 0 ? table[min(max(raw[i] >> bits, 0), table_cols - 1)] : 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if (at[i] < 0) continue;
+        const bool mapped = raw[i] >= 0 && (raw[i] >> bits) < table_cols;
+        indices[at[i]] = mapped ? (entry[i] << bits) | (raw[i] & ((1 << bits) - 1)) : -1;
+        if (raws) raws[at[i]] = raw[i];
+    }
+}
+
 // A V1 row with the sink/tail mask applied on the fly: positions of masked
 // pages (sm.maskpage) whose member lies outside [sink, tail) read as -inf.
 struct V1Src {
@@ -665,11 +713,11 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_rows(V1Params p) {
             v1_emit(p, row, ri, tx, tx < L ? tx : -1, inf);
         }
     } else {
-        select_stream(src, (uint32_t)T, sm);
-        for (int tx = threadIdx.x; tx < T; tx += kBlock) {
-            const int32_t s = sm.sel[tx];
-            v1_emit(p, row, ri, tx, s & 0x7fffffff, (s & (int32_t)kInfBit) != 0);
-        }
+        select_stream(src, (uint32_t)T, sm, [&](const auto& at, const auto& pos, const auto& key) {
+#pragma unroll
+            for (int i = 0; i < (int)(sizeof(at) / sizeof(at[0])); ++i)
+                if (at[i] >= 0) v1_emit(p, row, ri, at[i], (int32_t)pos[i], key[i] == kNegInfKey);
+        });
     }
     v1_pad_expansion(p, row);
 }
@@ -685,8 +733,15 @@ __global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
     }
     const float* rp = p.scores + row * p.score_stride;
     const RowSrc src{rp, L, (reinterpret_cast<uintptr_t>(rp) & 15) == 0};
-    select_stream(src, (uint32_t)T, sm);
-    for (int tx = threadIdx.x; tx < T; tx += kBlock) transform_emit(p, row, tx, sm.sel[tx] & 0x7fffffff);
+    select_stream(src, (uint32_t)T, sm, [&](const auto& at, const auto& pos, const auto&) {
+        constexpr int N = sizeof(at) / sizeof(at[0]);
+        int32_t raw[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) raw[i] = (int32_t)pos[i];
+        transform_emit_batch<N>(p.page_table + row * p.page_table_stride, p.page_table_cols, p.page_bits,
+                                p.page_indices + row * p.topk, p.raw_indices ? p.raw_indices + row * p.topk : nullptr,
+                                at, raw);
+    });
 }
 
 // ------------------------------------------------------- segmented rows
@@ -739,11 +794,14 @@ __device__ __forceinline__ void segment_select(const Src& src, int32_t lo, int32
         if (threadIdx.x == 0) ws.count[row * ws.nseg + s] = n;
         return;
     }
-    select_stream(src, (uint32_t)T, sm);
-    for (int tx = threadIdx.x; tx < T; tx += kBlock) {
-        ws.keys[at + tx] = max(sm.selkey[tx], 1u);
-        ws.pos[at + tx] = lo + (sm.sel[tx] & 0x7fffffff);
-    }
+    select_stream(src, (uint32_t)T, sm, [&](const auto& slot, const auto& pos, const auto& key) {
+#pragma unroll
+        for (int i = 0; i < (int)(sizeof(slot) / sizeof(slot[0])); ++i) {
+            if (slot[i] < 0) continue;
+            ws.keys[at + slot[i]] = max(key[i], 1u);
+            ws.pos[at + slot[i]] = lo + (int32_t)pos[i];
+        }
+    });
     if (threadIdx.x == 0) ws.count[row * ws.nseg + s] = T;
 }
 
@@ -808,12 +866,12 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_merge(V1Params p, Workspace
             v1_emit(p, row, ri, tx, ok ? tx : -1, inf);
         }
     } else {
-        select_stream(cand_source(ws, row), (uint32_t)T, sm);
         const int32_t* pos = ws.pos + ws.at(row, 0);
-        for (int tx = threadIdx.x; tx < T; tx += kBlock) {
-            const int32_t q = sm.sel[tx];
-            v1_emit(p, row, ri, tx, pos[q & 0x7fffffff], (q & (int32_t)kInfBit) != 0);
-        }
+        select_stream(cand_source(ws, row), (uint32_t)T, sm, [&](const auto& at, const auto& q, const auto& key) {
+#pragma unroll
+            for (int i = 0; i < (int)(sizeof(at) / sizeof(at[0])); ++i)
+                if (at[i] >= 0) v1_emit(p, row, ri, at[i], pos[q[i]], key[i] == kNegInfKey);
+        });
     }
     v1_pad_expansion(p, row);
 }
@@ -827,9 +885,17 @@ __global__ __launch_bounds__(kBlock, 8) void transform_merge(TransformParams p, 
         for (int tx = threadIdx.x; tx < T; tx += kBlock) transform_emit(p, row, tx, tx < L ? tx : -1);
         return;
     }
-    select_stream(cand_source(ws, row), (uint32_t)T, sm);
     const int32_t* pos = ws.pos + ws.at(row, 0);
-    for (int tx = threadIdx.x; tx < T; tx += kBlock) transform_emit(p, row, tx, pos[sm.sel[tx] & 0x7fffffff]);
+    const int32_t nq = ws.nseg * T;
+    select_stream(cand_source(ws, row), (uint32_t)T, sm, [&](const auto& at, const auto& q, const auto&) {
+        constexpr int N = sizeof(at) / sizeof(at[0]);
+        int32_t raw[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) raw[i] = pos[min((int32_t)q[i], nq - 1)];
+        transform_emit_batch<N>(p.page_table + row * p.page_table_stride, p.page_table_cols, p.page_bits,
+                                p.page_indices + row * p.topk, p.raw_indices ? p.raw_indices + row * p.topk : nullptr,
+                                at, raw);
+    });
 }
 
 // ------------------------------------------------------ unfused mask/map
