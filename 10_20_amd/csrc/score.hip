@@ -107,11 +107,22 @@ __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float*
     if (row >= rows) return;
     // lane l owns dims 2l, 2l+1
     float a0 = 0.f, a1 = 0.f;
-    for (int h = 0; h < heads; ++h) {
-        const float wh = w[row * heads + h];
-        const uint32_t b = *reinterpret_cast<const uint16_t*>(q + (row * heads + h) * 128 + 2 * l);
-        a0 = fmaf(wh, e4m3_value(b & 0xff), a0);
-        a1 = fmaf(wh, e4m3_value(b >> 8), a1);
+    for (int h0 = 0; h0 < heads; h0 += 16) {
+        // 16 heads' loads in flight (indices clamped, weights of missing heads zeroed)
+        float wh[16];
+        uint32_t b[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int h = min(h0 + j, heads - 1);
+            const float v = w[row * heads + h];
+            wh[j] = (h0 + j < heads) ? v : 0.f;
+            b[j] = *reinterpret_cast<const uint16_t*>(q + (row * heads + h) * 128 + 2 * l);
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            a0 = fmaf(wh[j], e4m3_value(b[j] & 0xff), a0);
+            a1 = fmaf(wh[j], e4m3_value(b[j] >> 8), a1);
+        }
     }
     uint8_t* dst = out + row * kPieceRowBytes;
     for (int pc = 0; pc < kPieces; ++pc) {
@@ -286,55 +297,17 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     const int64_t row0 = (int64_t)blockIdx.y * kQueriesPerGroup;
     const int32_t chunk0 = blockIdx.x * kChunkPages;
 
-    // lane q (mod 8) holds the clamped length of query row0 + q: one load
+    // The independent loads of the prologue are all issued before the first
+    // wait: query lengths (lane q mod 8: query row0 + q), the chunk's page
+    // table entries (lane i mod 16: chunk page i), query fragments, weights
+    // and records.
     int32_t lane_ctx;
     {
         const int64_t r = row0 + (l & (kQueriesPerGroup - 1));
         const int32_t c = min(p.ctx[min(r, (int64_t)p.rows - 1)], p.max_context_len);
         lane_ctx = r < p.rows ? c : 0;
     }
-    int32_t ctx[kQueriesPerWave];
-    int32_t max_ctx = 0;
-#pragma unroll
-    for (int q = 0; q < kQueriesPerGroup; ++q) max_ctx = max(max_ctx, __builtin_amdgcn_readlane(lane_ctx, q));
-#pragma unroll
-    for (int q = 0; q < kQueriesPerWave; ++q) ctx[q] = __builtin_amdgcn_readlane(lane_ctx, wv * kQueriesPerWave + q);
-    const int32_t npages = max(0, min(kChunkPages, (max_ctx + 63) / 64 - chunk0));
-    if (npages == 0) {
-        if (p.clean) {
-            for (int q = 0; q < kQueriesPerWave; ++q) {
-                const int64_t r = row0 + wv * kQueriesPerWave + q;
-                for (int j = chunk0 * 64 + l; j < (chunk0 + kChunkPages) * 64; j += kWave) store_logit(p, r, j, ctx[q], 0.f);
-            }
-        }
-        return;
-    }
-    // lane i < npages holds the pool page of chunk page i (-1: invalid)
     int32_t lane_page = page_of(p, row0, chunk0 + (l & (kChunkPages - 1)));
-    lane_page = l < npages ? lane_page : -1;
-
-    // per-lane load offsets (into the page) of this wave's three loads
-    int32_t voff[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int s = (2 * wv + i) * 64 + l;  // 16-byte LDS slot
-        const int key = s >> 3;
-        voff[i] = key * 128 + (((s & 7) ^ key_swizzle(key & 15)) << 4);
-    }
-    const int32_t soff = 8192 + 64 * wv + 4 * l;
-    auto issue = [&](uint8_t* buf, int32_t pg) {
-        const int32_t page = pg < npages ? __builtin_amdgcn_readlane(lane_page, pg) : -1;
-        const i32x4 rs = page_rsrc(p.kv, page);
-        const uint32_t base = lds_addr(buf);
-        dma16(rs, voff[0], base + (2 * wv) * 1024);
-        dma16(rs, voff[1], base + (2 * wv + 1) * 1024);
-        if (l < 16) dma4(rs, soff, base + 8192 + 64 * wv);
-    };
-    issue(st0, 0);
-    issue(st1, 1);
-    issue(st2, 2);
-    issue(st3, 3);
-
     // Query fragments, weights and linear-term coefficients.  Rows past the
     // end read the last row (their logits are never stored).
     v8i a[kQueriesPerWave][HB];
@@ -367,6 +340,48 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         const u32x4 x = src[0], y = src[1];
         alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
     }
+
+
+    int32_t ctx[kQueriesPerWave];
+    int32_t max_ctx = 0;
+#pragma unroll
+    for (int q = 0; q < kQueriesPerGroup; ++q) max_ctx = max(max_ctx, __builtin_amdgcn_readlane(lane_ctx, q));
+#pragma unroll
+    for (int q = 0; q < kQueriesPerWave; ++q) ctx[q] = __builtin_amdgcn_readlane(lane_ctx, wv * kQueriesPerWave + q);
+    const int32_t npages = max(0, min(kChunkPages, (max_ctx + 63) / 64 - chunk0));
+    if (npages == 0) {
+        if (p.clean) {
+            for (int q = 0; q < kQueriesPerWave; ++q) {
+                const int64_t r = row0 + wv * kQueriesPerWave + q;
+                for (int j = chunk0 * 64 + l; j < (chunk0 + kChunkPages) * 64; j += kWave) store_logit(p, r, j, ctx[q], 0.f);
+            }
+        }
+        return;
+    }
+    // lane i < npages holds the pool page of chunk page i (-1: invalid)
+    lane_page = l < npages ? lane_page : -1;
+
+    // per-lane load offsets (into the page) of this wave's three loads
+    int32_t voff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int s = (2 * wv + i) * 64 + l;  // 16-byte LDS slot
+        const int key = s >> 3;
+        voff[i] = key * 128 + (((s & 7) ^ key_swizzle(key & 15)) << 4);
+    }
+    const int32_t soff = 8192 + 64 * wv + 4 * l;
+    auto issue = [&](uint8_t* buf, int32_t pg) {
+        const int32_t page = pg < npages ? __builtin_amdgcn_readlane(lane_page, pg) : -1;
+        const i32x4 rs = page_rsrc(p.kv, page);
+        const uint32_t base = lds_addr(buf);
+        dma16(rs, voff[0], base + (2 * wv) * 1024);
+        dma16(rs, voff[1], base + (2 * wv + 1) * 1024);
+        if (l < 16) dma4(rs, soff, base + 8192 + 64 * wv);
+    };
+    issue(st0, 0);
+    issue(st1, 1);
+    issue(st2, 2);
+    issue(st3, 3);
 
     // B fragment of key block kb: key kb*16 + l%16, chunks 2*(l/16) and +1;
     // plus the scale of key l
@@ -451,12 +466,26 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     }
     V1_PAGE_BARRIER(0);
 
+    // Each lane writes 4 consecutive logits at a time; a group of 4 that
+    // straddles the context end or the column limit goes element by element.
+    const bool vec = (p.logits_stride & 3) == 0 && (reinterpret_cast<uintptr_t>(p.logits) & 15) == 0;
 #pragma unroll
     for (int q = 0; q < kQueriesPerWave; ++q) {
         const int64_t r = row0 + wv * kQueriesPerWave + q;
-        for (int pg = 0; pg < kChunkPages; ++pg) {
-            const int32_t j = (chunk0 + pg) * 64 + l;
-            store_logit(p, r, j, ctx[q], pg < npages ? olds[wv * kQueriesPerWave + q][pg][l] : 0.f);
+        if (r >= p.rows) continue;
+        const float* src = &olds[wv * kQueriesPerWave + q][0][0];
+#pragma unroll
+        for (int i = 0; i < kChunkPages * 64 / (4 * kWave); ++i) {
+            const int f = i * kWave + l;  // float4 index within the chunk
+            const int32_t j0 = chunk0 * 64 + 4 * f;
+            v4f v = v4f{0.f, 0.f, 0.f, 0.f};
+            if ((4 * f) / 64 < npages) v = *reinterpret_cast<const v4f*>(src + 4 * f);
+            if (vec && j0 + 3 < ctx[q]) {
+                *reinterpret_cast<v4f*>(p.logits + r * p.logits_stride + j0) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) store_logit(p, r, j0 + e, ctx[q], v[e]);
+            }
         }
     }
 }
