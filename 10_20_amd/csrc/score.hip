@@ -19,6 +19,8 @@
 // key row swizzled so that the 16-byte fragment reads are bank-conflict free)
 // and reused by 8 queries x 64 heads.  Rows with their own tables (decode) run one
 // query per work-group, each wave streaming whole pages straight from HBM.
+#include <algorithm>
+
 #include "common.h"
 
 namespace v1 {
@@ -55,6 +57,8 @@ struct ScoreParams {
     int32_t relu;
     int32_t clean;
     const uint8_t* pieces;  // per-query records from score_prep (shared-table kernel)
+    int32_t nchunks;        // shared-table kernel: chunks of kChunkPages pages over max_context_len
+    int32_t chunks_per_wg;  // shared-table kernel: consecutive chunks one work-group walks
 };
 
 // ---------------------------------------------------------- linear term
@@ -218,10 +222,15 @@ __device__ __forceinline__ float reduce_scatter4(const float (&s)[4]) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ int32_t page_of(const ScoreParams& p, int64_t row, int32_t blk) {
-    if (p.max_blocks <= 0) return -1;
+// Pool page of block blk of a row's table (-1: past the table or out of the
+// pool).  The unchecked form requires max_blocks > 0.
+__device__ __forceinline__ int32_t page_of_unchecked(const ScoreParams& p, int64_t row, int32_t blk) {
     const int32_t page = p.table[row * p.table_stride + min(max(blk, 0), p.max_blocks - 1)];
     return ((blk < p.max_blocks) & (page >= 0) & (page < p.kv_blocks)) ? page : -1;
+}
+
+__device__ __forceinline__ int32_t page_of(const ScoreParams& p, int64_t row, int32_t blk) {
+    return p.max_blocks > 0 ? page_of_unchecked(p, row, blk) : -1;
 }
 
 __device__ __forceinline__ void store_logit(const ScoreParams& p, int64_t row, int32_t j, int32_t ctx, float v) {
@@ -285,6 +294,16 @@ __device__ __forceinline__ void dma4(const i32x4& rs, int32_t voff, uint32_t lds
 // across it; no fence is used, as a fence would drain every load.
 #define V1_PAGE_BARRIER(pending) \
     asm volatile("s_waitcnt vmcnt(" #pending ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
+// Waits for every memory operation of this wave (stores included).
+#define V1_DRAIN() asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory")
+
+// One work-group takes 8 queries of a shared table and walks a range of
+// consecutive chunks (up to kMaxRangePages pages) through one continuous page
+// ring, so the query fragments, weights and page ids are loaded once per
+// range.  Logits of a chunk collect in LDS and are written back when the
+// walk enters the next chunk; the loads then in flight are drained with the
+// stores (stores and page loads share one counter).
+constexpr int kMaxRangePages = 2560;
 
 template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
@@ -292,22 +311,31 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t st1[V1_PAGE_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t st2[V1_PAGE_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t st3[V1_PAGE_BYTES];
-    __shared__ float olds[kQueriesPerGroup][kChunkPages][64];
-    const int l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    __shared__ __attribute__((aligned(16))) float olds[kQueriesPerGroup][kChunkPages][64];
+    __shared__ int32_t pids[kMaxRangePages];
+    const int t = threadIdx.x, l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int64_t row0 = (int64_t)blockIdx.y * kQueriesPerGroup;
-    const int32_t chunk0 = blockIdx.x * kChunkPages;
+    const int32_t c_begin = blockIdx.x * p.chunks_per_wg;
+    const int32_t nchunk = max(0, min(p.chunks_per_wg, p.nchunks - c_begin));
+    const int32_t page_begin = c_begin * kChunkPages;
 
     // The independent loads of the prologue are all issued before the first
-    // wait: query lengths (lane q mod 8: query row0 + q), the chunk's page
-    // table entries (lane i mod 16: chunk page i), query fragments, weights
-    // and records.
+    // wait: query lengths (lane q mod 8: query row0 + q), the range's page
+    // ids, query fragments, weights and records.
     int32_t lane_ctx;
     {
         const int64_t r = row0 + (l & (kQueriesPerGroup - 1));
         const int32_t c = min(p.ctx[min(r, (int64_t)p.rows - 1)], p.max_context_len);
         lane_ctx = r < p.rows ? c : 0;
     }
-    int32_t lane_page = page_of(p, row0, chunk0 + (l & (kChunkPages - 1)));
+    int32_t pid[kMaxRangePages / kThreads];
+    if (p.max_blocks > 0) {
+#pragma unroll
+        for (int k = 0; k < kMaxRangePages / kThreads; ++k) pid[k] = page_of_unchecked(p, row0, page_begin + k * kThreads + t);
+    } else {
+#pragma unroll
+        for (int k = 0; k < kMaxRangePages / kThreads; ++k) pid[k] = -1;
+    }
     // Query fragments, weights and linear-term coefficients.  Rows past the
     // end read the last row (their logits are never stored).
     v8i a[kQueriesPerWave][HB];
@@ -340,7 +368,8 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         const u32x4 x = src[0], y = src[1];
         alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
     }
-
+#pragma unroll
+    for (int k = 0; k < kMaxRangePages / kThreads; ++k) pids[k * kThreads + t] = pid[k];
 
     int32_t ctx[kQueriesPerWave];
     int32_t max_ctx = 0;
@@ -348,18 +377,40 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     for (int q = 0; q < kQueriesPerGroup; ++q) max_ctx = max(max_ctx, __builtin_amdgcn_readlane(lane_ctx, q));
 #pragma unroll
     for (int q = 0; q < kQueriesPerWave; ++q) ctx[q] = __builtin_amdgcn_readlane(lane_ctx, wv * kQueriesPerWave + q);
-    const int32_t npages = max(0, min(kChunkPages, (max_ctx + 63) / 64 - chunk0));
-    if (npages == 0) {
-        if (p.clean) {
-            for (int q = 0; q < kQueriesPerWave; ++q) {
-                const int64_t r = row0 + wv * kQueriesPerWave + q;
-                for (int j = chunk0 * 64 + l; j < (chunk0 + kChunkPages) * 64; j += kWave) store_logit(p, r, j, ctx[q], 0.f);
+    // pages of the range below the group's longest context
+    const int32_t npages = max(0, min(nchunk * kChunkPages, (max_ctx + 63) / 64 - page_begin));
+
+    // Logits of chunk k of the range (`valid` computed pages) from LDS to
+    // HBM, 4 consecutive columns per lane; a group of 4 that straddles the
+    // context end or the column limit goes element by element.
+    const bool vec = (p.logits_stride & 3) == 0 && (reinterpret_cast<uintptr_t>(p.logits) & 15) == 0;
+    auto flush = [&](int32_t k, int32_t valid) {
+        const int32_t col0 = (c_begin + k) * kChunkPages * 64;
+#pragma unroll
+        for (int q = 0; q < kQueriesPerWave; ++q) {
+            const int64_t r = row0 + wv * kQueriesPerWave + q;
+            if (r >= p.rows) continue;
+            const float* src = &olds[wv * kQueriesPerWave + q][0][0];
+#pragma unroll
+            for (int i = 0; i < kChunkPages * 64 / (4 * kWave); ++i) {
+                const int f = i * kWave + l;  // float4 index within the chunk
+                const int32_t j0 = col0 + 4 * f;
+                v4f v = v4f{0.f, 0.f, 0.f, 0.f};
+                if ((4 * f) / 64 < valid) v = *reinterpret_cast<const v4f*>(src + 4 * f);
+                if (vec && j0 + 3 < ctx[q]) {
+                    *reinterpret_cast<v4f*>(p.logits + r * p.logits_stride + j0) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) store_logit(p, r, j0 + e, ctx[q], v[e]);
+                }
             }
         }
+    };
+    if (npages == 0) {
+        for (int32_t k = 0; k < nchunk; ++k) flush(k, 0);
         return;
     }
-    // lane i < npages holds the pool page of chunk page i (-1: invalid)
-    lane_page = l < npages ? lane_page : -1;
+    __syncthreads();  // page ids in LDS
 
     // per-lane load offsets (into the page) of this wave's three loads
     int32_t voff[2];
@@ -370,8 +421,8 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         voff[i] = key * 128 + (((s & 7) ^ key_swizzle(key & 15)) << 4);
     }
     const int32_t soff = 8192 + 64 * wv + 4 * l;
-    auto issue = [&](uint8_t* buf, int32_t pg) {
-        const int32_t page = pg < npages ? __builtin_amdgcn_readlane(lane_page, pg) : -1;
+    auto issue = [&](uint8_t* buf, int32_t i) {
+        const int32_t page = i < npages ? __builtin_amdgcn_readfirstlane(pids[i]) : -1;
         const i32x4 rs = page_rsrc(p.kv, page);
         const uint32_t base = lds_addr(buf);
         dma16(rs, voff[0], base + (2 * wv) * 1024);
@@ -438,13 +489,15 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         for (int q = 0; q < kQueriesPerWave; ++q) olds[wv * kQueriesPerWave + q][pg][l] = out[q] * f.scale;
     };
 
-    // Step pg (page pg's fragments already in registers): page pg+1 is
-    // complete once only pages pg+2 and pg+3 are still in flight.  After the
-    // barrier every wave has read page pg out of LDS, so its buffer receives
-    // page pg+4; then page pg+1's fragments are read while page pg is
-    // computed.  Loads past the chunk read zeros, so every wave always has
-    // the same number of loads in flight.
+    // Step i (page i's fragments already in registers): page i+1 is complete
+    // once only pages i+2 and i+3 are still in flight.  After the barrier
+    // every wave has read page i out of LDS, so its buffer receives page i+4;
+    // then page i+1's fragments are read while page i is computed.  Loads
+    // past the range read zeros, so every wave always has the same number of
+    // loads in flight.  A step that starts a new chunk first writes back the
+    // finished one and drains (its stores and the page loads in flight).
     static_assert(kStages == 4 && kDmaPerPage * (kStages - 2) == 6, "barrier wait count");
+    static_assert(kChunkPages % kStages == 0, "chunk ends fall on the last step of a ring turn");
     Frag fa, fb;
     // Compiler-visible full wait: the query fragments, weights and records
     // loaded above are complete before the loop, so no wait for them is
@@ -452,42 +505,26 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     __builtin_amdgcn_s_waitcnt(0);
     V1_PAGE_BARRIER(0);
     load_frag(st0, fa);
-    auto step = [&](int32_t pg, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn) {
+    auto step = [&](int32_t i, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn, bool chunk_start) {
         V1_PAGE_BARRIER(6);
-        issue(cur, pg + kStages);
+        if (chunk_start && i > 0 && (i & (kChunkPages - 1)) == 0) {
+            flush((i / kChunkPages) - 1, kChunkPages);
+            V1_DRAIN();
+        }
+        issue(cur, i + kStages);
         load_frag(next, fn);
-        if (pg < npages) compute(fc, pg);
+        if (i < npages) compute(fc, i & (kChunkPages - 1));
     };
-    for (int32_t pg = 0; pg < npages; pg += kStages) {
-        step(pg, st0, st1, fa, fb);
-        step(pg + 1, st1, st2, fb, fa);
-        step(pg + 2, st2, st3, fa, fb);
-        step(pg + 3, st3, st0, fb, fa);
+    for (int32_t i = 0; i < npages; i += kStages) {
+        step(i, st0, st1, fa, fb, true);
+        step(i + 1, st1, st2, fb, fa, false);
+        step(i + 2, st2, st3, fa, fb, false);
+        step(i + 3, st3, st0, fb, fa, false);
     }
     V1_PAGE_BARRIER(0);
-
-    // Each lane writes 4 consecutive logits at a time; a group of 4 that
-    // straddles the context end or the column limit goes element by element.
-    const bool vec = (p.logits_stride & 3) == 0 && (reinterpret_cast<uintptr_t>(p.logits) & 15) == 0;
-#pragma unroll
-    for (int q = 0; q < kQueriesPerWave; ++q) {
-        const int64_t r = row0 + wv * kQueriesPerWave + q;
-        if (r >= p.rows) continue;
-        const float* src = &olds[wv * kQueriesPerWave + q][0][0];
-#pragma unroll
-        for (int i = 0; i < kChunkPages * 64 / (4 * kWave); ++i) {
-            const int f = i * kWave + l;  // float4 index within the chunk
-            const int32_t j0 = chunk0 * 64 + 4 * f;
-            v4f v = v4f{0.f, 0.f, 0.f, 0.f};
-            if ((4 * f) / 64 < npages) v = *reinterpret_cast<const v4f*>(src + 4 * f);
-            if (vec && j0 + 3 < ctx[q]) {
-                *reinterpret_cast<v4f*>(p.logits + r * p.logits_stride + j0) = v;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) store_logit(p, r, j0 + e, ctx[q], v[e]);
-            }
-        }
-    }
+    const int32_t last = (npages - 1) / kChunkPages;
+    flush(last, npages - last * kChunkPages);
+    for (int32_t k = last + 1; k < nchunk; ++k) flush(k, 0);
 }
 
 // ---------------------------------------------------------------- per row
@@ -568,6 +605,20 @@ using namespace v1;
 
 extern "C" int64_t v1_score_workspace(int32_t rows) { return rows > 0 ? (int64_t)rows * kPieceRowBytes : 0; }
 
+namespace {
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
+    }
+    return cus[dev];
+}
+}  // namespace
+
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
     V1_REQUIRE(a != nullptr, "score: null args");
     V1_REQUIRE(a->heads >= 1 && a->heads <= 64, "score: heads must be in [1, 64]");
@@ -591,7 +642,15 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
                            a->heads, a->relu, static_cast<uint8_t*>(a->workspace));
         const int rc = V1_LAUNCHED("score_prep");
         if (rc != V1_OK) return rc;
-        const dim3 grid(chunks, (uint32_t)cdiv(a->rows, kQueriesPerGroup));
+        // Split each row group's chunks into as few ranges as fill the chip
+        // (two work-groups per CU) and keep each range within kMaxRangePages.
+        const int64_t groups = cdiv(a->rows, kQueriesPerGroup);
+        int64_t nsplit = std::min<int64_t>((int64_t)chunks, std::max<int64_t>(1, cdiv(2 * device_cus(), groups)));
+        nsplit = std::max<int64_t>(nsplit, cdiv((int64_t)chunks * kChunkPages, kMaxRangePages));
+        p.nchunks = (int32_t)chunks;
+        p.chunks_per_wg = (int32_t)cdiv((int64_t)chunks, nsplit);
+        nsplit = cdiv((int64_t)chunks, p.chunks_per_wg);
+        const dim3 grid((uint32_t)nsplit, (uint32_t)groups);
         launch_hb<Shared>(hb, a->relu != 0, grid, st, p);
         return V1_LAUNCHED("score_shared");
     }
