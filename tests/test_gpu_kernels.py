@@ -577,6 +577,28 @@ def test_score_vs_dequantised_reference(dev, rows, heads, ctx, shared):
     assert_scores_close(got, ref, bound)
 
 
+@pytest.mark.parametrize("rows,ctx", [(45, 5000), (300, 700), (8, 9000)])
+def test_score_shared_uneven_lengths(dev, rows, ctx):
+    """Shared table with unordered lengths, empty rows and a column limit past
+    every context: the work split by equal page spans must still write every
+    logit once (unwritten columns would keep the NaN fill)."""
+    g = np.random.default_rng(rows + ctx)
+    q8, w, native, table, _ = _score_case(g, rows, 64, ctx, True, 200)
+    lens = g.integers(0, ctx + 1, rows).astype(np.int32)
+    lens[g.random(rows) < 0.2] = 0
+    width = ctx + 100
+    out = torch.full((rows, width + 4), float("nan"), device=dev)
+    bt = T(table, dev)[None].expand(rows, -1)
+    SC.fp8_paged_mqa_logits(T(q8, dev).view(torch.float8_e4m3fn), T(native, dev), T(w, dev), T(lens, dev), bt, None,
+                            width, clean_logits=True, out=out)
+    full = np.broadcast_to(table, (rows, table.shape[-1]))
+    ref = O.paged_logits(q8, w, native, full, lens, width)
+    bound = O.paged_logits(q8, w, native, full, lens, width, magnitude=True)
+    got = H(out).astype(np.float64)
+    assert np.isnan(got[:, width:]).all()
+    assert_scores_close(got[:, :width], ref, bound)
+
+
 def assert_scores_close(got, ref, bound):
     """1e-2 relative, plus the fp32 accumulation allowance 2^-16 * sum|w q k s|
     that a near-zero (cancelling) dot product needs."""

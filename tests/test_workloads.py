@@ -1,0 +1,183 @@
+"""End-to-end GPU parity on the benchmark workloads at their full sizes.
+
+Each stage runs through the C ABI on the GPU; its output is checked against the
+oracle on the same inputs (the GPU result of the previous stage), bit-exact for
+ids, tables and bytes and within the score tolerance for logits.  Where the
+oracle cannot cover every row in seconds, a fixed sample of rows (always the
+first, the last and the longest) is compared and the rest is checked through
+size-independent properties.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import pkg
+from oracle import v1 as O
+from test_gpu_kernels import H, T, assert_scores_close
+
+pytestmark = pytest.mark.gpu
+
+QF = pkg("query_fused")
+K = pkg("kernels")
+NK = pkg("native_kernels")
+SC = pkg("scoring")
+TK = pkg("topk")
+W = pkg("workloads")
+
+
+def _sample_rows(n, g, extra=()):
+    rows = {0, n - 1, *extra}
+    rows.update(int(x) for x in g.choice(n, min(n, 6), replace=False))
+    return np.array(sorted(rows))
+
+
+def test_config1_query_chain(dev):
+    """Reference example shape (1024 queries, 1 head, P=128, 40 of 64 pages,
+    2688 candidates): coarse score -> route (+ fine table) -> shared tail
+    staging -> fine score -> fused Top-2048 with mask -> slot gather, the
+    order of Query.compute (sglang/srt/layers/attention/v1_deepseek/runtime.py:417-678)."""
+    wl = W.config1()
+    a, prm = wl.arrays, wl.params
+    B, P, CAP, TAKE, WIDTH, TOP = prm["B"], prm["P"], prm["CAP"], prm["TAKE"], prm["WIDTH"], prm["TOPK"]
+    q = T(a["q8"], dev).view(torch.float8_e4m3fn)
+    w = T(a["w"], dev)
+    # coarse: 512 centers (8 per built page), columns of the 128-page route width
+    center_lens = np.full(B, 512, np.int32)
+    ctab = np.broadcast_to(a["center_table"], (B, a["center_table"].shape[0]))
+    coarse = SC.fp8_paged_mqa_logits(q, T(a["centers"], dev), w, T(center_lens, dev),
+                                     T(a["center_table"], dev)[None].expand(B, -1), None, P * 8, clean_logits=True)
+    ref = O.paged_logits(a["q8"], a["w"], a["centers"], ctab, center_lens, P * 8)
+    bound = O.paged_logits(a["q8"], a["w"], a["centers"], ctab, center_lens, P * 8, magnitude=True)
+    coarse_h = H(coarse)
+    assert_scores_close(coarse_h.astype(np.float64), ref, bound)
+
+    # route with the fine-table fill
+    sel = torch.empty((B, TAKE), device=dev, dtype=torch.int32)
+    ft = torch.empty((B, prm["FT_COLS"]), device=dev, dtype=torch.int32)
+    QF.module().route(coarse, T(a["lens"], dev), T(a["takes"], dev), sel, P, T(a["rt"], dev), ft,
+                      T(a["tail_rows"], dev), CAP, True)
+    e_sel = np.full((B, TAKE), -1, np.int32)
+    e_ft = np.full((B, prm["FT_COLS"]), -1, np.int32)
+    O.route(coarse_h, a["lens"], a["takes"], e_sel, P, a["rt"], e_ft, a["tail_rows"], CAP, True)
+    sel_h, ft_h = H(sel), H(ft)
+    assert np.array_equal(sel_h, e_sel) and np.array_equal(ft_h, e_ft)
+    # the unfused table kernel gives the same table
+    ft2 = torch.empty_like(ft)
+    K.fine_table_shared[(B,)](T(a["rt"], dev), sel, T(a["takes"], dev), T(a["lens"], dev), ft2, T(a["tail_rows"], dev),
+                              CAP, P, TAKE, prm["FT_COLS"], 68, 32)
+    assert np.array_equal(H(ft2), ft_h)
+
+    # shared tail staging into the fine pool (one owner: every row shares row 0's tail)
+    fine = a["fine"].copy()
+    fine_d = T(fine, dev)
+    K.stage_tail_shared[(-(-B // 32), 68)](T(a["native"], dev), None, T(a["nt"], dev), T(a["lens"], dev), fine_d, None,
+                                           T(a["tail_rows"], dev), CAP, P, 68, prm["SINK"], prm["WINDOW"], ROWS=B,
+                                           GROUP=32)
+    O.stage_tail(a["native"], a["nt"], a["lens"], fine, CAP, 68, prm["SINK"], prm["WINDOW"], tail_rows=a["tail_rows"],
+                 rows=B)
+    fine_h = H(fine_d)
+    assert np.array_equal(fine_h, fine)
+
+    # fine score over each row's fine table
+    fl = a["fine_lens"]
+    logits = SC.fp8_paged_mqa_logits(q, fine_d, w, T(fl, dev), ft, None, WIDTH, clean_logits=True)
+    ref = O.paged_logits(a["q8"], a["w"], fine_h, ft_h, fl, WIDTH)
+    bound = O.paged_logits(a["q8"], a["w"], fine_h, ft_h, fl, WIDTH, magnitude=True)
+    logits_h = H(logits)
+    assert_scores_close(logits_h.astype(np.float64), ref, bound)
+
+    # fused Top-2048 with the sink/tail mask, then the slot gather
+    physical = torch.empty((B, TOP), device=dev, dtype=torch.int32)
+    logical = torch.empty_like(physical)
+    raw = torch.empty_like(physical)
+    expanded = torch.empty((B, 4 * TOP + 64), device=dev, dtype=torch.int32)
+    QF.module().topk(logits, T(fl, dev), T(a["members"], dev), T(a["rt"], dev), T(a["nt"], dev), sel,
+                     T(a["lens"], dev), T(a["takes"], dev), physical, logical, raw, prm["WINDOW"], True, expanded,
+                     True, True, ft, False)
+    masked = logits_h.copy()
+    exp = O.fused_topk(masked, fl, a["members"], a["rt"], a["nt"], sel_h, a["lens"], a["takes"], TOP, prm["WINDOW"],
+                       True, 4 * TOP + 64, True, True, ft_h, False)
+    assert np.array_equal(H(logits), masked)
+    for name, got in (("raw", raw), ("logical", logical), ("physical", physical), ("expanded", expanded)):
+        assert np.array_equal(H(got), exp[name]), name
+    out = torch.empty((B, TOP, W.MLA_ROW_BYTES), device=dev, dtype=torch.uint8)
+    NK.gather_rows(T(a["latent"], dev), physical, out)
+    assert np.array_equal(H(out), O.gather_rows(a["latent"], exp["physical"]))
+
+
+def test_config3_gather_full(dev):
+    """1024 x 2048 ids (5% -1) through per-row 512-page windows of a 1M-row
+    pool of 656-byte rows, every output byte compared."""
+    wl = W.config3()
+    a, prm = wl.arrays, wl.params
+    out = torch.empty((prm["rows"], prm["top"], prm["row_bytes"]), device=dev, dtype=torch.uint8)
+    NK.gather_rows(T(a["pool"], dev), T(a["ids"], dev), out, table=T(a["table"], dev), page_bits=prm["page_bits"])
+    exp = O.gather_rows(a["pool"], a["ids"], a["table"], prm["page_bits"])
+    assert np.array_equal(H(out), exp)
+
+
+def test_config4_prefill_chunk(dev):
+    """4096 queries x 64 heads over a 32768-token causal context: score, Top-2048
+    slot map and gather for every row on the GPU; sampled rows against the oracle,
+    and for every row: slots inside the query's context, strictly ascending
+    candidate order, no duplicates."""
+    wl = W.config4()
+    a, prm = wl.arrays, wl.params
+    rows, ctx, TOP = prm["rows"], prm["ctx"], prm["topk"]
+    table = T(a["table"], dev)
+    logits = SC.fp8_paged_mqa_logits(T(a["q8"], dev).view(torch.float8_e4m3fn), T(a["native"], dev), T(a["w"], dev),
+                                     T(a["lens"], dev), table[None].expand(rows, -1), None, ctx, clean_logits=True)
+    slots = torch.empty((rows, TOP), device=dev, dtype=torch.int32)
+    raw = torch.empty_like(slots)
+    TK.topk_transform_512_v2(logits, T(a["lens"], dev), table[None].expand(rows, -1).contiguous(), slots, 64, None, raw)
+    out = torch.empty((rows, TOP, prm["row_bytes"]), device=dev, dtype=torch.uint8)
+    NK.gather_rows(T(a["latent"], dev), slots, out)
+
+    g = np.random.default_rng(4)
+    pick = _sample_rows(rows, g)
+    lg = H(logits[torch.from_numpy(pick).to(dev)]).astype(np.float64)
+    full = np.broadcast_to(a["table"], (len(pick), a["table"].shape[0]))
+    ref = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], full, a["lens"][pick], ctx)
+    bound = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], full, a["lens"][pick], ctx, magnitude=True)
+    assert_scores_close(lg, ref, bound)
+    e_slots, e_raw = O.transform_topk(lg.astype(np.float32), a["lens"][pick], full, TOP, 6)
+    raw_h, slots_h = H(raw), H(slots)
+    assert np.array_equal(raw_h[pick], e_raw) and np.array_equal(slots_h[pick], e_slots)
+    assert np.array_equal(H(out[torch.from_numpy(pick).to(dev)]), O.gather_rows(a["latent"], e_slots))
+    # every row: T distinct candidates, ascending, below the row's length
+    assert (raw_h >= 0).all() and (np.diff(raw_h, axis=1) > 0).all()
+    assert (raw_h < a["lens"][:, None]).all()
+    assert np.array_equal(slots_h, (a["table"][raw_h >> 6] << 6) | (raw_h & 63))
+
+
+def test_config5_decode_batch(dev):
+    """128 requests with their own page tables, contexts 4K..128K tokens (rows
+    past 32768 candidates take the segmented Top-K), pool reduced to 4096 pages
+    so the inputs build in seconds."""
+    wl = W.config5(pool_pages=4096)
+    a, prm = wl.arrays, wl.params
+    rows, TOP, max_ctx = prm["rows"], prm["topk"], prm["max_ctx"]
+    table = T(a["table"], dev)
+    # the Top-K reads rows with 16-byte loads: row stride padded to 4 columns
+    logits = torch.empty((rows, -(-max_ctx // 4) * 4), device=dev)[:, :max_ctx]
+    SC.fp8_paged_mqa_logits(T(a["q8"], dev).view(torch.float8_e4m3fn), T(a["native"], dev), T(a["w"], dev),
+                            T(a["lens"], dev), table, None, max_ctx, clean_logits=True, out=logits)
+    slots = torch.empty((rows, TOP), device=dev, dtype=torch.int32)
+    raw = torch.empty_like(slots)
+    TK.topk_transform_512_v2(logits, T(a["lens"], dev), table, slots, 64, None, raw)
+    g = np.random.default_rng(5)
+    latent = g.integers(0, 256, (prm["latent_rows"], prm["row_bytes"]), dtype=np.uint8)
+    out = torch.empty((rows, TOP, prm["row_bytes"]), device=dev, dtype=torch.uint8)
+    NK.gather_rows(T(latent, dev), slots, out)
+
+    pick = _sample_rows(rows, g, extra=(int(np.argmax(a["lens"])), int(np.argmin(a["lens"]))))
+    lg = H(logits[torch.from_numpy(pick).to(dev)]).astype(np.float64)
+    ref = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], a["table"][pick], a["lens"][pick], max_ctx)
+    bound = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], a["table"][pick], a["lens"][pick], max_ctx,
+                           magnitude=True)
+    assert_scores_close(lg, ref, bound)
+    e_slots, e_raw = O.transform_topk(lg.astype(np.float32), a["lens"][pick], a["table"][pick], TOP, 6)
+    raw_h, slots_h = H(raw), H(slots)
+    assert np.array_equal(raw_h[pick], e_raw) and np.array_equal(slots_h[pick], e_slots)
+    assert np.array_equal(H(out[torch.from_numpy(pick).to(dev)]), O.gather_rows(latent, e_slots))
+    assert (np.diff(raw_h, axis=1) > 0).all() and (raw_h < a["lens"][:, None]).all()
