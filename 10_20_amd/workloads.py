@@ -59,11 +59,19 @@ def pow2_scale(absmax):
     return np.ldexp(np.float32(1.0), e).astype(np.float32)
 
 
+def e4m3_encode_fast(x):
+    """e4m3_encode through torch's round-to-nearest-even cast (identical codes,
+    checked against e4m3_encode in the tests), for large arrays."""
+    import torch
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
 def quantize_rows(x):
     """Per-row (token) FP8 quantisation: returns (bytes [n, d], scale [n])."""
     x = np.asarray(x, dtype=np.float32)
     s = pow2_scale(np.abs(x).max(axis=-1))
-    return e4m3_encode(x / s[..., None]), s
+    return e4m3_encode_fast(x / s[..., None]), s
 
 
 def pack_pages(k8, ks, n_pages=None):

@@ -1,15 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the query-indexing hot path on one MI355X.
 
-A step is one pass of the path over one batch: FP8 paged index scoring ->
-exact Top-2048 with page-table slot mapping -> 656-byte latent-row gather
-into a reused [rows, 2048, 656] workspace.  Default workload: the
-DeepSeek-V3.2-style prefill indexer chunk (4096 queries x 64 heads x 128,
-32768-token FP8 context in 64-token pages, causal).  Inputs are synthetic
-(seeded PCG64) and resident in HBM before timing starts.
+A step is one pass of the path over one batch of synthetic input (seeded
+PCG64, resident in HBM before timing starts).  Workloads (--config):
 
-Prints one JSON line (queries/sec, per-stage times, roofline of the dominant
-kernel, CPU baseline of the reference's torch expressions).
+  4 (default)  prefill indexer chunk: 4096 queries x 64 heads x 128 FP8 against a
+               32768-token paged FP8 context, causal -> exact Top-2048 with page-table
+               slot mapping -> 656-byte latent-row gather into a reused workspace
+  1            the reference example shape: 1024 queries x 1 head; coarse score over
+               centers -> route (40 of 64 pages, fine table) -> shared tail staging ->
+               fine score over 2688 candidates -> fused Top-2048 with mask -> gather
+  3            K/V slot gather: 1024 x 2048 ids (5% padding) through per-query
+               512-page windows of a 1M-token pool of 656-byte rows
+  5            decode batch: 128 requests x 64 heads, contexts 4K..128K tokens with
+               their own page tables in a 2M-token pool -> Top-2048 -> gather
+
+Prints one JSON line: queries/sec, per-stage times, the roofline of the
+dominant kernel and the CPU baseline (the reference's torch expressions on
+the host cores, on a bounded sample of the same workload).
 """
 import argparse
 import importlib
@@ -24,8 +32,8 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
-# HBM traffic per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE on this
-# workload (calibrated against a plain copy), kept with the kernel trace.
+# HBM traffic per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE on the
+# default workload (calibrated against a plain copy), kept with the kernel trace.
 TRAFFIC_PROFILE = ROOT / "profiles" / "prefill_chunk_4096x32k.md"
 STAGE_KERNELS = {"score": ("score_prep", "score_shared"), "topk": ("transform_rows",), "gather": ("gather_rows16",)}
 
@@ -33,7 +41,7 @@ STAGE_KERNELS = {"score": ("score_prep", "score_shared"), "topk": ("transform_ro
 def measured_traffic(stage):
     """HBM bytes per step of a stage's kernels from the committed counter
     summary, or None when the summary does not list them."""
-    if not TRAFFIC_PROFILE.exists():
+    if stage not in STAGE_KERNELS or not TRAFFIC_PROFILE.exists():
         return None
     per_kernel = {}
     for line in TRAFFIC_PROFILE.read_text().splitlines():
@@ -71,31 +79,21 @@ def copy_calibration(nbytes):
     print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 3}), flush=True)
 
 
-def main():
-    args = parse()
-    if args.copy_calibration:
-        copy_calibration(args.copy_calibration)
-        return
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
-              file=sys.stderr)
-        sys.exit(2)
-    import numpy as np
-    import torch
+class Pkg:
+    def __init__(self):
+        for name in ("workloads", "scoring", "topk", "native_kernels", "query_fused", "kernels"):
+            setattr(self, name, importlib.import_module(f"10_20_amd.{name}"))
 
-    W = importlib.import_module("10_20_amd.workloads")
-    SC = importlib.import_module("10_20_amd.scoring")
-    TK = importlib.import_module("10_20_amd.topk")
-    NK = importlib.import_module("10_20_amd.native_kernels")
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
 
-    if args.config != 4:
-        raise SystemExit("only the prefill-chunk workload (config 4) is wired into bench.py so far")
-    wl = W.config4()
+def _score_flops(heads, lens):
+    return 2.0 * heads * 128 * float(lens.astype("int64").sum())
+
+
+def setup_prefill(P, dev, torch, np):
+    """Configuration 4: prefill indexer chunk."""
+    wl = P.workloads.config4()
     a, prm = wl.arrays, wl.params
-    rows, heads, T, row_bytes = prm["rows"], prm["heads"], prm["topk"], prm["row_bytes"]
-    ctx = prm["ctx"]
+    rows, heads, T, row_bytes, ctx = prm["rows"], prm["heads"], prm["topk"], prm["row_bytes"], prm["ctx"]
     q = torch.from_numpy(a["q8"]).to(dev).view(torch.float8_e4m3fn)
     w = torch.from_numpy(a["w"]).to(dev)
     native = torch.from_numpy(a["native"]).to(dev)
@@ -108,29 +106,185 @@ def main():
     slots = torch.empty((rows, T), device=dev, dtype=torch.int32)
     raw = torch.empty_like(slots)
     work = torch.empty((rows, T, row_bytes), device=dev, dtype=torch.uint8)
+    stages = [
+        ("score", lambda: P.scoring.fp8_paged_mqa_logits(q, native, w, lens, shared_table, None, ctx,
+                                                          clean_logits=False, out=logits)),
+        ("topk", lambda: P.topk.topk_transform_512_v2(logits, lens, dense_table, slots, 64, None, raw)),
+        ("gather", lambda: P.native_kernels.gather_rows(latent, slots, work)),
+    ]
+    L = a["lens"].astype(np.int64)
+    work_units = {
+        "score": (_score_flops(heads, L) / 1e12, "TFLOP/s", PEAK_FP8_TFLOPS, "mfma"),
+        "topk": ((4.0 * L.sum() + 8.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "gather": ((2.0 * row_bytes * rows * T + 4.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+    }
 
-    stages = ["score", "topk", "gather"]
-    ev = {s: [] for s in stages}
+    def cpu(budget):
+        from oracle import cpu_baseline
+        qps, n, threads = cpu_baseline.prefill_queries_per_second(a["q8"], a["w"], a["native"], a["table"],
+                                                                  a["lens"], a["latent"], T, budget)
+        return qps, threads, f"{n} of {rows} queries (score+top2048+slot map+gather)"
+
+    meta = {"workload": "prefill indexer chunk: 4096 queries x 64 heads x 128 FP8 vs 32768-token paged FP8 "
+                        "context, causal, Top-2048, 656-byte latent row gather",
+            "global_batch": rows, "seq_len": ctx, "parallelism": "single GPU"}
+    return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 4)"
+
+
+def setup_example(P, dev, torch, np):
+    """Configuration 1: the reference example's query chain."""
+    wl = P.workloads.config1()
+    a, prm = wl.arrays, wl.params
+    B, PG, CAP, TAKE, WIDTH, T = prm["B"], prm["P"], prm["CAP"], prm["TAKE"], prm["WIDTH"], prm["TOPK"]
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in a.items()}
+    q = d["q8"].view(torch.float8_e4m3fn)
+    center_lens = torch.full((B,), 512, device=dev, dtype=torch.int32)
+    ctab = d["center_table"][None].expand(B, -1)
+    coarse = torch.empty((B, PG * 8), device=dev)
+    sel = torch.empty((B, TAKE), device=dev, dtype=torch.int32)
+    ft = torch.empty((B, prm["FT_COLS"]), device=dev, dtype=torch.int32)
+    logits = torch.empty((B, WIDTH), device=dev)
+    physical = torch.empty((B, T), device=dev, dtype=torch.int32)
+    logical = torch.empty_like(physical)
+    raw = torch.empty_like(physical)
+    no_exp = torch.empty_strided((B, 0), (0, 1), device=dev, dtype=torch.int32)
+    work = torch.empty((B, T, P.workloads.MLA_ROW_BYTES), device=dev, dtype=torch.uint8)
+    fused = P.query_fused.module()
+    stages = [
+        ("coarse", lambda: P.scoring.fp8_paged_mqa_logits(q, d["centers"], d["w"], center_lens, ctab, None, PG * 8,
+                                                           clean_logits=True, out=coarse)),
+        ("route", lambda: fused.route(coarse, d["lens"], d["takes"], sel, PG, d["rt"], ft, d["tail_rows"], CAP, True)),
+        ("stage", lambda: P.kernels.stage_tail_shared[(-(-B // 32), 68)](
+            d["native"], None, d["nt"], d["lens"], d["fine"], None, d["tail_rows"], CAP, PG, 68, prm["SINK"],
+            prm["WINDOW"], ROWS=B, GROUP=32)),
+        ("score", lambda: P.scoring.fp8_paged_mqa_logits(q, d["fine"], d["w"], d["fine_lens"], ft, None, WIDTH,
+                                                          clean_logits=True, out=logits)),
+        ("topk", lambda: fused.topk(logits, d["fine_lens"], d["members"], d["rt"], d["nt"], sel, d["lens"],
+                                    d["takes"], physical, logical, raw, prm["WINDOW"], True, no_exp, True, True, ft,
+                                    False)),
+        ("gather", lambda: P.native_kernels.gather_rows(d["latent"], physical, work)),
+    ]
+    fl = a["fine_lens"].astype(np.int64)
+    rb = P.workloads.MLA_ROW_BYTES
+    work_units = {
+        "coarse": (_score_flops(1, np.full(B, 512)) / 1e12, "TFLOP/s", PEAK_FP8_TFLOPS, "mfma"),
+        "route": ((32.0 * 64 * B + 4.0 * B * (TAKE + prm["FT_COLS"])) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "stage": (2.0 * 2 * 8448 / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "score": (_score_flops(1, fl) / 1e12, "TFLOP/s", PEAK_FP8_TFLOPS, "mfma"),
+        "topk": ((4.0 * fl.sum() + 12.0 * B * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "gather": ((2.0 * rb * B * T + 4.0 * B * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+    }
+
+    def cpu(budget):
+        from oracle import cpu_baseline
+        qps, n, threads = cpu_baseline.example_queries_per_second(a, prm, budget)
+        return qps, threads, f"{n} of {B} queries (score over the 2688 candidates + top2048 + slot map + gather)"
+
+    meta = {"workload": "reference example query chain: 1024 queries x 1 head, route 40 of 64 pages, "
+                        "2688 candidates, fused Top-2048 with mask, 656-byte row gather",
+            "global_batch": B, "seq_len": WIDTH, "parallelism": "single GPU"}
+    return B, stages, work_units, cpu, meta, "synthetic (PCG64 seed 19)"
+
+
+def setup_gather(P, dev, torch, np):
+    """Configuration 3: K/V slot gather."""
+    wl = P.workloads.config3()
+    a, prm = wl.arrays, wl.params
+    rows, T, rb = prm["rows"], prm["top"], prm["row_bytes"]
+    pool = torch.from_numpy(a["pool"]).to(dev)
+    table = torch.from_numpy(a["table"]).to(dev)
+    ids = torch.from_numpy(a["ids"]).to(dev)
+    work = torch.empty((rows, T, rb), device=dev, dtype=torch.uint8)
+    stages = [("gather", lambda: P.native_kernels.gather_rows(pool, ids, work, table=table, page_bits=6))]
+    valid = int((a["ids"] >= 0).sum())
+    work_units = {"gather": ((rb * valid + rb * rows * T + 8.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm")}
+
+    def cpu(budget):
+        from oracle import cpu_baseline
+        qps, n, threads = cpu_baseline.gather_queries_per_second(a["pool"], a["ids"], a["table"], budget)
+        return qps, threads, f"{n} of {rows} queries (2048-slot gather)"
+
+    meta = {"workload": "K/V slot gather: 1024 queries x 2048 slots (5% padding) from a 1M-token pool of "
+                        "656-byte rows through per-query 512-page windows",
+            "global_batch": rows, "seq_len": T, "parallelism": "single GPU"}
+    return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 3)"
+
+
+def setup_decode(P, dev, torch, np):
+    """Configuration 5: decode batch with per-request page tables."""
+    wl = P.workloads.config5()
+    a, prm = wl.arrays, wl.params
+    rows, heads, T, rb, max_ctx = prm["rows"], prm["heads"], prm["topk"], prm["row_bytes"], prm["max_ctx"]
+    q = torch.from_numpy(a["q8"]).to(dev).view(torch.float8_e4m3fn)
+    w = torch.from_numpy(a["w"]).to(dev)
+    native = torch.from_numpy(a["native"]).to(dev)
+    table = torch.from_numpy(a["table"]).to(dev)
+    lens = torch.from_numpy(a["lens"]).to(dev)
+    latent = torch.randint(0, 256, (prm["latent_rows"], rb), device=dev, dtype=torch.uint8)
+    logits = torch.empty((rows, -(-max_ctx // 4) * 4), device=dev)[:, :max_ctx]
+    slots = torch.empty((rows, T), device=dev, dtype=torch.int32)
+    raw = torch.empty_like(slots)
+    work = torch.empty((rows, T, rb), device=dev, dtype=torch.uint8)
+    stages = [
+        ("score", lambda: P.scoring.fp8_paged_mqa_logits(q, native, w, lens, table, None, max_ctx,
+                                                          clean_logits=False, out=logits)),
+        ("topk", lambda: P.topk.topk_transform_512_v2(logits, lens, table, slots, 64, None, raw)),
+        ("gather", lambda: P.native_kernels.gather_rows(latent, slots, work)),
+    ]
+    L = a["lens"].astype(np.int64)
+    work_units = {
+        # decode scoring is bound by the K pages it streams: 132 B per (row, key) + Q, w and the logit
+        "score": ((132.0 * L.sum() + rows * heads * 132.0 + 4.0 * L.sum()) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "topk": ((4.0 * L.sum() + 8.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "gather": ((2.0 * rb * rows * T + 4.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+    }
+
+    def cpu(budget):
+        from oracle import cpu_baseline
+        qps, n, threads = cpu_baseline.decode_queries_per_second(a["q8"], a["w"], a["native"], a["table"],
+                                                                 a["lens"], T, budget)
+        return qps, threads, f"{n} of {rows} requests (score+top2048+slot map; gather rows synthetic)"
+
+    meta = {"workload": "decode batch: 128 requests x 64 heads FP8, contexts 4K-128K tokens with per-request "
+                        "page tables in a 2M-token pool, Top-2048, 656-byte row gather",
+            "global_batch": rows, "seq_len": max_ctx, "parallelism": "single GPU"}
+    return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 5)"
+
+
+SETUPS = {1: setup_example, 3: setup_gather, 4: setup_prefill, 5: setup_decode}
+
+
+def main():
+    args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    P = Pkg()
+    rows, stages, work_units, cpu_fn, meta, data = SETUPS[args.config](P, dev, torch, np)
+    names = [n for n, _ in stages]
+    ev = {n: [] for n in names}
 
     def step(record):
-        e0 = torch.cuda.Event(enable_timing=True) if record else None
+        prev = None
         if record:
-            e0.record()
-        SC.fp8_paged_mqa_logits(q, native, w, lens, shared_table, None, ctx, clean_logits=False, out=logits)
-        if record:
-            e1 = torch.cuda.Event(enable_timing=True)
-            e1.record()
-        TK.topk_transform_512_v2(logits, lens, dense_table, slots, 64, None, raw)
-        if record:
-            e2 = torch.cuda.Event(enable_timing=True)
-            e2.record()
-        NK.gather_rows(latent, slots, work)
-        if record:
-            e3 = torch.cuda.Event(enable_timing=True)
-            e3.record()
-            ev["score"].append((e0, e1))
-            ev["topk"].append((e1, e2))
-            ev["gather"].append((e2, e3))
+            prev = torch.cuda.Event(enable_timing=True)
+            prev.record()
+        for name, fn in stages:
+            fn()
+            if record:
+                e = torch.cuda.Event(enable_timing=True)
+                e.record()
+                ev[name].append((prev, e))
+                prev = e
 
     for _ in range(args.warmup):
         step(False)
@@ -141,47 +295,35 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
-    stage_ms = {s: sum(x.elapsed_time(y) for x, y in ev[s]) / args.steps for s in stages}
+    stage_ms = {n: sum(x.elapsed_time(y) for x, y in ev[n]) / args.steps for n in names}
 
-    L = a["lens"].astype(np.int64)
-    flops = 2.0 * heads * 128 * float(L.sum())
-    valid = rows * T  # every row has more than T candidates
-    work_units = {
-        "score": (flops / 1e12, "TFLOP/s", PEAK_FP8_TFLOPS, "mfma"),
-        "topk": ((4.0 * L.sum() + 8.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
-        "gather": ((row_bytes * valid + row_bytes * rows * T + 4.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
-    }
     stage_info = {}
-    for s in stages:
-        amount, unit, peak, bound = work_units[s]
-        ach = amount / (stage_ms[s] / 1e3)
-        stage_info[s] = {"ms": round(stage_ms[s], 4), "achieved": round(ach, 1), "unit": unit, "bound": bound,
+    for n in names:
+        amount, unit, peak, bound = work_units[n]
+        ach = amount / (stage_ms[n] / 1e3)
+        stage_info[n] = {"ms": round(stage_ms[n], 4), "achieved": round(ach, 1), "unit": unit, "bound": bound,
                          "frac": round(ach / peak, 4)}
-    dom = max(stages, key=lambda s: stage_ms[s])
+    dom = max(names, key=lambda n: stage_ms[n])
     amount, unit, peak, bound = work_units[dom]
     achieved = amount / (stage_ms[dom] / 1e3)
 
     cpu = None
     if args.cpu_budget > 0:
-        from oracle import cpu_baseline
-        qps, n, threads = cpu_baseline.prefill_queries_per_second(a["q8"], a["w"], a["native"], a["table"],
-                                                                  a["lens"], a["latent"], T, args.cpu_budget)
-        cpu = {"value": round(qps, 3), "unit": "queries/s", "cores": threads, "kind": "port",
-               "sample": f"{n} of {rows} queries (score+top2048+slot map+gather), torch CPU, {os.cpu_count()} "
-                         f"host cpus visible"}
+        qps_cpu, threads, sample = cpu_fn(args.cpu_budget)
+        cpu = {"value": round(qps_cpu, 3), "unit": "queries/s", "cores": threads, "kind": "port",
+               "sample": f"{sample}, torch CPU, {os.cpu_count()} host cpus visible"}
 
     qps = rows * args.steps / (t1 - t0)
     line = {
         "metric": "indexed queries/sec (score+Top2048+gather) and % of FP8-MFMA/HBM roofline",
         "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp8-e4m3 score / fp32 accumulate / int32 indices / u8 rows", "data": "synthetic (PCG64 seed 4)",
-        "config": {"workload": "prefill indexer chunk: 4096 queries x 64 heads x 128 FP8 vs 32768-token paged "
-                               "FP8 context, causal, Top-2048, 656-byte latent row gather",
-                   "global_batch": rows, "seq_len": ctx, "parallelism": "single GPU"},
+        "dtype": "fp8-e4m3 score / fp32 accumulate / int32 indices / u8 rows", "data": data,
+        "config": meta,
         "stages": stage_info,
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(dom)},
+                     "frac": round(achieved / peak, 4),
+                     "traffic": measured_traffic(dom) if args.config == 4 else None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

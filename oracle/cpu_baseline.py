@@ -44,3 +44,90 @@ def prefill_queries_per_second(q8, w, native, table, lens, latent, topk=2048, bu
         done += 1
     dt = time.perf_counter() - t0
     return done / dt, done, threads
+
+
+def _dequant_pages(native, pages):
+    """fp32 keys [len(pages) * 64, 128] and scales of native pages."""
+    kb = native[pages, :8192].reshape(-1, 128)
+    ks = native[pages, 8192:].copy().view(np.float32).reshape(-1)
+    k = torch.from_numpy(np.ascontiguousarray(kb)).view(torch.float8_e4m3fn).float()
+    return k, torch.from_numpy(np.ascontiguousarray(ks))
+
+
+def example_queries_per_second(a, prm, budget_s=10.0, min_rows=8):
+    """The reference example's torch path per query
+    (sglang/srt/layers/attention/v1_deepseek/example_v1_query_single_head.py:38-70):
+    coarse scores over centers, page max, top-40 pages, candidate keys (their
+    members, sink, tail), masked fine scores, Top-2048, slot map, row gather."""
+    threads = torch.get_num_threads()
+    B, take, n, window, sink_cap = prm["B"], prm["TAKE"], prm["N"], prm["WINDOW"], prm["SINK"]
+    centers, cs = _dequant_pages(a["centers"], np.arange(a["centers"].shape[0]))
+    centers = centers * cs[:, None]
+    nt = a["nt"][0]
+    keys, ks = _dequant_pages(a["native"], nt[: -(-n // 64)])
+    keys = keys * ks[:, None]
+    members = torch.from_numpy(a["members"].astype(np.int64))
+    rt = torch.from_numpy(a["rt"][0].astype(np.int64))
+    ntt = torch.from_numpy(nt.astype(np.int64))
+    lat = torch.from_numpy(a["latent"])
+    sink = min(n, sink_cap)
+    tail = max(sink, min((n - 1) // 1024 * 1024, max(sink, n - window)))
+    fixed = torch.cat((torch.arange(sink), torch.arange(tail, n)))
+    qs = torch.from_numpy(a["q8"][:, 0]).view(torch.float8_e4m3fn).float()
+    w = torch.from_numpy(a["w"][:, 0])
+    done, t0 = 0, time.perf_counter()
+    while done < B and (done < min_rows or time.perf_counter() - t0 < budget_s):
+        q = qs[done] * w[done]
+        coarse = torch.relu(centers @ q)
+        pages = coarse.view(64, 8).amax(1).topk(take).indices
+        chosen = members[rt[pages]].reshape(-1)
+        cand = torch.cat((chosen, fixed))
+        valid = torch.ones(cand.shape[0], dtype=torch.bool)
+        valid[: take * 64] = (chosen >= sink) & (chosen < tail)
+        valid &= torch.arange(cand.shape[0]) < int(a["fine_lens"][done])
+        scores = torch.relu(keys[cand.clamp(0, n - 1)] @ q).masked_fill(~valid, float("-inf"))
+        raw = scores.topk(min(2048, scores.shape[0])).indices
+        lg = cand[raw]
+        phys = ntt[lg // 64] * 64 + lg % 64
+        out = lat[phys]
+        assert out.shape[0] == raw.shape[0]
+        done += 1
+    return done / (time.perf_counter() - t0), done, threads
+
+
+def gather_queries_per_second(pool, ids, table, budget_s=10.0, min_rows=8):
+    """Fancy-index gather per query (test_gather_slots_small.py:18-24) through
+    the query's page window; -1 ids give zero rows."""
+    threads = torch.get_num_threads()
+    pool_t = torch.from_numpy(pool)
+    rows = ids.shape[0]
+    done, t0 = 0, time.perf_counter()
+    while done < rows and (done < min_rows or time.perf_counter() - t0 < budget_s):
+        i = torch.from_numpy(ids[done].astype(np.int64))
+        tab = torch.from_numpy(table[done].astype(np.int64))
+        ok = i >= 0
+        phys = torch.where(ok, tab[i.clamp(min=0) >> 6] * 64 + (i.clamp(min=0) & 63), 0)
+        out = pool_t[phys]
+        out[~ok] = 0
+        done += 1
+    return done / (time.perf_counter() - t0), done, threads
+
+
+def decode_queries_per_second(q8, w, native, table, lens, topk=2048, budget_s=10.0, min_rows=4):
+    """Per request: keys of its pages, (relu(q @ k.T) * w).sum(0) * s_k, Top-2048,
+    slot map (the row gather is left out of this sample)."""
+    threads = torch.get_num_threads()
+    rows = q8.shape[0]
+    order = np.random.default_rng(0).permutation(rows)
+    done, t0 = 0, time.perf_counter()
+    while done < rows and (done < min_rows or time.perf_counter() - t0 < budget_s):
+        r = int(order[done])
+        n = int(lens[r])
+        k, s = _dequant_pages(native, table[r, : -(-n // 64)])
+        q = torch.from_numpy(q8[r]).view(torch.float8_e4m3fn).float()
+        logits = (torch.relu(q @ k[:n].T) * torch.from_numpy(w[r])[:, None]).sum(0) * s[:n]
+        idx = logits.topk(min(topk, n)).indices
+        slots = torch.from_numpy(table[r].astype(np.int64))[idx // 64] * 64 + idx % 64
+        assert slots.shape[0] == min(topk, n)
+        done += 1
+    return done / (time.perf_counter() - t0), done, threads

@@ -32,6 +32,7 @@ def test_fp8_encode_matches_torch_cast():
     ours = W.e4m3_encode(x)
     ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     assert np.array_equal(ours, ref)
+    assert np.array_equal(W.e4m3_encode_fast(x), ours)
 
 
 def test_pow2_scale_is_exact_ceiling():
