@@ -605,20 +605,6 @@ using namespace v1;
 
 extern "C" int64_t v1_score_workspace(int32_t rows) { return rows > 0 ? (int64_t)rows * kPieceRowBytes : 0; }
 
-namespace {
-// Compute units of the current device (cached per device).
-int device_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int n = 0;
-        cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
-    }
-    return cus[dev];
-}
-}  // namespace
-
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
     V1_REQUIRE(a != nullptr, "score: null args");
     V1_REQUIRE(a->heads >= 1 && a->heads <= 64, "score: heads must be in [1, 64]");
@@ -645,7 +631,7 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         // Split each row group's chunks into as few ranges as fill the chip
         // (two work-groups per CU) and keep each range within kMaxRangePages.
         const int64_t groups = cdiv(a->rows, kQueriesPerGroup);
-        int64_t nsplit = std::min<int64_t>((int64_t)chunks, std::max<int64_t>(1, cdiv(2 * device_cus(), groups)));
+        int64_t nsplit = std::min<int64_t>((int64_t)chunks, std::max<int64_t>(1, cdiv(2 * v1::device_cus(), groups)));
         nsplit = std::max<int64_t>(nsplit, cdiv((int64_t)chunks * kChunkPages, kMaxRangePages));
         p.nchunks = (int32_t)chunks;
         p.chunks_per_wg = (int32_t)cdiv((int64_t)chunks, nsplit);

@@ -27,6 +27,8 @@
 // it) the same steps run on the whole row, streamed again from cache.
 // Rows longer than 32768 columns are cut into 32768-column segments whose
 // Top-T land in a workspace; a merge work-group selects from their union.
+#include <algorithm>
+
 #include "common.h"
 
 namespace v1 {
@@ -656,13 +658,14 @@ struct V1Src {
     }
 };
 
-// Sets sm.maskpage for the ranks touching [lo, lo + kSpan) and writes -inf in
-// place for every masked position below min(take * 64, cols) in that range.
+// Sets sm.maskpage for the ranks touching [lo, lo + span) (span <= kSpan) and
+// writes -inf in place for every masked position below min(take * 64, cols)
+// in that range.
 // sglang/kernels/jit/csrc/deepseek_v4/v1_query.cuh:71-107.  Ends with a barrier.
-__device__ void v1_prepare_mask(const V1Params& p, int64_t row, const RowInfo& ri, int32_t lo, SelSmem& sm,
+__device__ void v1_prepare_mask(const V1Params& p, int64_t row, const RowInfo& ri, int32_t lo, int32_t span, SelSmem& sm,
                                 int32_t& masked_end) {
     const int t = threadIdx.x;
-    const int32_t limit = min(lo + kSpan, min(ri.take * 64, p.cols));
+    const int32_t limit = min(lo + span, min(ri.take * 64, p.cols));
     masked_end = p.mask ? max(0, limit - lo) : 0;
     const int32_t nranks = (masked_end + 63) / 64;
     for (int32_t r = t; r < nranks; r += kBlock) sm.maskpage[r] = v1_mask_page(p, row, lo / 64 + r, ri);
@@ -699,7 +702,7 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_rows(V1Params p) {
     const RowInfo ri = v1_row_info(p, row);
     const int32_t L = max(0, min(p.fine_lens[row], p.cols));
     int32_t masked_end;
-    v1_prepare_mask(p, row, ri, 0, sm, masked_end);
+    v1_prepare_mask(p, row, ri, 0, kSpan, sm, masked_end);
     const V1Src src = v1_source(p, row, ri, 0, L, masked_end, sm);
     const int32_t T = p.topk;
     if (L <= T) {
@@ -751,18 +754,34 @@ struct Workspace {
     int32_t* pos;
     int32_t* count;
     int32_t nseg;
+    int32_t seg;  // columns per segment (a multiple of 64, <= kSpan)
     int32_t T;
     __device__ __forceinline__ int64_t at(int64_t row, int32_t s) const { return (row * nseg + s) * (int64_t)T; }
 };
 
-inline int64_t workspace_bytes(int32_t batch, int32_t cols, int32_t topk) {
+// Segments of a row: the fewest that keep each within kSpan columns (more
+// segments make the merge, which selects over nseg * topk candidates, cost as
+// much as they save).  One segment means the single-pass kernel.
+struct SegPlan {
+    int32_t nseg, seg;
+};
+inline SegPlan plan_segments(int32_t batch, int32_t cols, int32_t topk) {
+    (void)batch;
+    (void)topk;
     const int64_t nseg = cdiv(cols, kSpan);
-    return (int64_t)batch * nseg * ((int64_t)topk * 8 + 4);
+    if (nseg <= 1) return SegPlan{1, cols};
+    const int64_t seg = cdiv(cdiv(cols, nseg), 64) * 64;
+    return SegPlan{(int32_t)cdiv(cols, seg), (int32_t)seg};
 }
 
-inline Workspace make_workspace(void* base, int32_t batch, int32_t cols, int32_t topk) {
+inline int64_t workspace_bytes(int32_t batch, const SegPlan& plan, int32_t topk) {
+    return plan.nseg > 1 ? (int64_t)batch * plan.nseg * ((int64_t)topk * 8 + 4) : 0;
+}
+
+inline Workspace make_workspace(void* base, int32_t batch, const SegPlan& plan, int32_t topk) {
     Workspace ws;
-    ws.nseg = (int32_t)cdiv(cols, kSpan);
+    ws.nseg = plan.nseg;
+    ws.seg = plan.seg;
     ws.T = topk;
     const int64_t pairs = (int64_t)batch * ws.nseg;
     ws.keys = static_cast<uint32_t*>(base);
@@ -811,11 +830,11 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_segments(V1Params p, Worksp
     const int64_t row = blockIdx.y;
     const RowInfo ri = v1_row_info(p, row);
     const int32_t L = max(0, min(p.fine_lens[row], p.cols));
-    const int32_t lo = s * kSpan;
+    const int32_t lo = s * ws.seg;
     int32_t masked_end;
-    v1_prepare_mask(p, row, ri, lo, sm, masked_end);
+    v1_prepare_mask(p, row, ri, lo, ws.seg, sm, masked_end);
     if (L <= p.topk) return;  // the merge kernel takes every candidate
-    const int32_t n = max(0, min(L - lo, kSpan));
+    const int32_t n = max(0, min(L - lo, ws.seg));
     segment_select(v1_source(p, row, ri, lo, n, masked_end, sm), lo, p.topk, ws, row, s, sm);
 }
 
@@ -825,8 +844,8 @@ __global__ __launch_bounds__(kBlock, 8) void transform_segments(TransformParams 
     const int64_t row = blockIdx.y;
     const int32_t L = max(0, min(p.seq_lens[row], p.cols));
     if (L <= p.topk) return;
-    const int32_t lo = s * kSpan;
-    const int32_t n = max(0, min(L - lo, kSpan));
+    const int32_t lo = s * ws.seg;
+    const int32_t n = max(0, min(L - lo, ws.seg));
     const float* rp = p.scores + row * p.score_stride + lo;
     segment_select(RowSrc{rp, n, (reinterpret_cast<uintptr_t>(rp) & 15) == 0}, lo, p.topk, ws, row, s, sm);
 }
@@ -972,14 +991,17 @@ template <typename P>
 int launch_topk(void (*single)(P), void (*seg)(P, Workspace), void (*merge)(P, Workspace), int32_t cols,
                 int32_t batch, int32_t topk, void* wsp, int64_t ws_bytes, const P& p, hipStream_t st,
                 const char* name) {
-    if (cols <= kSpan) {
+    const SegPlan plan = plan_segments(batch, cols, topk);
+    const int64_t need = workspace_bytes(batch, plan, topk);
+    // rows within one work-group's span also run in one pass when the caller
+    // gives no (or too small a) workspace for the split
+    if (plan.nseg == 1 || (cols <= kSpan && (wsp == nullptr || ws_bytes < need))) {
         hipLaunchKernelGGL(single, dim3(batch), dim3(kBlock), 0, st, p);
         return V1_LAUNCHED(name);
     }
-    V1_REQUIRE(wsp != nullptr && ws_bytes >= workspace_bytes(batch, cols, topk),
-               "%s: rows longer than %d columns need a workspace of %lld bytes", name, kSpan,
-               (long long)workspace_bytes(batch, cols, topk));
-    const Workspace ws = make_workspace(wsp, batch, cols, topk);
+    V1_REQUIRE(wsp != nullptr && ws_bytes >= need, "%s: rows longer than %d columns need a workspace of %lld bytes",
+               name, kSpan, (long long)need);
+    const Workspace ws = make_workspace(wsp, batch, plan, topk);
     V1_REQUIRE((int64_t)ws.nseg * topk <= kSpan, "%s: %d columns exceed the %lld supported at topk %d", name, cols,
                (long long)(kSpan / topk) * kSpan, topk);
     hipLaunchKernelGGL(seg, dim3(ws.nseg, batch), dim3(kBlock), 0, st, p, ws);
@@ -995,8 +1017,8 @@ int launch_topk(void (*single)(P), void (*seg)(P, Workspace), void (*merge)(P, W
 using namespace v1;
 
 extern "C" int64_t v1_topk_workspace(int32_t batch, int32_t cols, int32_t topk) {
-    if (cols <= kSpan || batch <= 0 || topk <= 0) return 0;
-    return workspace_bytes(batch, cols, topk);
+    if (batch <= 0 || topk <= 0 || cols <= 0) return 0;
+    return workspace_bytes(batch, plan_segments(batch, cols, topk), topk);
 }
 
 extern "C" int v1_topk(const v1_topk_args* a, void* stream) {

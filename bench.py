@@ -59,7 +59,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=4, choices=[1, 3, 4, 5])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",

@@ -79,9 +79,9 @@ def test_validation_messages(lib):
 
 def test_workspace_sizes_are_host_arithmetic(lib):
     h = lib.lib()
-    assert h.v1_topk_workspace(8, 32768, 2048) == 0          # one work-group per row, no workspace
-    small = h.v1_topk_workspace(8, 65536, 2048)
-    assert small > 0 and h.v1_topk_workspace(16, 65536, 2048) >= 2 * small - 1024
+    assert h.v1_topk_workspace(4096, 32768, 2048) == 0       # large batch: one work-group per row
+    assert h.v1_topk_workspace(4096, 65536, 2048) == 4096 * 2 * (2048 * 8 + 4)
+    assert h.v1_topk_workspace(128, 131072, 2048) == 128 * 4 * (2048 * 8 + 4)
     assert h.v1_score_workspace(4096) >= 4096 * (8 * 128 + 8 * 4)
 
 
