@@ -80,6 +80,13 @@ _SIGNATURES = {
     "v1_allocate": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _vp, _vp]),
     "v1_publish": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i64, _vp]),
     "v1_release": (_c_i32, [_vp, _vp, _vp, _vp, _c_i32, _vp]),
+    "v1_sort_pairs_u64_workspace": (_c_i64, [_c_i64]),
+    "v1_sort_pairs_u64": (_c_i32, [_vp, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _c_i64, _vp]),
+    "v1_page_insert_workspace": (_c_i64, [_c_i32, _c_i32]),
+    "v1_page_insert": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _c_i32, _c_i64, _vp, _vp, _vp, _c_i32, _vp, _vp, _vp,
+                                _c_i64, _vp]),
+    "v1_page_release_workspace": (_c_i64, [_c_i32]),
+    "v1_page_release": (_c_i32, [_vp, _c_i32, _vp, _vp, _vp, _c_i32, _vp, _vp, _c_i64, _vp]),
     "v1_query_metadata": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                    _c_i32, _c_i32, _vp]),
     "v1_query_lengths": (_c_i32, [_vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),

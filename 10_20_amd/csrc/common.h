@@ -3,6 +3,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <algorithm>
 #include <stdarg.h>
 #include <stdio.h>
 #include "../../include/v1idx.h"
@@ -25,6 +27,16 @@ int hip_status(hipError_t e, const char* what);
 #define V1_LAUNCHED(what) ::v1::hip_status(hipGetLastError(), what)
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Device-wide primitives (sort64.hip) shared by the batched page manager.
+// sort_pairs: stable ascending sort of (uint64 key, uint32 value) pairs.
+int64_t sort_pairs_workspace(int64_t n);
+int sort_pairs(const uint64_t* keys, const uint32_t* vals, uint64_t* keys_out, uint32_t* vals_out, int64_t n,
+               int key_bits, void* ws, int64_t ws_bytes, hipStream_t st, const char* name);
+// scan_exclusive: out[i] = sum of in[0..i), *total = sum of all (device pointers).
+int64_t scan_workspace(int64_t n);
+int scan_exclusive(const uint32_t* in, uint32_t* out, uint32_t* total, int64_t n, void* ws, int64_t ws_bytes,
+                   hipStream_t st, const char* name);
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

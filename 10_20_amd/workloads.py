@@ -147,6 +147,55 @@ def config1(seed=19, rows=1024):
              WIDTH=2688))
 
 
+def splitmix64(x):
+    """SplitMix64 finaliser (Steele, Lea, Flood 2014) of uint64 values."""
+    z = np.asarray(x, dtype=np.uint64) + np.uint64(0x9E3779B97F4A7C15)
+    with np.errstate(over="ignore"):
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def config2(seed=2, requests=4096, max_pages=64, capacity=65536, zipf=1.1, collide=0, release_frac=0.5):
+    """Page management: `requests` requests of U{1..max_pages} pages; each page
+    is a Zipf(zipf) draw d (many pages shared), its key splitmix64(d) as int64
+    and its bytes a function of d (config2_payload).  `collide` rarely-drawn
+    pages get the key of another draw (equal key, other bytes).  `released`
+    marks a seeded `release_frac` of the requests whose pages are released
+    after the insert (config2_release_list).  Pages hold 64 MLA rows of 656
+    bytes (41984 B)."""
+    g = rng(seed)
+    lens = g.integers(1, max_pages + 1, requests)
+    n = int(lens.sum())
+    draws = g.zipf(zipf, n).astype(np.uint64)
+    uniq, inv, counts = np.unique(draws, return_inverse=True, return_counts=True)
+    ukeys = splitmix64(uniq).view(np.int64)
+    if collide:
+        rare = np.flatnonzero(counts <= 3)
+        victims = g.choice(rare, collide, replace=False)
+        donors = g.choice(len(uniq), collide)
+        donors = np.where(donors == victims, (donors + 1) % len(uniq), donors)
+        ukeys = ukeys.copy()
+        ukeys[victims] = ukeys[donors]
+    req = np.repeat(np.arange(requests, dtype=np.int32), lens)
+    released = g.random(requests) < release_frac
+    return Workload("config2", seed, dict(lens=lens.astype(np.int32), req=req, draw=inv.astype(np.int32),
+                                          keys=ukeys[inv], ukeys=ukeys, released=released),
+                    dict(requests=requests, entries=n, distinct=len(uniq), capacity=capacity,
+                         page_bytes=PAGE * MLA_ROW_BYTES))
+
+
+def config2_payload(wl, page_bytes):
+    """uint8 [distinct, page_bytes]: the bytes of each distinct draw (seeded)."""
+    return rng(wl.seed + 1000).integers(0, 256, size=(wl.params["distinct"], page_bytes), dtype=np.uint8)
+
+
+def config2_release_list(wl, table):
+    """Pages of the released requests, in request order."""
+    sel = wl.arrays["released"][wl.arrays["req"]]
+    return np.asarray(table)[sel].astype(np.int32)
+
+
 def config3(seed=3, rows=1024, pool_tokens=1 << 20, window_pages=512, pad=0.05):
     """K/V slot gather: 656-byte rows of a 1M-token paged pool; each query has
     its own 512-page request window (random pages of the pool) and 2048 ids

@@ -241,6 +241,50 @@ int v1_release(const int32_t* table, int32_t* refs, int32_t* free_stack, int32_t
                int32_t pages, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Device-wide stable sort of (uint64 key, uint32 value) pairs, ascending by
+ * key, equal keys in input order: the int64-key grouping of _sort
+ * (sglang/srt/layers/attention/v1_native/fused_grouping.py:64-76) over a whole
+ * batch of page keys rather than one 4096-key group.  key_bits: the low bits
+ * that may differ (64 for arbitrary keys).  Outputs must not alias inputs.
+ * ---------------------------------------------------------------------- */
+int64_t v1_sort_pairs_u64_workspace(int64_t n);
+int v1_sort_pairs_u64(const uint64_t* keys, const uint32_t* vals, uint64_t* keys_out,
+                      uint32_t* vals_out, int64_t n, int32_t key_bits, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Batched page manager: match_pages -> allocate -> publish for a batch of
+ * requests (kernels.py:72-167, host order runtime.py:230-270), and release
+ * (kernels.py:170-179) of a list of pages.  The results equal running the
+ * per-lease kernels request after request:
+ *   - entry e (page bytes tmp[e], int64 key keys[e], request req[e], req
+ *     non-decreasing) takes the lowest live page with equal key and equal
+ *     bytes; live = refs > 0 before the batch or published by an earlier
+ *     request of the batch; entries of one request never match each other;
+ *   - unmatched entries take free_stack[count - 1 - rank] in entry order;
+ *   - table[e] = page, refs[page] += 1, fresh pages get the bytes and key.
+ * The key stands in for the reference's (h0, h1) fingerprint.  Release
+ * decrements in list order; a page that reaches 0 is pushed on the free stack
+ * in list order.  A batch that fails (status bits below, OR-ed into *status)
+ * leaves pool, keys, refs, free stack and count unchanged.  page_bytes is a
+ * multiple of 16 (41984 for 64 MLA rows of 656 bytes, 8448 for native pages).
+ * ---------------------------------------------------------------------- */
+#define V1_STATUS_EXHAUSTED 1   /* free stack smaller than the fresh pages needed */
+#define V1_STATUS_COLLISIONS 2  /* more than 4096 entries whose key collides with other bytes */
+#define V1_STATUS_BAD_ORDER 4   /* req decreases */
+#define V1_STATUS_UNDERFLOW 8   /* release of a page whose count is 0, or a page id out of range */
+#define V1_STATUS_BAD_STATE 16  /* count outside [0, capacity] or a free-stack page id out of range */
+int64_t v1_page_insert_workspace(int32_t capacity, int32_t n);
+int v1_page_insert(uint8_t* pool, int64_t* pool_keys, int32_t* refs, int32_t* free_stack,
+                   int32_t* count, int32_t capacity, int64_t page_bytes, const int64_t* keys,
+                   const uint8_t* tmp, const int32_t* req, int32_t n, int32_t* table,
+                   int32_t* status, void* workspace, int64_t workspace_bytes, void* stream);
+int64_t v1_page_release_workspace(int32_t n);
+int v1_page_release(const int32_t* pages, int32_t n, int32_t* refs, int32_t* free_stack,
+                    int32_t* count, int32_t capacity, int32_t* status, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Query metadata, fine page tables and shared tail staging:
  * query_metadata    sglang/srt/layers/attention/v1_deepseek/kernels.py:568-591
  * query_lengths     kernels.py:224-245

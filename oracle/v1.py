@@ -382,6 +382,63 @@ def release(table, refs, free, count):
     return count + len(dead)
 
 
+def page_insert_batch(pool, pool_keys, refs, free, count, keys, tmp, req):
+    """match_pages -> allocate -> publish (kernels.py:72-167) called request
+    after request (runtime.py:230-270) with an int64 key in place of the
+    (h0, h1) fingerprint.  An entry takes the lowest live page (refs > 0) with
+    equal key and bytes; entries of one request are not matched against each
+    other; unmatched entries take free[count-1-rank].  All or nothing: raises
+    RuntimeError (state untouched) when the free stack runs out.  Returns
+    (table, pool, pool_keys, refs, free, new_count) as new arrays."""
+    pool, pool_keys, refs, free = pool.copy(), pool_keys.copy(), refs.copy(), free.copy()
+    n = len(keys)
+    table = np.empty(n, dtype=np.int32)
+    live = {}
+    for p in np.nonzero(refs > 0)[0]:
+        live.setdefault(int(pool_keys[p]), []).append(int(p))
+    bounds = np.flatnonzero(np.diff(np.asarray(req, dtype=np.int64))) + 1
+    starts = np.concatenate([[0], bounds]).astype(np.int64) if n else np.zeros(0, np.int64)
+    ends = np.concatenate([bounds, [n]]).astype(np.int64) if n else np.zeros(0, np.int64)
+    for s, e in zip(starts, ends):
+        match = np.full(e - s, -1, dtype=np.int64)
+        for i in range(s, e):
+            for p in sorted(live.get(int(keys[i]), ())):
+                if np.array_equal(pool[p], tmp[i]):
+                    match[i - s] = p
+                    break
+        fresh = match < 0
+        need = int(fresh.sum())
+        if count < need:
+            raise RuntimeError("V1 DeepSeek page arena exhausted")
+        rank = np.cumsum(fresh) - 1
+        dst = np.where(fresh, free[np.clip(count - 1 - rank, 0, None)], match)
+        count -= need
+        np.add.at(refs, dst, 1)
+        table[s:e] = dst
+        for i in np.flatnonzero(fresh) + s:
+            p = int(table[i])
+            pool[p] = tmp[i]
+            pool_keys[p] = keys[i]
+            live.setdefault(int(keys[i]), []).append(p)
+    return table, pool, pool_keys, refs, free, count
+
+
+def page_release_batch(pages, refs, free, count):
+    """release (kernels.py:170-179) of a list of pages in list order; raises
+    RuntimeError (state untouched) when a page has no reference left or is out
+    of range.  Returns (refs, free, new_count) as new arrays."""
+    refs, free = refs.copy(), free.copy()
+    pages = np.asarray(pages, dtype=np.int64)
+    if len(pages):
+        if pages.min() < 0 or pages.max() >= len(refs):
+            raise RuntimeError("page release of an id out of range")
+        u, c = np.unique(pages, return_counts=True)
+        if np.any(refs[u] < c):
+            raise RuntimeError("page release underflow")
+    count = release(pages, refs, free, count)
+    return refs, free, count
+
+
 # ---------------------------------------------------------------- gather
 def gather_slots(k_pool, v_pool, req, ids, head):
     """sglang/srt/layers/attention/v1_native/kernels.py:62-77 -> (kg, vg) [rows, top, 1, 128]."""

@@ -407,3 +407,123 @@ def test_score_formula_order_by_hand():
     assert np.isneginf(out[0, 1:]).all()
     signed = O.paged_logits(q8, w, native, np.int32([[0]]), np.int32([1]), 1, relu=False)
     assert signed[0, 0] == pytest.approx((0.5 * 2 - 7.0 * 3) * 0.25)
+
+
+# ------------------------------------------------- batched page manager
+def _per_request_chain(pool, pool_keys, refs, free, count, keys, tmp, req):
+    """The pinned per-lease oracle functions (match_pages, allocate, publish)
+    called request after request, with the key as h0 and h1 = 0, members 0."""
+    pool, pool_keys, refs, free = pool.copy(), pool_keys.copy(), refs.copy(), free.copy()
+    cap = len(refs)
+    members = np.zeros((cap, 64), np.int32)
+    table = np.empty(len(keys), np.int32)
+    for r in np.unique(req):
+        sel = np.flatnonzero(req == r)
+        t, mp = tmp[sel], np.zeros((len(sel), 64), np.int32)
+        h = np.stack([keys[sel], np.zeros(len(sel), np.int64)], 1)
+        hashes = np.stack([pool_keys, np.zeros(cap, np.int64)], 1)
+        m = O.match_pages(t, mp, h, pool, members, hashes, refs, cap)
+        tables = np.full(len(sel), -1, np.int32)
+        count, fresh = O.allocate(0, m, free, count, refs, tables)
+        centers_tmp = np.zeros((-(-len(sel) * 8 // 64), 8448), np.uint8)
+        O.publish(0, t, centers_tmp, mp, h, tables, fresh, pool, np.zeros_like(centers_tmp), members, hashes)
+        pool_keys = hashes[:, 0].copy()
+        table[sel] = tables
+    return table, pool, pool_keys, refs, free, count
+
+
+def _small_pool_case(seed, cap=160, requests=24, max_pages=9, page_bytes=32, collide=4):
+    wl = W.config2(seed=seed, requests=requests, max_pages=max_pages, capacity=cap, collide=collide)
+    a = wl.arrays
+    payload = W.config2_payload(wl, page_bytes)
+    return wl, a["keys"], payload[a["draw"]], a["req"]
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_page_insert_batch_equals_per_request_chain(seed):
+    wl, keys, tmp, req = _small_pool_case(seed)
+    cap = 160
+    g = np.random.default_rng(seed)
+    # pre-live pages: some hold batch keys (same or other bytes), some are unrelated
+    pool = g.integers(0, 256, (cap, tmp.shape[1]), dtype=np.uint8)
+    pool_keys = g.integers(-2**62, 2**62, cap)
+    refs = np.zeros(cap, np.int32)
+    pick = g.choice(len(keys), 12, replace=False)
+    live = g.choice(cap, 24, replace=False)
+    pool[live[:12]] = tmp[pick]
+    pool_keys[live[:12]] = keys[pick]
+    pool_keys[live[12:18]] = keys[pick[:6]]          # equal key, other bytes: collision with a live page
+    refs[live] = g.integers(1, 4, 24)
+    free_pages = np.setdiff1d(np.arange(cap), live)
+    free = np.concatenate([g.permutation(free_pages), np.full(len(live), -7)]).astype(np.int32)
+    count = len(free_pages)
+    got = O.page_insert_batch(pool, pool_keys, refs, free, count, keys, tmp, req)
+    exp = _per_request_chain(pool, pool_keys, refs, free, count, keys, tmp, req)
+    for x, y in zip(got, exp):
+        assert np.array_equal(x, y)
+    table, pool2, _, refs2, free2, count2 = got
+    # invariants: every entry holds one reference; table pages hold the entry's bytes
+    assert (refs2 - refs).sum() == len(keys) and np.array_equal(np.bincount(table, minlength=cap), refs2 - refs)
+    assert np.array_equal(pool2[table], tmp)
+    assert sorted(free2[:count2].tolist() + np.flatnonzero(refs2 > 0).tolist()) == list(range(cap))
+
+
+def test_page_insert_batch_lifecycle_kat(kats):
+    """The reference lifecycle (test_page_management_and_tail_small.py:14-57)
+    as two one-request batches and two releases."""
+    kat = kats["page_lifecycle"]
+    cap = kat["capacity"]
+    tmp = np.repeat(np.arange(16, dtype=np.uint8)[:, None], 8448, axis=1)
+    keys = np.arange(16, dtype=np.int64) * 1000003
+    req = np.zeros(16, np.int32)
+    state = (np.zeros_like(tmp), np.zeros(cap, np.int64), np.zeros(cap, np.int32), np.arange(cap, dtype=np.int32),
+             cap)
+    t0, pool, pk, refs, free, count = O.page_insert_batch(*state, keys, tmp, req)
+    assert t0.tolist() == kat["first_table"] and count == kat["count_after_first"]
+    assert (refs == kat["refs_after_first"]).all()
+    t1, pool, pk, refs, free, count = O.page_insert_batch(pool, pk, refs, free, count, keys, tmp, req)
+    assert t1.tolist() == t0.tolist() and (refs == kat["refs_after_second"]).all() and count == 0
+    refs, free, count = O.page_release_batch(t0, refs, free, count)
+    assert count == 0 and (refs == kat["refs_after_release_a"]).all()
+    refs, free, count = O.page_release_batch(t1, refs, free, count)
+    assert count == kat["count_after_release_b"] and sorted(free.tolist()) == list(range(16))
+
+
+def test_page_insert_batch_same_request_duplicates_take_fresh_pages():
+    """Entries of one request never match each other (match_pages only sees
+    live pages, kernels.py:72-113); a later request takes the lowest of them."""
+    tmp = np.zeros((5, 16), np.uint8)
+    keys = np.full(5, 42, np.int64)
+    req = np.int32([0, 0, 0, 1, 1])
+    t, pool, pk, refs, free, count = O.page_insert_batch(
+        np.zeros((8, 16), np.uint8), np.zeros(8, np.int64), np.zeros(8, np.int32), np.arange(8, dtype=np.int32), 8,
+        keys, tmp, req)
+    assert t.tolist() == [7, 6, 5, 5, 5] and count == 5 and refs.tolist() == [0] * 5 + [3, 1, 1]
+
+
+def test_page_insert_batch_exhaustion_is_all_or_nothing():
+    tmp = np.arange(6, dtype=np.uint8)[:, None].repeat(16, 1)
+    with pytest.raises(RuntimeError, match="exhausted"):
+        O.page_insert_batch(np.zeros((4, 16), np.uint8), np.zeros(4, np.int64), np.zeros(4, np.int32),
+                            np.arange(4, dtype=np.int32), 4, np.arange(6, dtype=np.int64), tmp,
+                            np.int32([0, 0, 0, 1, 1, 1]))
+
+
+def test_page_release_batch_underflow_and_order():
+    refs = np.int32([2, 1, 1, 0])
+    free = np.full(8, -9, np.int32)
+    refs2, free2, count = O.page_release_batch(np.int32([0, 1, 0, 2]), refs, free, 3)
+    assert count == 6 and free2[3:6].tolist() == [1, 0, 2] and refs2.tolist() == [0, 0, 0, 0]
+    assert refs.tolist() == [2, 1, 1, 0]  # inputs untouched
+    with pytest.raises(RuntimeError, match="underflow"):
+        O.page_release_batch(np.int32([0, 0, 0]), refs, free, 3)
+    with pytest.raises(RuntimeError, match="out of range"):
+        O.page_release_batch(np.int32([4]), refs, free, 3)
+
+
+def test_config2_shape():
+    wl = W.config2()
+    p = wl.params
+    assert p["requests"] == 4096 and 125000 < p["entries"] < 140000 and p["distinct"] < p["capacity"]
+    assert p["page_bytes"] == 41984 and wl.arrays["keys"].dtype == np.int64
+    assert np.all(np.diff(wl.arrays["req"]) >= 0)
