@@ -85,7 +85,7 @@ _SIGNATURES = {
     "v1_page_insert_workspace": (_c_i64, [_c_i32, _c_i32]),
     "v1_page_insert": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _c_i32, _c_i64, _vp, _vp, _vp, _c_i32, _vp, _vp, _vp,
                                 _c_i64, _vp]),
-    "v1_page_release_workspace": (_c_i64, [_c_i32]),
+    "v1_page_release_workspace": (_c_i64, [_c_i32, _c_i32]),
     "v1_page_release": (_c_i32, [_vp, _c_i32, _vp, _vp, _vp, _c_i32, _vp, _vp, _c_i64, _vp]),
     "v1_query_metadata": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                    _c_i32, _c_i32, _vp]),
@@ -94,6 +94,8 @@ _SIGNATURES = {
                                _vp]),
     "v1_stage_tail": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64,
                                _c_i64, _vp]),
+    "v1_stage_tail_rows": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                    _c_i64, _c_i64, _c_i32, _vp]),
     "v1_mask_fine": (_c_i32, [_vp, _c_i64, _vp, _c_i32, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32,
                               _c_i32, _c_i32, _vp]),
     "v1_output_ids": (_c_i32, [_vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i32,

@@ -333,6 +333,45 @@ __global__ __launch_bounds__(256) void stage_tail_kernel(const uint8_t* native, 
     }
 }
 
+// stage_tail over pages of 64 rows of row_bytes each (MLA latent rows of 656
+// bytes: 512 FP8 + 64 bf16 RoPE + fp32 scales), the same slot rule as
+// stage_tail_kernel with one contiguous row per token instead of 128 key bytes
+// plus a separate scale.  Rows are 16-byte multiples; chunk c of the page is
+// part c % parts of slot c / parts.
+__global__ __launch_bounds__(256) void stage_tail_rows_kernel(const uint8_t* native, const int32_t* nt,
+                                                              const int32_t* lens, uint8_t* fine,
+                                                              const int32_t* tail_rows, int32_t capacity, int32_t np,
+                                                              int32_t scratch, int32_t sink_cap, int32_t window,
+                                                              int64_t native_pages, int64_t fine_pages,
+                                                              int32_t row_bytes) {
+    const int64_t row = blockIdx.x;
+    const int32_t p = blockIdx.y;
+    if (tail_rows != nullptr && tail_rows[row] != row) return;
+    const int32_t n = lens[row];
+    const int32_t sink = min(n, sink_cap);
+    const int32_t tail = max(sink, min(max(n - 1, 0) / 1024 * 1024, max(sink, n - window)));
+    const int32_t count = sink + n - tail;
+    if (!(p * 64 < count || p == 0)) return;
+    const int64_t dst = capacity + row * scratch + p;
+    if (dst >= fine_pages) return;
+    const int64_t page_bytes = (int64_t)row_bytes * 64;
+    const int32_t parts = row_bytes / 16;
+    u32x4* out = reinterpret_cast<u32x4*>(fine + dst * page_bytes);
+    for (int32_t c = threadIdx.x; c < 64 * parts; c += 256) {
+        const int32_t slot = c / parts, part = c - slot * parts;
+        const int32_t i = p * 64 + slot;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (i < count) {
+            const int32_t logical = i < sink ? i : tail + i - sink;
+            const int32_t e = logical / 64;
+            const int64_t page = e < np ? nt[row * np + e] : -1;
+            if (page >= 0 && page < native_pages)
+                v = reinterpret_cast<const u32x4*>(native + page * page_bytes + (int64_t)(logical % 64) * row_bytes)[part];
+        }
+        out[c] = v;
+    }
+}
+
 }  // namespace
 }  // namespace v1
 
@@ -426,4 +465,19 @@ extern "C" int v1_stage_tail(const uint8_t* native, const int32_t* nt, const int
     hipLaunchKernelGGL(stage_tail_kernel, dim3(rows, scratch), dim3(256), 0, as_stream(stream), native, nt, lens, fine,
                        tail_rows, capacity, np, scratch, sink, window, native_pages, fine_pages);
     return V1_LAUNCHED("stage_tail");
+}
+
+extern "C" int v1_stage_tail_rows(const uint8_t* native, const int32_t* nt, const int32_t* lens, uint8_t* fine,
+                                  const int32_t* tail_rows, int32_t rows, int32_t capacity, int32_t np,
+                                  int32_t scratch, int32_t sink, int32_t window, int64_t native_pages,
+                                  int64_t fine_pages, int32_t row_bytes, void* stream) {
+    V1_REQUIRE(rows >= 0 && np > 0 && scratch > 0 && capacity >= 0, "stage_tail_rows: bad shape");
+    V1_REQUIRE(row_bytes > 0 && row_bytes % 16 == 0, "stage_tail_rows: row_bytes must be a positive multiple of 16");
+    V1_REQUIRE((reinterpret_cast<uintptr_t>(native) & 15) == 0 && (reinterpret_cast<uintptr_t>(fine) & 15) == 0,
+               "stage_tail_rows: pools must be 16-byte aligned");
+    if (rows == 0) return V1_OK;
+    V1_REQUIRE(native && nt && lens && fine, "stage_tail_rows: null buffer");
+    hipLaunchKernelGGL(stage_tail_rows_kernel, dim3(rows, scratch), dim3(256), 0, as_stream(stream), native, nt, lens,
+                       fine, tail_rows, capacity, np, scratch, sink, window, native_pages, fine_pages, row_bytes);
+    return V1_LAUNCHED("stage_tail_rows");
 }

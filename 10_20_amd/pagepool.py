@@ -28,13 +28,19 @@ def _check_i32(name, t, n=None):
 
 
 class PagePool:
-    def __init__(self, capacity, page_bytes, device="cuda"):
-        if capacity <= 0 or page_bytes <= 0 or page_bytes % 16:
+    """`capacity` managed pages, followed in the same byte pool by
+    `scratch_pages` pages that the manager never hands out (the tail scratch
+    region that stage_tail writes from page `capacity` on)."""
+
+    def __init__(self, capacity, page_bytes, device="cuda", scratch_pages=0):
+        if capacity <= 0 or page_bytes <= 0 or page_bytes % 16 or scratch_pages < 0:
             raise ValueError("capacity must be positive and page_bytes a positive multiple of 16")
         device = torch.device(device)
         self.capacity = int(capacity)
         self.page_bytes = int(page_bytes)
-        self.pool = torch.zeros(self.capacity, self.page_bytes, dtype=torch.uint8, device=device)
+        self.pages = torch.zeros(self.capacity + int(scratch_pages), self.page_bytes, dtype=torch.uint8,
+                                 device=device)
+        self.pool = self.pages[:self.capacity]
         self.keys = torch.zeros(self.capacity, dtype=torch.int64, device=device)
         self.refs = torch.zeros(self.capacity, dtype=torch.int32, device=device)
         self.free = torch.arange(self.capacity, dtype=torch.int32, device=device)
@@ -44,6 +50,13 @@ class PagePool:
     @property
     def device(self):
         return self.pool.device
+
+    def reset(self):
+        """Every page free (free stack 0..capacity-1, page 0 popped last), no
+        references; page bytes and keys are left as they are."""
+        self.refs.zero_()
+        torch.arange(self.capacity, dtype=torch.int32, device=self.device, out=self.free)
+        self.count.fill_(self.capacity)
 
     def status(self, clear=True):
         """Failure bits OR-ed by the calls since the last clear (reads the device)."""
@@ -91,7 +104,7 @@ class PagePool:
         _lib.require_gpu(pages, self.pool)
         _check_i32("pages", pages)
         n = pages.numel()
-        nbytes = _lib.lib().v1_page_release_workspace(n)
+        nbytes = _lib.lib().v1_page_release_workspace(self.capacity, n)
         wp, wn = workspace(self.device, nbytes, "page_release")
         _lib.call("v1_page_release", _lib.ptr(pages), n, _lib.ptr(self.refs), _lib.ptr(self.free),
                   _lib.ptr(self.count), self.capacity, _lib.ptr(self.status_word), wp, wn,
@@ -115,3 +128,23 @@ def sort_pairs_u64(keys, vals):
     _lib.call("v1_sort_pairs_u64", _lib.ptr(keys), _lib.ptr(vals), _lib.ptr(ko), _lib.ptr(vo), n, 64, wp, wn,
               _lib.stream_of(keys))
     return ko, vo
+
+
+def stage_tail_rows(native, nt, lens, fine, tail_rows, capacity, scratch, sink=64, window=64):
+    """stage_tail_shared (kernels.py:518-564; tail_rows None: stage_tail
+    :407-441) over uint8 pools [pages, 64 * row_bytes] of row pages: owner row r
+    copies its sink and tail tokens to pages capacity + r * scratch + p."""
+    _lib.require_gpu(native, nt, lens, fine, tail_rows)
+    if native.dtype != torch.uint8 or fine.dtype != torch.uint8 or native.dim() != 2 or fine.dim() != 2:
+        raise ValueError("native and fine must be uint8 [pages, 64 * row_bytes] tensors")
+    if native.shape[1] != fine.shape[1] or native.shape[1] % (64 * 16):
+        raise ValueError("pages must hold 64 rows of a multiple of 16 bytes, equal in both pools")
+    if not (native.is_contiguous() and fine.is_contiguous()):
+        raise ValueError("native and fine must be contiguous")
+    _check_i32("nt", nt)
+    _check_i32("lens", lens, nt.shape[0])
+    if tail_rows is not None:
+        _check_i32("tail_rows", tail_rows, nt.shape[0])
+    _lib.call("v1_stage_tail_rows", _lib.ptr(native), _lib.ptr(nt), _lib.ptr(lens), _lib.ptr(fine),
+              _lib.ptr(tail_rows), nt.shape[0], int(capacity), nt.shape[1], int(scratch), int(sink), int(window),
+              native.shape[0], fine.shape[0], native.shape[1] // 64, _lib.stream_of(native))

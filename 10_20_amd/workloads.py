@@ -196,6 +196,23 @@ def config2_release_list(wl, table):
     return np.asarray(table)[sel].astype(np.int32)
 
 
+def config2_tails(wl, table, seed_offset=7):
+    """Tail staging inputs of the page-management workload: request pairs
+    (2k, 2k+1) share one tail (tail_rows[2k+1] = 2k), each request's native
+    table lists its own pages (cycled), and its length n = 1024 j + 64 tokens
+    (j in 1..3) gives a 128-token tail (64 sink + 64 tail slots, two pages)."""
+    g = rng(wl.seed + seed_offset)
+    lens_p = wl.arrays["lens"]
+    R = len(lens_p)
+    starts = np.concatenate([[0], np.cumsum(lens_p)[:-1]])
+    n = np.repeat(1024 * g.integers(1, 4, (R + 1) // 2) + 64, 2)[:R].astype(np.int32)
+    np_ = int(-(-int(n.max()) // PAGE))
+    cols = np.arange(np_)
+    nt = np.asarray(table)[starts[:, None] + cols[None, :] % lens_p[:, None]].astype(np.int32)
+    tail_rows = (np.arange(R) // 2 * 2).astype(np.int32)
+    return dict(nt=nt, lens=n, tail_rows=tail_rows, np=np_, scratch=2)
+
+
 def config3(seed=3, rows=1024, pool_tokens=1 << 20, window_pages=512, pad=0.05):
     """K/V slot gather: 656-byte rows of a 1M-token paged pool; each query has
     its own 512-page request window (random pages of the pool) and 2048 ids

@@ -10,6 +10,9 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
   1            the reference example shape: 1024 queries x 1 head; coarse score over
                centers -> route (40 of 64 pages, fine table) -> shared tail staging ->
                fine score over 2688 candidates -> fused Top-2048 with mask -> gather
+  2            page management: 4096 requests (~132 K Zipf page keys) -> stable key grouping,
+               match -> allocate -> publish into a 65536-page pool of 41984-byte pages,
+               128-token tail staging for owner pairs, release of half the requests
   3            K/V slot gather: 1024 x 2048 ids (5% padding) through per-query
                512-page windows of a 1M-token pool of 656-byte rows
   5            decode batch: 128 requests x 64 heads, contexts 4K..128K tokens with
@@ -60,7 +63,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=4, choices=[1, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES bytes (HBM counter calibration) and exit")
@@ -81,7 +84,7 @@ def copy_calibration(nbytes):
 
 class Pkg:
     def __init__(self):
-        for name in ("workloads", "scoring", "topk", "native_kernels", "query_fused", "kernels"):
+        for name in ("workloads", "scoring", "topk", "native_kernels", "query_fused", "kernels", "pagepool"):
             setattr(self, name, importlib.import_module(f"10_20_amd.{name}"))
 
 
@@ -251,7 +254,64 @@ def setup_decode(P, dev, torch, np):
     return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 5)"
 
 
-SETUPS = {1: setup_example, 3: setup_gather, 4: setup_prefill, 5: setup_decode}
+def setup_pages(P, dev, torch, np):
+    """Configuration 2: page management (grouping, match -> allocate -> publish,
+    tail staging, release) for a batch of 4096 requests."""
+    wl = P.workloads.config2()
+    a, prm = wl.arrays, wl.params
+    R, cap, pb = prm["requests"], prm["capacity"], prm["page_bytes"]
+    n = prm["entries"]
+    gen = torch.Generator(device=dev).manual_seed(wl.seed)
+    uniq = torch.randint(0, 256, (prm["distinct"], pb), generator=gen, device=dev, dtype=torch.uint8)
+    tmp = uniq[torch.from_numpy(a["draw"]).to(dev).long()]
+    del uniq
+    keys = torch.from_numpy(a["keys"]).to(dev)
+    req = torch.from_numpy(a["req"]).to(dev)
+    table = torch.empty(n, device=dev, dtype=torch.int32)
+    # one insert to fix the table the release list and the tail tables are drawn from
+    probe = P.pagepool.PagePool(cap, pb, dev)
+    probe.insert(keys, tmp, req, table)
+    if probe.status():
+        raise RuntimeError("page-management workload does not fit the pool")
+    t_host = table.cpu().numpy()
+    fresh = int(cap - probe.count.item())
+    del probe
+    tails = P.workloads.config2_tails(wl, t_host)
+    rel = torch.from_numpy(P.workloads.config2_release_list(wl, t_host)).to(dev)
+    pool = P.pagepool.PagePool(cap, pb, dev, scratch_pages=R * tails["scratch"])
+    nt = torch.from_numpy(tails["nt"]).to(dev)
+    tl = torch.from_numpy(tails["lens"]).to(dev)
+    owners = torch.from_numpy(tails["tail_rows"]).to(dev)
+    stages = [
+        ("reset", pool.reset),
+        ("insert", lambda: pool.insert(keys, tmp, req, table)),
+        ("stage", lambda: P.pagepool.stage_tail_rows(pool.pages, nt, tl, pool.pages, owners, cap,
+                                                     tails["scratch"])),
+        ("release", lambda: pool.release(rel)),
+    ]
+    owners_n = int((tails["tail_rows"] == np.arange(R)).sum())
+    work_units = {
+        "reset": (12.0 * cap / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        # every entry's page is read at least once (compared or copied), fresh pages written once
+        "insert": (((n + fresh) * pb + 8.0 * n) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "stage": (2.0 * owners_n * 2 * pb / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "release": (16.0 * rel.numel() / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+    }
+
+    def cpu(budget):
+        from oracle import cpu_baseline
+        rps, done, threads = cpu_baseline.pages_requests_per_second(a["keys"], a["draw"], a["lens"], cap, pb,
+                                                                    budget)
+        return rps, threads, f"{done} of {R} requests (match -> allocate -> publish from an empty pool)"
+
+    meta = {"workload": f"page management: {R} requests of 1-64 pages ({n} Zipf(1.1) page keys, {fresh} distinct "
+                        f"pages) into a {cap}-page pool of 41984-byte pages, 128-token tail staging of "
+                        f"{owners_n} owner requests, release of {rel.numel()} pages",
+            "global_batch": R, "seq_len": int(prm['entries']), "parallelism": "single GPU"}
+    return R, stages, work_units, cpu, meta, "synthetic (PCG64 seed 2; page bytes from a seeded torch generator)"
+
+
+SETUPS = {1: setup_example, 2: setup_pages, 3: setup_gather, 4: setup_prefill, 5: setup_decode}
 
 
 def main():
@@ -307,16 +367,17 @@ def main():
     amount, unit, peak, bound = work_units[dom]
     achieved = amount / (stage_ms[dom] / 1e3)
 
+    rate_unit = "requests/s" if args.config == 2 else "queries/s"
     cpu = None
     if args.cpu_budget > 0:
         qps_cpu, threads, sample = cpu_fn(args.cpu_budget)
-        cpu = {"value": round(qps_cpu, 3), "unit": "queries/s", "cores": threads, "kind": "port",
+        cpu = {"value": round(qps_cpu, 3), "unit": rate_unit, "cores": threads, "kind": "port",
                "sample": f"{sample}, torch CPU, {os.cpu_count()} host cpus visible"}
 
     qps = rows * args.steps / (t1 - t0)
     line = {
         "metric": "indexed queries/sec (score+Top2048+gather) and % of FP8-MFMA/HBM roofline",
-        "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "value": round(qps, 1), "unit": rate_unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8-e4m3 score / fp32 accumulate / int32 indices / u8 rows", "data": data,
         "config": meta,

@@ -279,7 +279,7 @@ int v1_page_insert(uint8_t* pool, int64_t* pool_keys, int32_t* refs, int32_t* fr
                    int32_t* count, int32_t capacity, int64_t page_bytes, const int64_t* keys,
                    const uint8_t* tmp, const int32_t* req, int32_t n, int32_t* table,
                    int32_t* status, void* workspace, int64_t workspace_bytes, void* stream);
-int64_t v1_page_release_workspace(int32_t n);
+int64_t v1_page_release_workspace(int32_t capacity, int32_t n);
 int v1_page_release(const int32_t* pages, int32_t n, int32_t* refs, int32_t* free_stack,
                     int32_t* count, int32_t capacity, int32_t* status, void* workspace,
                     int64_t workspace_bytes, void* stream);
@@ -308,6 +308,13 @@ int v1_stage_tail(const uint8_t* native, const int32_t* nt, const int32_t* lens,
                   const int32_t* tail_rows, int32_t rows, int32_t capacity, int32_t np,
                   int32_t scratch, int32_t sink, int32_t window, int64_t native_pages,
                   int64_t fine_pages, void* stream);
+/* stage_tail / stage_tail_shared (kernels.py:518-564, :407-441) over pages of
+ * 64 rows of row_bytes each (656 for MLA latent rows): the same owner, slot and
+ * zero-fill rule, one contiguous row per token. */
+int v1_stage_tail_rows(const uint8_t* native, const int32_t* nt, const int32_t* lens, uint8_t* fine,
+                       const int32_t* tail_rows, int32_t rows, int32_t capacity, int32_t np,
+                       int32_t scratch, int32_t sink, int32_t window, int64_t native_pages,
+                       int64_t fine_pages, int32_t row_bytes, void* stream);
 int v1_mask_fine(float* scores, int64_t score_stride, const void* selected, int32_t selected_bits,
                  const int32_t* rt, const int32_t* members, const int32_t* lens,
                  const int32_t* takes, int32_t rows, int32_t maxp, int32_t take_stride,

@@ -6,6 +6,8 @@ torch expressions for the query path, run with torch on the host cores.
   top-k  scores.topk(2048) and page -> slot mapping nt[i // 64] * 64 + i % 64
          sglang/srt/layers/attention/v1_deepseek/example_v1_query_single_head.py:55-70
   gather fancy indexing, sglang/srt/layers/attention/v1_native/test_gather_slots_small.py:18-24
+  pages  the oracle's page manager, request after request (a host port of
+         sglang/srt/layers/attention/v1_deepseek/kernels.py:72-167)
 """
 import time
 
@@ -131,3 +133,42 @@ def decode_queries_per_second(q8, w, native, table, lens, topk=2048, budget_s=10
         assert slots.shape[0] == min(topk, n)
         done += 1
     return done / (time.perf_counter() - t0), done, threads
+
+
+class _RowsOf:
+    """tmp[i] = payload[inv[i]] without materialising every entry's page."""
+
+    def __init__(self, payload, inv):
+        self.payload, self.inv = payload, inv
+
+    def __getitem__(self, i):
+        return self.payload[self.inv[i]]
+
+
+def pages_requests_per_second(keys, draws, lens, capacity, page_bytes, budget_s=10.0, sample_requests=4096,
+                              min_requests=4, seed=1002):
+    """The page manager run request after request on the host (the oracle's
+    in-place match_pages -> allocate -> publish, kernels.py:72-167, with a
+    key -> live pages map), over the first `sample_requests` requests of the
+    workload from an empty pool of `capacity` pages of page_bytes, until the
+    time budget ends.  Distinct draws get distinct seeded bytes (made before
+    timing).  One thread."""
+    from . import v1 as O
+    R = min(sample_requests, len(lens))
+    n = int(np.asarray(lens[:R], dtype=np.int64).sum())
+    uniq, inv = np.unique(draws[:n], return_inverse=True)
+    payload = np.random.default_rng(seed).integers(0, 256, size=(len(uniq), page_bytes), dtype=np.uint8)
+    tmp = _RowsOf(payload, inv)
+    pool = np.zeros((capacity, page_bytes), dtype=np.uint8)
+    pool_keys = np.zeros(capacity, dtype=np.int64)
+    refs = np.zeros(capacity, dtype=np.int32)
+    free = np.arange(capacity, dtype=np.int32)
+    count, live = capacity, {}
+    table = np.empty(n, dtype=np.int32)
+    starts = np.concatenate([[0], np.cumsum(lens[:R])]).astype(np.int64)
+    done, t0 = 0, time.perf_counter()
+    while done < R and (done < min_requests or time.perf_counter() - t0 < budget_s):
+        count = O.insert_request_inplace(pool, pool_keys, refs, free, count, live, keys, tmp, starts[done],
+                                         starts[done + 1], table)
+        done += 1
+    return done / (time.perf_counter() - t0), done, 1

@@ -285,6 +285,28 @@ def stage_tail(native, nt, lens, fine, capacity, scratch, sink_cap, window, tail
             fine[dst, 8192:] = sb.view(np.uint8)
 
 
+def stage_tail_rows(native, nt, lens, fine, capacity, scratch, sink_cap, window, row_bytes, tail_rows=None):
+    """stage_tail(_shared) (kernels.py:518-564, :407-441) over pages of 64 rows
+    of row_bytes each, one row per token (in place on fine)."""
+    nat = native.reshape(native.shape[0], 64, row_bytes)
+    out = fine.reshape(fine.shape[0], 64, row_bytes)
+    for row in range(nt.shape[0]):
+        if tail_rows is not None and int(tail_rows[row]) != row:
+            continue
+        n = int(lens[row])
+        sink, tail = _bounds(n, window, sink_cap)
+        count = sink + n - tail
+        for p in range(scratch):
+            if not (p * 64 < count or p == 0):
+                continue
+            dst = capacity + row * scratch + p
+            out[dst] = 0
+            for o in range(min(64, max(count - p * 64, 0))):
+                i = p * 64 + o
+                lg = i if i < sink else tail + i - sink
+                out[dst, o] = nat[int(nt[row, lg // 64]), lg % 64]
+
+
 # ------------------------------------------------------------------ sort
 def sort_f32(perm, keys, n, groups, heads=1, head_stride=4096):
     """sglang/srt/layers/attention/v1_native/fused_grouping.py:64-76: returns O."""
@@ -382,6 +404,43 @@ def release(table, refs, free, count):
     return count + len(dead)
 
 
+def live_index(pool_keys, refs):
+    """key -> live pages (refs > 0) in page order."""
+    live = {}
+    for p in np.nonzero(refs > 0)[0]:
+        live.setdefault(int(pool_keys[p]), []).append(int(p))
+    return live
+
+
+def insert_request_inplace(pool, pool_keys, refs, free, count, live, keys, tmp, s, e, table):
+    """One request (entries s..e): match_pages (kernels.py:72-113: lowest live
+    page with equal key and bytes), allocate (:116-131: free[count-1-rank],
+    refs += 1), publish (:134-167: bytes and key to fresh pages), in place.
+    Returns the new count; raises RuntimeError before any change when the
+    free stack is too short."""
+    match = np.full(e - s, -1, dtype=np.int64)
+    for i in range(s, e):
+        for p in live.get(int(keys[i]), ()):
+            if np.array_equal(pool[p], tmp[i]):
+                match[i - s] = p
+                break
+    fresh = match < 0
+    need = int(fresh.sum())
+    if count < need:
+        raise RuntimeError("V1 DeepSeek page arena exhausted")
+    rank = np.cumsum(fresh) - 1
+    dst = np.where(fresh, free[np.clip(count - 1 - rank, 0, None)], match)
+    np.add.at(refs, dst, 1)
+    table[s:e] = dst
+    for i in np.flatnonzero(fresh) + s:
+        p = int(table[i])
+        pool[p] = tmp[i]
+        pool_keys[p] = keys[i]
+        pages = live.setdefault(int(keys[i]), [])
+        pages.insert(int(np.searchsorted(pages, p)), p)
+    return count - need
+
+
 def page_insert_batch(pool, pool_keys, refs, free, count, keys, tmp, req):
     """match_pages -> allocate -> publish (kernels.py:72-167) called request
     after request (runtime.py:230-270) with an int64 key in place of the
@@ -393,33 +452,12 @@ def page_insert_batch(pool, pool_keys, refs, free, count, keys, tmp, req):
     pool, pool_keys, refs, free = pool.copy(), pool_keys.copy(), refs.copy(), free.copy()
     n = len(keys)
     table = np.empty(n, dtype=np.int32)
-    live = {}
-    for p in np.nonzero(refs > 0)[0]:
-        live.setdefault(int(pool_keys[p]), []).append(int(p))
+    live = live_index(pool_keys, refs)
     bounds = np.flatnonzero(np.diff(np.asarray(req, dtype=np.int64))) + 1
     starts = np.concatenate([[0], bounds]).astype(np.int64) if n else np.zeros(0, np.int64)
     ends = np.concatenate([bounds, [n]]).astype(np.int64) if n else np.zeros(0, np.int64)
     for s, e in zip(starts, ends):
-        match = np.full(e - s, -1, dtype=np.int64)
-        for i in range(s, e):
-            for p in sorted(live.get(int(keys[i]), ())):
-                if np.array_equal(pool[p], tmp[i]):
-                    match[i - s] = p
-                    break
-        fresh = match < 0
-        need = int(fresh.sum())
-        if count < need:
-            raise RuntimeError("V1 DeepSeek page arena exhausted")
-        rank = np.cumsum(fresh) - 1
-        dst = np.where(fresh, free[np.clip(count - 1 - rank, 0, None)], match)
-        count -= need
-        np.add.at(refs, dst, 1)
-        table[s:e] = dst
-        for i in np.flatnonzero(fresh) + s:
-            p = int(table[i])
-            pool[p] = tmp[i]
-            pool_keys[p] = keys[i]
-            live.setdefault(int(keys[i]), []).append(p)
+        count = insert_request_inplace(pool, pool_keys, refs, free, count, live, keys, tmp, s, e, table)
     return table, pool, pool_keys, refs, free, count
 
 

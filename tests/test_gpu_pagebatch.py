@@ -152,6 +152,33 @@ def test_page_insert_collision_classes(dev):
     assert p.status() == 0
 
 
+def test_page_insert_all_ones_key_and_dense_keys(dev):
+    """The key -1 (all ones: the hash table's free marker) and a batch whose
+    keys all fall in one small range (long probe chains)."""
+    g = np.random.default_rng(12)
+    cap, n = 512, 900
+    req = np.sort(g.integers(0, 40, n)).astype(np.int32)
+    keys = np.where(g.random(n) < 0.3, -1, g.integers(0, 40, n)).astype(np.int64)
+    tmp = np.zeros((n, 32), np.uint8)
+    tmp[:, 0] = (keys % 7).astype(np.uint8)
+    tmp[:, 1] = g.integers(0, 2, n)  # two byte contents per key: collisions
+    pool = np.zeros((cap, 32), np.uint8)
+    pool_keys = np.zeros(cap, np.int64)
+    refs = np.zeros(cap, np.int32)
+    pool_keys[[3, 9]] = -1
+    pool[9, 1] = 1
+    pool[9, 0] = (-1 % 7)
+    refs[[3, 9]] = 2
+    free = np.concatenate([np.setdiff1d(np.arange(cap), [3, 9]), [0, 0]]).astype(np.int32)
+    st = (pool, pool_keys, refs, free, cap - 2)
+    p = make_pool(dev, *st)
+    t = H(p.insert(T(keys, dev), T(tmp, dev), T(req, dev)))
+    exp = O.page_insert_batch(*st, keys, tmp, req)
+    assert np.array_equal(t, exp[0])
+    assert_state(p, *exp[1:])
+    assert p.status() == 0
+
+
 def test_page_insert_failures_leave_state(dev):
     g = np.random.default_rng(5)
     cap = 64
@@ -241,3 +268,47 @@ def test_config2_full_pages_match_row_tables(dev):
     assert torch.equal(big.count, small.count)
     assert torch.equal(big.pool[t_big.long()], tmp)
     assert big.status() == 0 and small.status() == 0
+
+
+# ------------------------------------------------------ tail staging (rows)
+@pytest.mark.parametrize("rows,row_bytes,scratch", [(4, 656, 68), (37, 656, 20), (9, 32, 68)])
+def test_stage_tail_rows_vs_oracle(dev, rows, row_bytes, scratch):
+    g = np.random.default_rng(rows)
+    pages, cap = 300, 50
+    native = g.integers(0, 256, (pages, 64 * row_bytes), dtype=np.uint8)
+    np_ = 40
+    nt = g.integers(0, pages, (rows, np_)).astype(np.int32)
+    lens = g.integers(1, np_ * 64 + 1, rows).astype(np.int32)
+    lens[:2] = [1100, 64]
+    owners = np.where(g.random(rows) < 0.4, 0, np.arange(rows)).astype(np.int32)
+    fine = np.full((cap + rows * scratch, 64 * row_bytes), 255, np.uint8)
+    exp = fine.copy()
+    O.stage_tail_rows(native, nt, lens, exp, cap, scratch, 64, 64, row_bytes, tail_rows=owners)
+    f = T(fine, dev)
+    PP.stage_tail_rows(T(native, dev), T(nt, dev), T(lens, dev), f, T(owners, dev), cap, scratch)
+    assert np.array_equal(H(f), exp)
+
+
+def test_config2_tail_staging_vs_oracle(dev):
+    """128-token tails of 2048 owner requests over the page pool the batch
+    insert filled (656-byte rows, 41984-byte pages)."""
+    wl = W.config2()
+    a = wl.arrays
+    cap, pb = wl.params["capacity"], wl.params["page_bytes"]
+    pool = PP.PagePool(cap, pb, dev)
+    uniq = W.config2_payload(wl, pb)
+    tmp = torch.from_numpy(uniq).to(dev)[T(a["draw"], dev).long()]
+    table = H(pool.insert(T(a["keys"], dev), tmp, T(a["req"], dev)))
+    tails = W.config2_tails(wl, table)
+    R = len(a["lens"])
+    fine = torch.zeros((cap + R * tails["scratch"], pb), dtype=torch.uint8, device=dev)
+    fine[:cap].copy_(pool.pool)
+    PP.stage_tail_rows(pool.pool, T(tails["nt"], dev), T(tails["lens"], dev), fine, T(tails["tail_rows"], dev),
+                       cap, tails["scratch"])
+    got = H(fine[cap:])
+    pool_h = H(pool.pool)
+    exp = np.zeros((cap + R * tails["scratch"], pb), np.uint8)
+    O.stage_tail_rows(pool_h, tails["nt"], tails["lens"], exp, cap, tails["scratch"], 64, 64, 656,
+                      tail_rows=tails["tail_rows"])
+    assert np.array_equal(got, exp[cap:])
+    assert not got.reshape(R // 2, 2, tails["scratch"], pb)[:, 1].any()  # non-owner scratch stays zero

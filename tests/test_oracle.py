@@ -527,3 +527,28 @@ def test_config2_shape():
     assert p["requests"] == 4096 and 125000 < p["entries"] < 140000 and p["distinct"] < p["capacity"]
     assert p["page_bytes"] == 41984 and wl.arrays["keys"].dtype == np.int64
     assert np.all(np.diff(wl.arrays["req"]) >= 0)
+
+
+def _as_rows(pages8448):
+    """Native pages re-laid as 64 rows of 132 bytes (128 key bytes + fp32 scale)."""
+    k = pages8448[:, :8192].reshape(-1, 64, 128)
+    s = pages8448[:, 8192:].reshape(-1, 64, 4)
+    return np.concatenate([k, s], axis=2).reshape(len(pages8448), 64 * 132)
+
+
+def test_stage_tail_rows_equals_native_layout(kats):
+    """Row-layout staging equals the pinned native-layout staging after the
+    re-layout, on the reference shared-tail KAT and on random lengths."""
+    kat = kats["shared_tail"]
+    native, nt = shared_tail_inputs(kat)
+    rows, cap, scratch = kat["rows"], kat["cap"], kat["scratch"]
+    for lens, owners in ((np.int32(kat["lens"]), np.int32(kat["owners"])),
+                         (np.int32([1, 64, 65, 700]), None), (np.int32([1100, 128, 1088, 2000]), np.int32([0, 1, 1, 3]))):
+        lens = np.minimum(lens, nt.shape[1] * 64)
+        a = np.full((cap + rows * scratch, 8448), 255, np.uint8)
+        O.stage_tail(native, nt, lens, a, cap, scratch, 64, 64, tail_rows=owners)
+        b = np.full((cap + rows * scratch, 64 * 132), 255, np.uint8)
+        O.stage_tail_rows(_as_rows(native), nt, lens, b, cap, scratch, 64, 64, 132, tail_rows=owners)
+        touched = ~(a == 255).all(axis=1)
+        assert np.array_equal(touched, ~(b == 255).all(axis=1))
+        assert np.array_equal(_as_rows(a[touched]), b[touched])
