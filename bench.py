@@ -35,26 +35,43 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
-# HBM traffic per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE on the
-# default workload (calibrated against a plain copy), kept with the kernel trace.
-TRAFFIC_PROFILE = ROOT / "profiles" / "prefill_chunk_4096x32k.md"
-STAGE_KERNELS = {"score": ("score_prep", "score_shared"), "topk": ("transform_rows",), "gather": ("gather_rows16",)}
+# HBM traffic per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (calibrated against a
+# plain copy), kept with the kernel trace of the same workload.
+TRAFFIC = {
+    4: (ROOT / "profiles" / "prefill_chunk_4096x32k.md",
+        {"score": ("score_prep", "score_shared"), "topk": ("transform_rows",), "gather": ("gather_rows16",)}),
+    2: (ROOT / "profiles" / "page_management_4096req.md",
+        {"insert": ("pb_init", "pb_hash", "pb_classify", "pb_slow_live", "pb_slow", "pb_allocate", "pb_table",
+                    "pb_publish", "pb_commit")}),
+}
 
 
-def measured_traffic(stage):
+def measured_traffic(config, stage):
     """HBM bytes per step of a stage's kernels from the committed counter
-    summary, or None when the summary does not list them."""
-    if stage not in STAGE_KERNELS or not TRAFFIC_PROFILE.exists():
+    summary, or None when it does not list them (the insert's two small
+    prefix-sum kernels, under 1 MB, are left out)."""
+    if config not in TRAFFIC:
         return None
-    per_kernel = {}
-    for line in TRAFFIC_PROFILE.read_text().splitlines():
+    path, stages = TRAFFIC[config]
+    if stage not in stages or not path.exists():
+        return None
+    per_kernel, cols = {}, None
+    for line in path.read_text().splitlines():
         cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
-        if len(cells) == 6 and cells[0] and not cells[0].startswith("-"):
-            try:
-                per_kernel[cells[0].split("<")[0]] = float(cells[5])
-            except ValueError:
-                continue
-    vals = [per_kernel.get(k) for k in STAGE_KERNELS[stage]]
+        if cols is None:
+            if any(c.startswith("HBM read bytes") for c in cells):
+                cols = ([i for i, c in enumerate(cells) if c.startswith("HBM read bytes")][0],
+                        [i for i, c in enumerate(cells) if c.startswith("HBM write bytes")][0])
+            continue
+        if len(cells) <= max(cols) or not cells[0] or cells[0].startswith("-"):
+            if not line.strip():
+                cols = None
+            continue
+        try:
+            per_kernel[cells[0].split("<")[0]] = float(cells[cols[0]]) + float(cells[cols[1]])
+        except ValueError:
+            continue
+    vals = [per_kernel.get(k) for k in stages[stage]]
     return None if any(v is None for v in vals) else sum(vals)
 
 
@@ -384,7 +401,7 @@ def main():
         "stages": stage_info,
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4),
-                     "traffic": measured_traffic(dom) if args.config == 4 else None},
+                     "traffic": measured_traffic(args.config, dom)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
