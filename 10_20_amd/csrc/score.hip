@@ -58,8 +58,14 @@ struct ScoreParams {
     int32_t clean;
     const uint8_t* pieces;  // per-query records from score_prep (shared-table kernel)
     int32_t nchunks;        // shared-table kernel: chunks of kChunkPages pages over max_context_len
-    int32_t chunks_per_wg;  // shared-table kernel: consecutive chunks one work-group walks
+    int32_t groups;         // shared-table kernel: 8-query row groups
+    int32_t items;          // shared-table kernel: groups x levels
+    uint32_t* work;         // shared-table kernel: next work item (zeroed by score_prep)
+    int32_t bulk;           // shared-table kernel: levels of full-size ranges (chunks [L*F, (L+1)*F))
+    int32_t lvl_start[16];  // shared-table kernel: chunk range of each later level's items
+    int32_t lvl_chunks[16];
 };
+constexpr int kMaxLevels = 16;
 
 // ---------------------------------------------------------- linear term
 // relu(x) = (x + |x|) / 2, so  sum_h w_h relu(q_h . k)
@@ -105,9 +111,10 @@ __device__ __forceinline__ uint32_t e4m3_code(float x) {
 // One wave per query row: q' = sum_h w_h q_h split into its pieces, and the
 // record described above.
 __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float* w, int32_t rows, int32_t heads,
-                                                  int32_t relu, uint8_t* out) {
+                                                  int32_t relu, uint8_t* out, uint32_t* work) {
     const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
     const int l = __lane_id();
+    if (blockIdx.x == 0 && threadIdx.x == 0) *work = 0u;  // the work counter of score_shared
     if (row >= rows) return;
     // lane l owns dims 2l, 2l+1
     float a0 = 0.f, a1 = 0.f;
@@ -294,16 +301,15 @@ __device__ __forceinline__ void dma4(const i32x4& rs, int32_t voff, uint32_t lds
 // across it; no fence is used, as a fence would drain every load.
 #define V1_PAGE_BARRIER(pending) \
     asm volatile("s_waitcnt vmcnt(" #pending ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
-// Waits for every memory operation of this wave (stores included).
-#define V1_DRAIN() asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory")
 
-// One work-group takes 8 queries of a shared table and walks a range of
-// consecutive chunks (up to kMaxRangePages pages) through one continuous page
-// ring, so the query fragments, weights and page ids are loaded once per
-// range.  Logits of a chunk collect in LDS and are written back when the
-// walk enters the next chunk; the loads then in flight are drained with the
-// stores (stores and page loads share one counter).
-constexpr int kMaxRangePages = 2560;
+// Work items are (8-query group, range of consecutive chunks of up to
+// kMaxRangePages pages).  A persistent work-group pulls items from a counter,
+// so work-groups that run faster (or drew shorter rows) take more of them and
+// the kernel ends within about one item of the average.  An item walks its
+// chunks through one continuous page ring, so the query fragments, weights
+// and page ids are loaded once per item; each page's logits are stored from
+// registers as soon as they are computed.
+constexpr int kMaxRangePages = 256;
 
 template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
@@ -311,12 +317,22 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t st1[V1_PAGE_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t st2[V1_PAGE_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t st3[V1_PAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) float olds[kQueriesPerGroup][kChunkPages][64];
     __shared__ int32_t pids[kMaxRangePages];
+    __shared__ int32_t item_sh;
     const int t = threadIdx.x, l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int64_t row0 = (int64_t)blockIdx.y * kQueriesPerGroup;
-    const int32_t c_begin = blockIdx.x * p.chunks_per_wg;
-    const int32_t nchunk = max(0, min(p.chunks_per_wg, p.nchunks - c_begin));
+  for (;;) {
+    // every wave has finished the previous item (its LDS is free) when the
+    // next one is drawn
+    __syncthreads();
+    if (t == 0) item_sh = (int32_t)atomicAdd(p.work, 1u);
+    __syncthreads();
+    const int32_t item = __builtin_amdgcn_readfirstlane(item_sh);
+    if (item >= p.items) break;
+    const int32_t group = item % p.groups, level = item / p.groups;
+    const int64_t row0 = (int64_t)group * kQueriesPerGroup;
+    constexpr int32_t kFull = kMaxRangePages / kChunkPages;
+    const int32_t c_begin = level < p.bulk ? level * kFull : p.lvl_start[level - p.bulk];
+    const int32_t nchunk = level < p.bulk ? kFull : p.lvl_chunks[level - p.bulk];
     const int32_t page_begin = c_begin * kChunkPages;
 
     // The independent loads of the prologue are all issued before the first
@@ -380,35 +396,19 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // pages of the range below the group's longest context
     const int32_t npages = max(0, min(nchunk * kChunkPages, (max_ctx + 63) / 64 - page_begin));
 
-    // Logits of chunk k of the range (`valid` computed pages) from LDS to
-    // HBM, 4 consecutive columns per lane; a group of 4 that straddles the
-    // context end or the column limit goes element by element.
-    const bool vec = (p.logits_stride & 3) == 0 && (reinterpret_cast<uintptr_t>(p.logits) & 15) == 0;
-    auto flush = [&](int32_t k, int32_t valid) {
-        const int32_t col0 = (c_begin + k) * kChunkPages * 64;
+    // Pages of the item past the group's longest context are computed by
+    // nobody: with clean_logits their columns below max_context_len get -inf.
+    auto fill_rest = [&](int32_t from_page) __attribute__((always_inline)) {
+        if (!p.clean) return;
+        for (int32_t pg = from_page; pg < nchunk * kChunkPages; ++pg) {
 #pragma unroll
-        for (int q = 0; q < kQueriesPerWave; ++q) {
-            const int64_t r = row0 + wv * kQueriesPerWave + q;
-            if (r >= p.rows) continue;
-            const float* src = &olds[wv * kQueriesPerWave + q][0][0];
-#pragma unroll
-            for (int i = 0; i < kChunkPages * 64 / (4 * kWave); ++i) {
-                const int f = i * kWave + l;  // float4 index within the chunk
-                const int32_t j0 = col0 + 4 * f;
-                v4f v = v4f{0.f, 0.f, 0.f, 0.f};
-                if ((4 * f) / 64 < valid) v = *reinterpret_cast<const v4f*>(src + 4 * f);
-                if (vec && j0 + 3 < ctx[q]) {
-                    *reinterpret_cast<v4f*>(p.logits + r * p.logits_stride + j0) = v;
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) store_logit(p, r, j0 + e, ctx[q], v[e]);
-                }
-            }
+            for (int q = 0; q < kQueriesPerWave; ++q)
+                store_logit(p, row0 + wv * kQueriesPerWave + q, (page_begin + pg) * 64 + l, ctx[q], 0.f);
         }
     };
     if (npages == 0) {
-        for (int32_t k = 0; k < nchunk; ++k) flush(k, 0);
-        return;
+        fill_rest(0);
+        continue;
     }
     __syncthreads();  // page ids in LDS
 
@@ -457,23 +457,42 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         const v8i (&b)[4] = f.b;
         float out[kQueriesPerWave];
         if (RELU) {
+            // The page's MFMAs as one stream: per key block the linear-term
+            // block, then each query's head blocks.  Each result is consumed
+            // kLag MFMAs after it is issued, so the MFMA pipe keeps working
+            // while the VALU folds the older result (no wait on the newest).
+            constexpr int kPer = 1 + kQueriesPerWave * HB;
+            constexpr int kTotal = 4 * kPer;
+            constexpr int kLag = 3;
             float part[kQueriesPerWave][4];
+            v4f d[kLag + 1];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                const v4f dl = mfma_fp8(alin, b[kb]);
-#pragma unroll
-                for (int q = 0; q < kQueriesPerWave; ++q) {
-                    float acc = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc = fmaf(coef[q][i], dl[i], acc);
-#pragma unroll
-                    for (int hb = 0; hb < HB; ++hb) {
-                        const v4f d = mfma_fp8(a[q][hb], b[kb]);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc = fmaf(w[q][hb][i], fabsf(d[i]), acc);
-                    }
-                    part[q][kb] = acc;
+            for (int idx = 0; idx < kTotal + kLag; ++idx) {
+                if (idx < kTotal) {
+                    const int kb = idx / kPer, r = idx % kPer;
+                    d[idx % (kLag + 1)] = r == 0 ? mfma_fp8(alin, b[kb]) : mfma_fp8(a[(r - 1) / HB][(r - 1) % HB], b[kb]);
                 }
+                // keep this order: the compiler would otherwise move each
+                // consumer next to its MFMA and pad the gap with nops
+                __builtin_amdgcn_sched_barrier(0);
+                if (idx >= kLag) {
+                    const int j = idx - kLag, kb = j / kPer, r = j % kPer;
+                    const v4f x = d[j % (kLag + 1)];
+                    if (r == 0) {
+#pragma unroll
+                        for (int q = 0; q < kQueriesPerWave; ++q) {
+                            float acc = 0.f;
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) acc = fmaf(coef[q][i], x[i], acc);
+                            part[q][kb] = acc;
+                        }
+                    } else {
+                        const int q = (r - 1) / HB, hb = (r - 1) % HB;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) part[q][kb] = fmaf(w[q][hb][i], fabsf(x[i]), part[q][kb]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
             for (int q = 0; q < kQueriesPerWave; ++q) out[q] = reduce_scatter4(part[q]);
@@ -485,19 +504,26 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
                 out[q] = reduce_scatter4(part);
             }
         }
+        // lane l holds key l of the page: each query's 64 logits are one
+        // coalesced 256-byte store
 #pragma unroll
-        for (int q = 0; q < kQueriesPerWave; ++q) olds[wv * kQueriesPerWave + q][pg][l] = out[q] * f.scale;
+        for (int q = 0; q < kQueriesPerWave; ++q)
+            store_logit(p, row0 + wv * kQueriesPerWave + q, (page_begin + pg) * 64 + l, ctx[q], out[q] * f.scale);
     };
 
     // Step i (page i's fragments already in registers): page i+1 is complete
     // once only pages i+2 and i+3 are still in flight.  After the barrier
     // every wave has read page i out of LDS, so its buffer receives page i+4;
-    // then page i+1's fragments are read while page i is computed.  Loads
-    // past the range read zeros, so every wave always has the same number of
-    // loads in flight.  A step that starts a new chunk first writes back the
-    // finished one and drains (its stores and the page loads in flight).
-    static_assert(kStages == 4 && kDmaPerPage * (kStages - 2) == 6, "barrier wait count");
-    static_assert(kChunkPages % kStages == 0, "chunk ends fall on the last step of a ring turn");
+    // then page i+1's fragments are read while page i is computed and its
+    // logits stored.  Loads past the range read zeros, so every wave always
+    // has the same number of loads in flight.
+    // The wait count: the loads of one wave land in issue order, so while page
+    // i+1 (kDmaPerPage loads) is pending so are the kDmaPerPage * (kStages - 2)
+    // loads issued after it, and `vmcnt <= N` with N below their sum cannot
+    // hold.  Stores share the counter and may finish in any order relative to
+    // the loads; N also lets the last kQueriesPerWave of them stay in flight.
+    constexpr int kWaitCount = kDmaPerPage * (kStages - 2) + kQueriesPerWave;
+    static_assert(kStages == 4 && kWaitCount == 8 && kWaitCount < kDmaPerPage * (kStages - 1), "barrier wait count");
     Frag fa, fb;
     // Compiler-visible full wait: the query fragments, weights and records
     // loaded above are complete before the loop, so no wait for them is
@@ -505,26 +531,21 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     __builtin_amdgcn_s_waitcnt(0);
     V1_PAGE_BARRIER(0);
     load_frag(st0, fa);
-    auto step = [&](int32_t i, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn, bool chunk_start) {
-        V1_PAGE_BARRIER(6);
-        if (chunk_start && i > 0 && (i & (kChunkPages - 1)) == 0) {
-            flush((i / kChunkPages) - 1, kChunkPages);
-            V1_DRAIN();
-        }
+    auto step = [&](int32_t i, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn) {
+        V1_PAGE_BARRIER(8);  // kWaitCount
         issue(cur, i + kStages);
         load_frag(next, fn);
-        if (i < npages) compute(fc, i & (kChunkPages - 1));
+        if (i < npages) compute(fc, i);
     };
     for (int32_t i = 0; i < npages; i += kStages) {
-        step(i, st0, st1, fa, fb, true);
-        step(i + 1, st1, st2, fb, fa, false);
-        step(i + 2, st2, st3, fa, fb, false);
-        step(i + 3, st3, st0, fb, fa, false);
+        step(i, st0, st1, fa, fb);
+        step(i + 1, st1, st2, fb, fa);
+        step(i + 2, st2, st3, fa, fb);
+        step(i + 3, st3, st0, fb, fa);
     }
-    V1_PAGE_BARRIER(0);
-    const int32_t last = (npages - 1) / kChunkPages;
-    flush(last, npages - last * kChunkPages);
-    for (int32_t k = last + 1; k < nchunk; ++k) flush(k, 0);
+    V1_PAGE_BARRIER(0);  // the page buffers are reused by the next item
+    fill_rest(npages);
+  }
 }
 
 // ---------------------------------------------------------------- per row
@@ -603,7 +624,8 @@ void launch_hb(int hb, bool relu, dim3 g, hipStream_t st, const ScoreParams& p) 
 
 using namespace v1;
 
-extern "C" int64_t v1_score_workspace(int32_t rows) { return rows > 0 ? (int64_t)rows * kPieceRowBytes : 0; }
+// per-query records, then the work counter
+extern "C" int64_t v1_score_workspace(int32_t rows) { return rows > 0 ? (int64_t)rows * kPieceRowBytes + 256 : 0; }
 
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
     V1_REQUIRE(a != nullptr, "score: null args");
@@ -621,23 +643,41 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
     const uint32_t chunks = (uint32_t)cdiv(cdiv(a->max_context_len, 64), kChunkPages);
     hipStream_t st = as_stream(stream);
     if (a->block_table_stride == 0) {
-        V1_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= (int64_t)a->rows * kPieceRowBytes,
-                   "score: workspace of %lld bytes required", (long long)((int64_t)a->rows * kPieceRowBytes));
-        p.pieces = static_cast<const uint8_t*>(a->workspace);
+        const int64_t need = v1_score_workspace(a->rows);
+        V1_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= need, "score: workspace of %lld bytes required",
+                   (long long)need);
+        V1_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 15) == 0, "score: workspace must be 16-byte aligned");
+        uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+        p.pieces = ws;
+        p.work = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes);
         hipLaunchKernelGGL(score_prep, dim3((uint32_t)cdiv(a->rows, 4)), dim3(256), 0, st, a->q, a->weights, a->rows,
-                           a->heads, a->relu, static_cast<uint8_t*>(a->workspace));
+                           a->heads, a->relu, ws, p.work);
         const int rc = V1_LAUNCHED("score_prep");
         if (rc != V1_OK) return rc;
-        // Split each row group's chunks into as few ranges as fill the chip
-        // (two work-groups per CU) and keep each range within kMaxRangePages.
+        // Work items: each row group's chunks cut into ranges that halve in
+        // size (at most kMaxRangePages pages), all groups' largest ranges
+        // first; work-groups pull them in that order, so the last ones taken
+        // are short and the work-groups end together.
         const int64_t groups = cdiv(a->rows, kQueriesPerGroup);
-        int64_t nsplit = std::min<int64_t>((int64_t)chunks, std::max<int64_t>(1, cdiv(2 * v1::device_cus(), groups)));
-        nsplit = std::max<int64_t>(nsplit, cdiv((int64_t)chunks * kChunkPages, kMaxRangePages));
+        const int64_t wgs = 2 * (int64_t)v1::device_cus();
+        constexpr int64_t kFull = kMaxRangePages / kChunkPages;
+        p.bulk = (int32_t)((int64_t)chunks > 2 * kFull ? ((int64_t)chunks - kFull) / kFull : 0);
+        int nlevels = 0;
+        for (int64_t c = (int64_t)p.bulk * kFull; c < (int64_t)chunks;) {
+            const int64_t left = (int64_t)chunks - c;
+            const int64_t size = std::min<int64_t>(left == 1 ? 1 : (left + 1) / 2, kFull);
+            p.lvl_start[nlevels] = (int32_t)c;
+            p.lvl_chunks[nlevels] = (int32_t)size;
+            ++nlevels;
+            c += size;
+        }
+        static_assert(kMaxLevels >= 8, "the halving tail of at most 2 full ranges has at most 7 levels");
         p.nchunks = (int32_t)chunks;
-        p.chunks_per_wg = (int32_t)cdiv((int64_t)chunks, nsplit);
-        nsplit = cdiv((int64_t)chunks, p.chunks_per_wg);
-        const dim3 grid((uint32_t)nsplit, (uint32_t)groups);
-        launch_hb<Shared>(hb, a->relu != 0, grid, st, p);
+        p.groups = (int32_t)groups;
+        const int64_t items = groups * ((int64_t)p.bulk + nlevels);
+        V1_REQUIRE(items < (1ll << 31) - (1ll << 20), "score: too many work items");
+        p.items = (int32_t)items;
+        launch_hb<Shared>(hb, a->relu != 0, dim3((uint32_t)std::min<int64_t>(items, wgs)), st, p);
         return V1_LAUNCHED("score_shared");
     }
     const dim3 grid(chunks, (uint32_t)a->rows);
