@@ -500,9 +500,12 @@ def physical_rows(ids, table=None, page_bits=0):
 
 
 def gather_rows(pool, ids, table=None, page_bits=0):
+    """Rows of `pool` at the physical ids; -1 and ids outside the pool give
+    zero rows (this build's contract for ids the reference leaves undefined)."""
     phys = physical_rows(ids, table, page_bits)
-    out = pool[np.where(phys >= 0, phys, 0)]
-    out[phys < 0] = 0
+    ok = (phys >= 0) & (phys < len(pool))
+    out = pool[np.where(ok, phys, 0)]
+    out[~ok] = 0
     return out
 
 
