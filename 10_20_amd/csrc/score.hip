@@ -61,6 +61,7 @@ struct ScoreParams {
     int32_t groups;         // shared-table kernel: 8-query row groups
     int32_t items;          // shared-table kernel: groups x levels
     uint32_t* work;         // shared-table kernel: next work item (zeroed by score_prep)
+    float* sink;            // shared-table kernel: 64 floats that masked-out logit stores write
     int32_t bulk;           // shared-table kernel: levels of full-size ranges (chunks [L*F, (L+1)*F))
     int32_t lvl_start[16];  // shared-table kernel: chunk range of each later level's items
     int32_t lvl_chunks[16];
@@ -356,7 +357,11 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // end read the last row (their logits are never stored).
     v8i a[kQueriesPerWave][HB];
     float w[kQueriesPerWave][HB][4];
-    float coef[kQueriesPerWave][4];
+    // Linear-term MFMA row block: row r holds piece 2*(r/4) + r%2 of query
+    // (r/2)%2, so result row 4*(l/16)+i of lane l is piece 2*(l/16) + i%2 of
+    // query i/2, and coef[i] is that piece's scale.
+    static_assert(kQueriesPerWave == 2, "two queries per linear-term row block");
+    float coef[4];
     v8i alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int q = 0; q < kQueriesPerWave; ++q) {
@@ -370,17 +375,16 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
             for (int i = 0; i < 4; ++i) w[q][hb][i] = x[i];
         }
         if (RELU) {
-            // result row 4*(l/16)+i holds piece (row & 7) of query (row >> 3)
-            const v4f x = *reinterpret_cast<const v4f*>(rec + kRecScales + 16 * ((l >> 4) & 1));
-            const float mine = (l >> 5) == q ? 1.f : 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) coef[q][i] = x[i] * mine;
+            const float2 x = *reinterpret_cast<const float2*>(rec + kRecScales + 8 * (l >> 4));
+            coef[2 * q] = x.x;
+            coef[2 * q + 1] = x.y;
         }
     }
     if (RELU) {
-        // MFMA row block: rows 0-7 are query 0's pieces, rows 8-15 query 1's
-        const int64_t rq = min(row0 + wv * kQueriesPerWave + ((l & 15) >> 3), (int64_t)p.rows - 1);
-        const u32x4* src = reinterpret_cast<const u32x4*>(p.pieces + rq * kPieceRowBytes + (l & 7) * 128 + 32 * (l >> 4));
+        const int rr = l & 15;
+        const int64_t rq = min(row0 + wv * kQueriesPerWave + ((rr >> 1) & 1), (int64_t)p.rows - 1);
+        const int piece = 2 * (rr >> 2) + (rr & 1);
+        const u32x4* src = reinterpret_cast<const u32x4*>(p.pieces + rq * kPieceRowBytes + piece * 128 + 32 * (l >> 4));
         const u32x4 x = src[0], y = src[1];
         alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
     }
@@ -421,18 +425,19 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         voff[i] = key * 128 + (((s & 7) ^ key_swizzle(key & 15)) << 4);
     }
     const int32_t soff = 8192 + 64 * wv + 4 * l;
-    auto issue = [&](uint8_t* buf, int32_t i) {
-        const int32_t page = i < npages ? __builtin_amdgcn_readfirstlane(pids[i]) : -1;
+    auto issue = [&](uint8_t* buf, int32_t page) {
         const i32x4 rs = page_rsrc(p.kv, page);
         const uint32_t base = lds_addr(buf);
         dma16(rs, voff[0], base + (2 * wv) * 1024);
         dma16(rs, voff[1], base + (2 * wv + 1) * 1024);
         if (l < 16) dma4(rs, soff, base + 8192 + 64 * wv);
     };
-    issue(st0, 0);
-    issue(st1, 1);
-    issue(st2, 2);
-    issue(st3, 3);
+    issue(st0, __builtin_amdgcn_readfirstlane(pids[0]));
+    issue(st1, 1 < npages ? __builtin_amdgcn_readfirstlane(pids[1]) : -1);
+    issue(st2, 2 < npages ? __builtin_amdgcn_readfirstlane(pids[2]) : -1);
+    issue(st3, 3 < npages ? __builtin_amdgcn_readfirstlane(pids[3]) : -1);
+    // page id of the next page to load, read from LDS one step ahead
+    int32_t pid_next = pids[kStages];
 
     // B fragment of key block kb: key kb*16 + l%16, chunks 2*(l/16) and +1;
     // plus the scale of key l
@@ -453,95 +458,129 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         f.scale = reinterpret_cast<const float*>(buf + 8192)[l];
     };
 
-    auto compute = [&](const Frag& f, int32_t pg) {
-        const v8i (&b)[4] = f.b;
-        float out[kQueriesPerWave];
-        if (RELU) {
-            // The page's MFMAs as one stream: per key block the linear-term
-            // block, then each query's head blocks.  Each result is consumed
-            // kLag MFMAs after it is issued, so the MFMA pipe keeps working
-            // while the VALU folds the older result (no wait on the newest).
-            constexpr int kPer = 1 + kQueriesPerWave * HB;
-            constexpr int kTotal = 4 * kPer;
-            constexpr int kLag = 3;
-            float part[kQueriesPerWave][4];
-            v4f d[kLag + 1];
+    // A page is one stream of kTotal MFMAs: per key block the linear-term
+    // block (ReLU form), then each query's head blocks.  Result idx is folded
+    // into the per-lane partials kLag MFMAs after it is issued, so the MFMA
+    // pipe keeps working while the VALU folds older results; the stream runs
+    // on across pages, the first kLag slots of a page finishing the previous
+    // page's partials.
+    constexpr int kPer = (RELU ? 1 : 0) + kQueriesPerWave * HB;
+    constexpr int kTotal = 4 * kPer;
+    constexpr int kLag = 3;
+    static_assert(kTotal % (kLag + 1) == 0 && kTotal > kLag + 4, "result ring continues across pages");
+    // slots of the page-boundary work inside the stream: the previous page's
+    // logits are stored once its partials are complete, then the page
+    // barrier and the next load are issued, then the next page's fragments read
+    constexpr int kStoreAt = kLag - 1, kSyncAt = kLag + 2, kFragAt = kLag + 4;
+    v4f d[kLag + 1];
 #pragma unroll
-            for (int idx = 0; idx < kTotal + kLag; ++idx) {
-                if (idx < kTotal) {
-                    const int kb = idx / kPer, r = idx % kPer;
-                    d[idx % (kLag + 1)] = r == 0 ? mfma_fp8(alin, b[kb]) : mfma_fp8(a[(r - 1) / HB][(r - 1) % HB], b[kb]);
-                }
+    for (int k = 0; k <= kLag; ++k) d[k] = v4f{0.f, 0.f, 0.f, 0.f};
+    auto mfma_at = [&](int idx, const Frag& f) __attribute__((always_inline)) {
+        const int kb = idx / kPer, r = idx % kPer;
+        const int rr = RELU ? max(r - 1, 0) : r;  // head block (r == 0 is the linear-term block)
+        d[idx % (kLag + 1)] = (RELU && r == 0) ? mfma_fp8(alin, f.b[kb]) : mfma_fp8(a[rr / HB][rr % HB], f.b[kb]);
+    };
+    auto consume = [&](int jj, float (&part)[kQueriesPerWave][4]) __attribute__((always_inline)) {
+        const int kb = jj / kPer, r = jj % kPer;
+        const v4f x = d[jj % (kLag + 1)];
+        if (RELU && r == 0) {
+#pragma unroll
+            for (int q = 0; q < kQueriesPerWave; ++q) part[q][kb] = fmaf(coef[2 * q + 1], x[2 * q + 1], coef[2 * q] * x[2 * q]);
+        } else {
+            const int rr = RELU ? r - 1 : r;
+            const int q = rr / HB, hb = rr % HB;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float prev = (!RELU && hb == 0 && i == 0) ? 0.f : part[q][kb];
+                part[q][kb] = fmaf(w[q][hb][i], RELU ? fabsf(x[i]) : x[i], prev);
+            }
+        }
+    };
+    // Every step issues exactly kQueriesPerWave logit stores: lanes with
+    // nothing to write (no page, a row past the end, a column past the
+    // context without clean_logits) store to the sink.  The count of vector
+    // memory operations per step is then fixed, which the page wait relies on.
+    auto store = [&](int32_t pg, bool live, const float (&part)[kQueriesPerWave][4], float scale) {
+#pragma unroll
+        for (int q = 0; q < kQueriesPerWave; ++q) {
+            const float out = reduce_scatter4(part[q]) * scale;
+            const int64_t row = row0 + wv * kQueriesPerWave + q;
+            const int32_t j = (page_begin + pg) * 64 + l;
+            const bool in = live & (row < p.rows) & (j < p.max_context_len) & ((j < ctx[q]) | (p.clean != 0));
+            float* dst = in ? p.logits + row * p.logits_stride + j : p.sink + l;
+            *dst = j < ctx[q] ? out : -__builtin_huge_valf();
+        }
+    };
+
+    // The page wait.  A wave's vector memory operations complete in issue
+    // order (loads and stores alike share vmcnt and retire in order), and per
+    // step a wave issues kQueriesPerWave stores and then kDmaPerPage loads.
+    // At step i the loads of page i+1 were issued at step i-3; after them came
+    // the stores and loads of steps i-2 and i-1 and the stores of step i, so
+    // `vmcnt <= kWaitCount` holds only once page i+1 has landed.  (The first
+    // pages are covered by the full wait before the loop.)
+    constexpr int kWaitCount = (kDmaPerPage + kQueriesPerWave) * (kStages - 2) + kQueriesPerWave;
+    static_assert(kStages == 4 && kWaitCount == 12, "barrier wait count");
+    // After the barrier every wave has read page i out of LDS (its fragments
+    // were read at step i-1), so its buffer receives page i+4.
+    auto sync = [&](int32_t i, uint8_t* cur) __attribute__((always_inline)) {
+        V1_PAGE_BARRIER(12);  // kWaitCount
+        issue(cur, i + kStages < npages ? __builtin_amdgcn_readfirstlane(pid_next) : -1);
+        pid_next = pids[min(i + kStages + 1, kMaxRangePages - 1)];
+    };
+    auto drain = [&](float (&part)[kQueriesPerWave][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = kTotal - kLag; j < kTotal; ++j) consume(j, part);
+    };
+    // Step i: page i's fragments are in fc; fn holds page i-1's until page
+    // i+1's are read into it.
+    auto step = [&](int32_t i, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn,
+                    float (&pc)[kQueriesPerWave][4], float (&pp)[kQueriesPerWave][4]) {
+        if (i < npages) {
+#pragma unroll
+            for (int idx = 0; idx < kTotal; ++idx) {
+                mfma_at(idx, fc);
                 // keep this order: the compiler would otherwise move each
                 // consumer next to its MFMA and pad the gap with nops
                 __builtin_amdgcn_sched_barrier(0);
-                if (idx >= kLag) {
-                    const int j = idx - kLag, kb = j / kPer, r = j % kPer;
-                    const v4f x = d[j % (kLag + 1)];
-                    if (r == 0) {
-#pragma unroll
-                        for (int q = 0; q < kQueriesPerWave; ++q) {
-                            float acc = 0.f;
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) acc = fmaf(coef[q][i], x[i], acc);
-                            part[q][kb] = acc;
-                        }
-                    } else {
-                        const int q = (r - 1) / HB, hb = (r - 1) % HB;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) part[q][kb] = fmaf(w[q][hb][i], fabsf(x[i]), part[q][kb]);
-                    }
-                }
+                if (idx >= kLag)
+                    consume(idx - kLag, pc);
+                else
+                    consume(kTotal + idx - kLag, pp);
+                if (idx == kStoreAt) store(i - 1, i > 0, pp, fn.scale);
+                if (idx == kSyncAt) sync(i, cur);
+                if (idx == kFragAt) load_frag(next, fn);
                 __builtin_amdgcn_sched_barrier(0);
             }
-#pragma unroll
-            for (int q = 0; q < kQueriesPerWave; ++q) out[q] = reduce_scatter4(part[q]);
         } else {
-#pragma unroll
-            for (int q = 0; q < kQueriesPerWave; ++q) {
-                float part[4];
-                page_partials<HB, false>(a[q], b, w[q], part);
-                out[q] = reduce_scatter4(part);
-            }
+            // past the last page: finish and store it (first time only)
+            if (i == npages) drain(pp);
+            store(i - 1, i == npages, pp, fn.scale);
+            sync(i, cur);
+            load_frag(next, fn);
         }
-        // lane l holds key l of the page: each query's 64 logits are one
-        // coalesced 256-byte store
-#pragma unroll
-        for (int q = 0; q < kQueriesPerWave; ++q)
-            store_logit(p, row0 + wv * kQueriesPerWave + q, (page_begin + pg) * 64 + l, ctx[q], out[q] * f.scale);
     };
-
-    // Step i (page i's fragments already in registers): page i+1 is complete
-    // once only pages i+2 and i+3 are still in flight.  After the barrier
-    // every wave has read page i out of LDS, so its buffer receives page i+4;
-    // then page i+1's fragments are read while page i is computed and its
-    // logits stored.  Loads past the range read zeros, so every wave always
-    // has the same number of loads in flight.
-    // The wait count: the loads of one wave land in issue order, so while page
-    // i+1 (kDmaPerPage loads) is pending so are the kDmaPerPage * (kStages - 2)
-    // loads issued after it, and `vmcnt <= N` with N below their sum cannot
-    // hold.  Stores share the counter and may finish in any order relative to
-    // the loads; N also lets the last kQueriesPerWave of them stay in flight.
-    constexpr int kWaitCount = kDmaPerPage * (kStages - 2) + kQueriesPerWave;
-    static_assert(kStages == 4 && kWaitCount == 8 && kWaitCount < kDmaPerPage * (kStages - 1), "barrier wait count");
     Frag fa, fb;
+    float pa[kQueriesPerWave][4], pb[kQueriesPerWave][4];
+#pragma unroll
+    for (int q = 0; q < kQueriesPerWave; ++q)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pa[q][k] = pb[q][k] = 0.f;
     // Compiler-visible full wait: the query fragments, weights and records
     // loaded above are complete before the loop, so no wait for them is
     // placed inside it.  (It also covers the first pages.)
     __builtin_amdgcn_s_waitcnt(0);
     V1_PAGE_BARRIER(0);
     load_frag(st0, fa);
-    auto step = [&](int32_t i, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn) {
-        V1_PAGE_BARRIER(8);  // kWaitCount
-        issue(cur, i + kStages);
-        load_frag(next, fn);
-        if (i < npages) compute(fc, i);
-    };
     for (int32_t i = 0; i < npages; i += kStages) {
-        step(i, st0, st1, fa, fb);
-        step(i + 1, st1, st2, fb, fa);
-        step(i + 2, st2, st3, fa, fb);
-        step(i + 3, st3, st0, fb, fa);
+        step(i, st0, st1, fa, fb, pa, pb);
+        step(i + 1, st1, st2, fb, fa, pb, pa);
+        step(i + 2, st2, st3, fa, fb, pa, pb);
+        step(i + 3, st3, st0, fb, fa, pb, pa);
+    }
+    if (npages % kStages == 0) {
+        drain(pb);
+        store(npages - 1, true, pb, fb.scale);
     }
     V1_PAGE_BARRIER(0);  // the page buffers are reused by the next item
     fill_rest(npages);
@@ -624,8 +663,8 @@ void launch_hb(int hb, bool relu, dim3 g, hipStream_t st, const ScoreParams& p) 
 
 using namespace v1;
 
-// per-query records, then the work counter
-extern "C" int64_t v1_score_workspace(int32_t rows) { return rows > 0 ? (int64_t)rows * kPieceRowBytes + 256 : 0; }
+// per-query records, the work counter (256 bytes), the store sink (256 bytes)
+extern "C" int64_t v1_score_workspace(int32_t rows) { return rows > 0 ? (int64_t)rows * kPieceRowBytes + 512 : 0; }
 
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
     V1_REQUIRE(a != nullptr, "score: null args");
@@ -650,6 +689,7 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         uint8_t* ws = static_cast<uint8_t*>(a->workspace);
         p.pieces = ws;
         p.work = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes);
+        p.sink = reinterpret_cast<float*>(ws + (int64_t)a->rows * kPieceRowBytes + 256);
         hipLaunchKernelGGL(score_prep, dim3((uint32_t)cdiv(a->rows, 4)), dim3(256), 0, st, a->q, a->weights, a->rows,
                            a->heads, a->relu, ws, p.work);
         const int rc = V1_LAUNCHED("score_prep");

@@ -599,6 +599,31 @@ def test_score_shared_uneven_lengths(dev, rows, ctx):
     assert_scores_close(got[:, :width], ref, bound)
 
 
+@pytest.mark.parametrize("rows,heads,relu", [(45, 64, True), (21, 48, False), (13, 7, True), (300, 64, False)])
+def test_score_shared_unclean_leaves_columns(dev, rows, heads, relu):
+    """Shared table, clean_logits off: columns at or past each row's length
+    keep the caller's values (whole pages of a row past its length issue no
+    store into the logits), with or without the ReLU."""
+    g = np.random.default_rng(rows * 7 + heads)
+    ctx = 4500
+    q8, w, native, table, _ = _score_case(g, rows, heads, ctx, True, 200)
+    lens = g.integers(0, ctx + 1, rows).astype(np.int32)
+    lens[g.random(rows) < 0.2] = 0
+    lens[::5] = ctx
+    out = torch.full((rows, ctx), 7.0, device=dev)
+    bt = T(table, dev)[None].expand(rows, -1)
+    SC.fp8_paged_mqa_logits(T(q8, dev).view(torch.float8_e4m3fn), T(native, dev), T(w, dev), T(lens, dev), bt, None,
+                            ctx, clean_logits=False, relu=relu, out=out)
+    full = np.broadcast_to(table, (rows, table.shape[-1]))
+    ref = O.paged_logits(q8, w, native, full, lens, ctx, relu=relu, clean=False)
+    bound = O.paged_logits(q8, w, native, full, lens, ctx, clean=False, magnitude=True)
+    got = H(out).astype(np.float64)
+    past = np.arange(ctx)[None, :] >= lens[:, None]
+    assert (got[past] == 7.0).all()
+    ref[past] = 7.0
+    assert_scores_close(got, ref, bound)
+
+
 def assert_scores_close(got, ref, bound):
     """1e-2 relative, plus the fp32 accumulation allowance 2^-16 * sum|w q k s|
     that a near-zero (cancelling) dot product needs."""
