@@ -13,9 +13,9 @@
 // streams of some rows overlap the LDS selection of others.
 //  1. 2048 keys sampled in 256 runs of 8 (a few percent of the row's cache
 //     lines) give a pivot that about 1.3*T of the row's keys exceed.
-//  2. One streaming pass, wave-independent (no barriers), sends every key at or
-//     above the pivot to an LDS candidate buffer (wave-aggregated slot
-//     allocation) and keeps the row's key statistics.
+//  2. One streaming pass, wave-independent (no barriers), sends every score at
+//     or above the pivot to an LDS candidate buffer (a float compare per score,
+//     ballot-counted slots per wave).
 //  3. LDS radix passes over the candidates (the first digit starts where the
 //     largest and smallest candidate differ) give the T-th largest key tau and
 //     the number r of tau-valued keys to take.
@@ -24,7 +24,9 @@
 //     min(== tau before it, r).  No sort is needed and the order is exact;
 //     each winner is written straight to its output slot.
 // When the pivot misses (fewer than T or more than kCandMax keys at or above
-// it) the same steps run on the whole row, streamed again from cache.
+// it) a second pivot, aimed by the observed count, is streamed once more; a
+// second miss runs the same steps exactly on the whole row (statistics, radix
+// passes), streamed again.
 // Rows longer than 32768 columns are cut into 32768-column segments whose
 // Top-T land in a workspace; a merge work-group selects from their union.
 #include <algorithm>
@@ -44,6 +46,8 @@ constexpr int kCandMax = 3584;
 constexpr int kCandPerThread = kCandMax / kBlock;  // 7
 constexpr int kSampleRuns = 256;                   // pivot sample: runs of 8 keys
 constexpr uint32_t kNegInfKey = 0x007fffffu;
+constexpr uint32_t kPosInfKey = 0xff800000u;  // key of +inf; keys above it are positive NaNs
+constexpr uint32_t kNegInfBits = 0xff800000u;  // float bits of -inf
 static_assert(kHist == 4 * kBlock && kWords % kBlock == 0 && kCandMax % kBlock == 0, "work split");
 static_assert(kSampleRuns * 8 == 4 * kBlock, "two threads per sample run");
 
@@ -224,25 +228,11 @@ struct Ranker {
     }
 };
 
-// Selects the T largest keys of positions [0, n) of `src` (n > T, n <= kSpan;
-// ties toward the lower position).  emit(slot[], position[], key[]) takes a
-// thread's batch of items (arrays of one length; slot -1 = not selected):
-// every slot in [0, T) is delivered exactly once, the slots ascending by
-// position.  Batches let the emitter issue all of a thread's output loads
-// before its stores.  src.load4(p, k) returns the keys of positions p..p+3
-// (p % 4 == 0), key 0 past n.  Ends with a barrier.
-template <class Src, class Emit>
-__device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emit& emit) {
-    const int t = threadIdx.x, w = t / kWave, lane = __lane_id();
-    const int32_t n = src.n;
-    // 1. pivot from 2048 sampled keys: threads 2r, 2r+1 read run r of 8 keys
-    uint32_t sk[4];
-    src.load4((int32_t)((((int64_t)(t >> 1) * n / kSampleRuns) & ~7ll) + 4 * (t & 1)), sk);
-    uint32_t smax = 0, smin = 0xffffffffu, scnt = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) key_stats(sk[e], smax, smin, scnt);
-    if (t == 0) sm.ncand = 0;
-    block_stats(smax, smin, scnt, sm);
+// Pivot from the sampled keys sk (threads 2r, 2r+1 hold run r of 8 keys;
+// block statistics smax / smin / scnt) such that about target * T of the n
+// keys are expected at or above it.  Ends with a barrier.
+__device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_t smin, uint32_t scnt, int32_t n,
+                                 uint32_t T, float target, SelSmem& sm) {
     uint32_t pivot = kNegInfKey + 1;
     if (scnt > 0 && smax == smin) {
         pivot = smin;
@@ -256,7 +246,7 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emi
         for (int e = 0; e < 4; ++e)
             if (sk[e] > kNegInfKey) atomicAdd(&sm.hist[(sk[e] >> lo) & (kHist - 1u)], 1u);
         __syncthreads();
-        const uint32_t want = (uint32_t)min((uint64_t)scnt, (uint64_t)scnt * T * 13 / (10ull * (uint64_t)n) + 16ull);
+        const uint32_t want = (uint32_t)min((float)scnt, (float)scnt * (float)T * target / (float)n + 16.f);
         uint32_t bin, above;
         find_bin(want, sm, bin, above);
         // Expected candidates with the pivot at the bin's lower edge (every
@@ -284,102 +274,185 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emi
         }
         pivot = max(pivot, kNegInfKey + 1);
     }
-    // 2. stream: candidates >= pivot into LDS, row statistics on the side.
-    //    Each wave keeps kBatch 1 KB loads in flight.
-    uint32_t rmax = 0, rmin = 0xffffffffu, rcnt = 0;
-    const int32_t steps = (n + 255) / 256;
+    __syncthreads();
+    return pivot;
+}
+
+// Step 2: every entry at or above the pivot goes to the LDS candidate buffer
+// (sm.ncand counts them all; the first kCandMax are kept).  Score rows are
+// tested as floats against the pivot's float (key order and float order
+// agree on every non-NaN score, with -0 == +0) and stored as raw bits, which
+// the selection turns into keys; a wave batch holding a NaN, or a pivot in
+// the NaN key range, takes the exact key test.  Slots come from one LDS
+// allocation per wave and pair of batches (ballot counts, mbcnt ranks).  Each
+// wave keeps kBatch 1 KB loads in flight.
+template <class Src>
+__device__ void stream_candidates(const Src& src, uint32_t pivot, SelSmem& sm) {
+    const int w = threadIdx.x / kWave, lane = __lane_id();
+    const int32_t steps = (src.n + 255) / 256;
     constexpr int kBatch = 4;
+    const bool float_test = Src::kFloats && pivot <= kPosInfKey;
+    const float fpivot = key_score(pivot);
     for (int32_t s0 = w; s0 < steps; s0 += kWaves * kBatch) {
-        uint32_t k[kBatch][4];
+        uint32_t v[kBatch][4];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int32_t s = s0 + u * kWaves;
-            if (s < steps) {
-                src.load4(s * 256 + 4 * lane, k[u]);
-            } else {
-                k[u][0] = k[u][1] = k[u][2] = k[u][3] = 0u;
+        for (int u = 0; u < kBatch; ++u) src.load_raw4((s0 + u * kWaves) * 256 + 4 * lane, v[u]);
+        // slots are allocated per pair of batches (keeps the lane masks in
+        // scalar registers)
+#pragma unroll
+        for (int h = 0; h < kBatch; h += 2) {
+            bool c[2][4];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                bool nan = false;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x = __uint_as_float(v[h + u][e]);
+                    c[u][e] = Src::kFloats ? x >= fpivot : v[h + u][e] >= pivot;
+                    nan |= x != x;
+                }
+                if (Src::kFloats && (!float_test || __builtin_amdgcn_ballot_w64(nan) != 0)) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) c[u][e] = score_key(__uint_as_float(v[h + u][e])) >= pivot;
+                }
             }
-        }
+            uint64_t m[2][4];
+            uint32_t pre[2][4], total = 0;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int32_t p = (s0 + u * kWaves) * 256 + 4 * lane;
-            uint32_t c = 0;
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                key_stats(k[u][e], rmax, rmin, rcnt);
-                c += k[u][e] >= pivot ? 1u : 0u;
-            }
-            const uint32_t incl = wave_inclusive_sum(c);
-            const uint32_t total = readlane(incl, kWave - 1);
+                for (int e = 0; e < 4; ++e) {
+                    m[u][e] = __builtin_amdgcn_ballot_w64(c[u][e]);
+                    pre[u][e] = total;
+                    total += (uint32_t)__builtin_popcountll(m[u][e]);
+                }
             if (total == 0) continue;
             uint32_t base = 0;
-            if (lane == kWave - 1) base = atomicAdd(&sm.ncand, total);
-            uint32_t at = readlane(base, kWave - 1) + incl - c;
+            if (lane == 0) base = atomicAdd(&sm.ncand, total);
+            base = readlane(base, 0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if (k[u][e] >= pivot) {
-                    if (at < (uint32_t)kCandMax) {
-                        sm.cand_key[at] = k[u][e];
-                        sm.cand_pos[at] = (uint16_t)(p + e);
+            for (int u = 0; u < 2; ++u) {
+                const int32_t p = (s0 + (h + u) * kWaves) * 256 + 4 * lane;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (c[u][e]) {
+                        const uint32_t at = base + pre[u][e] +
+                            __builtin_amdgcn_mbcnt_hi((uint32_t)(m[u][e] >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m[u][e], 0u));
+                        if (at < (uint32_t)kCandMax) {
+                            sm.cand_key[at] = v[h + u][e];
+                            sm.cand_pos[at] = (uint16_t)(p + e);
+                        }
                     }
-                    ++at;
                 }
             }
         }
     }
-    __syncthreads();
-    const uint32_t ncand = sm.ncand;
-    block_stats(rmax, rmin, rcnt, sm);
-    Ranker::clear(sm);
-    __syncthreads();
-    if (ncand >= T && ncand <= (uint32_t)kCandMax) {
-        // 3. radix select on the candidates (kCandPerThread per thread, slot q = i*kBlock + t)
-        uint32_t ck[kCandPerThread];
-        uint32_t cmax = 0, cmin = 0xffffffffu, cc = 0;
+}
+
+// Steps 3 and 4 over ncand (T <= ncand <= kCandMax) buffered candidates.
+// Ends with a barrier.
+template <class Src, class Emit>
+__device__ void select_candidates(uint32_t ncand, uint32_t T, SelSmem& sm, const Emit& emit) {
+    const int t = threadIdx.x;
+    // 3. radix select on the candidates (kCandPerThread per thread, slot q = i*kBlock + t)
+    uint32_t ck[kCandPerThread];
+    uint32_t cmax = 0, cmin = 0xffffffffu, cc = 0;
 #pragma unroll
-        for (int i = 0; i < kCandPerThread; ++i) {
-            const uint32_t q = i * kBlock + t;
-            ck[i] = q < ncand ? sm.cand_key[q] : 0u;
-            key_stats(ck[i], cmax, cmin, cc);
-        }
-        block_stats(cmax, cmin, cc, sm);
-        uint32_t tau = cmax, r = T;
-        if (cmax != cmin) {
-            Radix rx;
-            rx.start(cmax, cmin, T);
-            while (rx.shift > 0) {
-                clear_hist(sm);
-                __syncthreads();
-#pragma unroll
-                for (int i = 0; i < kCandPerThread; ++i)
-                    if (rx.counts(ck[i], true)) atomicAdd(&sm.hist[rx.digit(ck[i])], 1u);
-                __syncthreads();
-                rx.finish(sm);
-            }
-            tau = rx.prefix;
-            r = rx.remaining;
-        }
-        // 4. position ranks
-#pragma unroll
-        for (int i = 0; i < kCandPerThread; ++i) {
-            const uint32_t q = i * kBlock + t;
-            if (q < ncand) Ranker::mark(sm, sm.cand_pos[q], ck[i] > tau, ck[i] == tau);
-        }
-        __syncthreads();
-        Ranker::scan(sm);
-        int32_t at[kCandPerThread];
-        uint32_t cp[kCandPerThread];
-#pragma unroll
-        for (int i = 0; i < kCandPerThread; ++i) {
-            const uint32_t q = i * kBlock + t;
-            cp[i] = q < ncand ? (uint32_t)sm.cand_pos[q] : 0u;
-            at[i] = (q < ncand && ck[i] >= tau) ? Ranker::slot(sm, cp[i], ck[i] > tau, r) : -1;
-        }
-        emit(at, cp, ck);
-        __syncthreads();
-        return;
+    for (int i = 0; i < kCandPerThread; ++i) {
+        const uint32_t q = i * kBlock + t;
+        ck[i] = q < ncand ? (Src::kFloats ? score_key(__uint_as_float(sm.cand_key[q])) : sm.cand_key[q]) : 0u;
+        key_stats(ck[i], cmax, cmin, cc);
     }
-    // fallback: the same steps on the whole row, streamed again
+    block_stats(cmax, cmin, cc, sm);
+    uint32_t tau = cmax, r = T;
+    if (cmax != cmin) {
+        Radix rx;
+        rx.start(cmax, cmin, T);
+        while (rx.shift > 0) {
+            clear_hist(sm);
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < kCandPerThread; ++i)
+                if (rx.counts(ck[i], true)) atomicAdd(&sm.hist[rx.digit(ck[i])], 1u);
+            __syncthreads();
+            rx.finish(sm);
+        }
+        tau = rx.prefix;
+        r = rx.remaining;
+    }
+    // 4. position ranks
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i) {
+        const uint32_t q = i * kBlock + t;
+        if (q < ncand) Ranker::mark(sm, sm.cand_pos[q], ck[i] > tau, ck[i] == tau);
+    }
+    __syncthreads();
+    Ranker::scan(sm);
+    int32_t at[kCandPerThread];
+    uint32_t cp[kCandPerThread];
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i) {
+        const uint32_t q = i * kBlock + t;
+        cp[i] = q < ncand ? (uint32_t)sm.cand_pos[q] : 0u;
+        at[i] = (q < ncand && ck[i] >= tau) ? Ranker::slot(sm, cp[i], ck[i] > tau, r) : -1;
+    }
+    emit(at, cp, ck);
+    __syncthreads();
+}
+
+// Selects the T largest keys of positions [0, n) of `src` (n > T, n <= kSpan;
+// ties toward the lower position).  emit(slot[], position[], key[]) takes a
+// thread's batch of items (arrays of one length; slot -1 = not selected):
+// every slot in [0, T) is delivered exactly once, the slots ascending by
+// position.  Batches let the emitter issue all of a thread's output loads
+// before its stores.  src.load4(p, k) returns the keys of positions p..p+3
+// (p % 4 == 0), key 0 past n; src.load_raw4 the raw entries (float bits, -inf
+// past n, when Src::kFloats; else keys).  Ends with a barrier.
+template <class Src, class Emit>
+__device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emit& emit) {
+    const int t = threadIdx.x, w = t / kWave, lane = __lane_id();
+    const int32_t n = src.n;
+    // 1. pivot from 2048 sampled keys: threads 2r, 2r+1 read run r of 8 keys
+    uint32_t sk[4];
+    src.load4((int32_t)((((int64_t)(t >> 1) * n / kSampleRuns) & ~7ll) + 4 * (t & 1)), sk);
+    uint32_t smax = 0, smin = 0xffffffffu, scnt = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key_stats(sk[e], smax, smin, scnt);
+    if (t == 0) sm.ncand = 0;
+    block_stats(smax, smin, scnt, sm);
+    // Pivot attempts: the first aims at 1.3 T candidates; after a miss the
+    // target is corrected by the observed candidate count and the row is
+    // streamed once more; a second miss takes the exact passes below.
+    const int32_t steps = (n + 255) / 256;
+    float target = 1.3f;
+    for (int attempt = 0; attempt < 2; ++attempt) {
+        const uint32_t pivot = choose_pivot(sk, smax, smin, scnt, n, T, target, sm);
+        stream_candidates(src, pivot, sm);
+        __syncthreads();
+        const uint32_t ncand = sm.ncand;
+        Ranker::clear(sm);
+        __syncthreads();
+        if (ncand >= T && ncand <= (uint32_t)kCandMax) {
+            select_candidates<Src>(ncand, T, sm, emit);
+            return;
+        }
+        if (scnt == 0 || smax == smin) break;
+        target *= ncand < T ? fmaxf(1.25f, 1.15f * (float)T / fmaxf((float)ncand, 1.f))
+                            : fminf(0.8f, 0.9f * (float)kCandMax / (float)ncand);
+        if (t == 0) sm.ncand = 0;
+        __syncthreads();
+    }
+    // fallback: the same steps on the whole row, streamed again (first for
+    // the row's key statistics)
+    uint32_t rmax = 0, rmin = 0xffffffffu, rcnt = 0;
+    for (int32_t s = w; s < steps; s += kWaves) {
+        uint32_t k[4];
+        src.load4(s * 256 + 4 * lane, k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) key_stats(k[e], rmax, rmin, rcnt);
+    }
+    block_stats(rmax, rmin, rcnt, sm);
     uint32_t tau, r;
     if (rcnt >= T) {
         if (rmax == rmin) {
@@ -455,9 +528,23 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emi
 // ------------------------------------------------------------ key sources
 // Columns [lo, lo + n) of one fp32 score row.
 struct RowSrc {
+    static constexpr bool kFloats = true;
     const float* row;  // already offset by lo
     int32_t n;
     bool vec;
+    // raw float bits of positions p..p+3, -inf past n
+    __device__ __forceinline__ void load_raw4(int32_t p, uint32_t (&v)[4]) const {
+        if (vec && p + 3 < n) {
+            const float4 x = *reinterpret_cast<const float4*>(row + p);
+            v[0] = __float_as_uint(x.x);
+            v[1] = __float_as_uint(x.y);
+            v[2] = __float_as_uint(x.z);
+            v[3] = __float_as_uint(x.w);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = p + e < n ? __float_as_uint(row[p + e]) : kNegInfBits;
+        }
+    }
     __device__ __forceinline__ void load4(int32_t p, uint32_t (&k)[4]) const {
         if (vec && p + 3 < n) {
             const float4 v = *reinterpret_cast<const float4*>(row + p);
@@ -635,12 +722,28 @@ __device__ __forceinline__ void transform_emit_batch(const int32_t* __restrict__
 // A V1 row with the sink/tail mask applied on the fly: positions of masked
 // pages (sm.maskpage) whose member lies outside [sink, tail) read as -inf.
 struct V1Src {
+    static constexpr bool kFloats = true;
     RowSrc base;
     const int32_t* members;
     const int32_t* maskpage;  // LDS, indexed by (position - segment start) / 64
     int32_t masked_end;       // positions below it may be masked (take * 64 - lo)
     int32_t sink, tail;
     int32_t n;
+    __device__ __forceinline__ void load_raw4(int32_t p, uint32_t (&v)[4]) const {
+        base.load_raw4(p, v);
+        if (p < masked_end) {
+            const int32_t page = maskpage[p >> 6];
+            if (page >= 0) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (p + e < n) {
+                        const int32_t lg = members[(int64_t)page * 64 + ((p + e) & 63)];
+                        if (lg < sink || lg >= tail) v[e] = kNegInfBits;
+                    }
+                }
+            }
+        }
+    }
     __device__ __forceinline__ void load4(int32_t p, uint32_t (&k)[4]) const {
         base.load4(p, k);
         if (p < masked_end) {
@@ -852,11 +955,13 @@ __global__ __launch_bounds__(kBlock, 8) void transform_segments(TransformParams 
 
 // The concatenated segment candidates of a row: position q = s*T + k.
 struct CandSrc {
+    static constexpr bool kFloats = false;
     const uint32_t* keys;  // workspace keys of this row
     const int32_t* count;  // per segment
     int32_t T;
     int32_t nseg;
     int32_t n;
+    __device__ __forceinline__ void load_raw4(int32_t q, uint32_t (&k)[4]) const { load4(q, k); }
     __device__ __forceinline__ void load4(int32_t q, uint32_t (&k)[4]) const {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {

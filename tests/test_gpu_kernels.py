@@ -657,11 +657,25 @@ def _adversarial_rows(kind, g, cols):
         return (np.float32(1.0) + g.integers(0, 64, cols).astype(np.float32) * np.float32(2 ** -23)).astype(np.float32)
     if kind == "signed_zero":
         return np.where(g.random(cols) < 0.5, np.float32(0.0), np.float32(-0.0)).astype(np.float32)
+    if kind == "nan_sprinkled":  # +NaN above +inf, -NaN below -inf, payload order among NaNs
+        r = g.standard_normal(cols).astype(np.float32)
+        bits = r.view(np.uint32)
+        pos = g.random(cols) < 0.01
+        neg = ~pos & (g.random(cols) < 0.01)
+        bits[pos] = 0x7f800001 + g.integers(0, 1 << 22, int(pos.sum())).astype(np.uint32)
+        bits[neg] = 0xff800001 + g.integers(0, 1 << 22, int(neg.sum())).astype(np.uint32)
+        return r
+    if kind == "nan_heavy":  # more +NaNs than T: the pivot falls in the NaN key range
+        r = g.standard_normal(cols).astype(np.float32)
+        bits = r.view(np.uint32)
+        at = g.choice(cols, min(cols, 3000), replace=False)
+        bits[at] = 0x7fc00000 + g.integers(0, 1 << 22, at.size).astype(np.uint32) % (1 << 22)
+        return r
     raise ValueError(kind)
 
 
 @pytest.mark.parametrize("kind", ["plateau", "ascending", "descending", "neg_inf_heavy", "two_values", "tiny_spread",
-                                  "signed_zero"])
+                                  "signed_zero", "nan_sprinkled", "nan_heavy"])
 @pytest.mark.parametrize("cols", [2049, 9000, 32768, 100000])
 def test_topk_adversarial_rows(dev, kind, cols):
     g = np.random.default_rng(cols)
