@@ -963,6 +963,19 @@ struct CandSrc {
     int32_t n;
     __device__ __forceinline__ void load_raw4(int32_t q, uint32_t (&k)[4]) const { load4(q, k); }
     __device__ __forceinline__ void load4(int32_t q, uint32_t (&k)[4]) const {
+        if ((T & 3) == 0) {
+            // q % 4 == 0: the four entries lie in one segment's list, which
+            // starts 16-byte aligned
+            const int32_t s = q / T, j = q - s * T;
+            const int32_t c = s < nseg ? count[s] : 0;
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (j < c) v = *reinterpret_cast<const uint4*>(keys + q);
+            k[0] = j < c ? v.x : 0u;
+            k[1] = j + 1 < c ? v.y : 0u;
+            k[2] = j + 2 < c ? v.z : 0u;
+            k[3] = j + 3 < c ? v.w : 0u;
+            return;
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int32_t qq = q + e;
@@ -989,6 +1002,11 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_merge(V1Params p, Workspace
             const bool inf = ok && score_key(rowp[tx]) == kNegInfKey;
             v1_emit(p, row, ri, tx, ok ? tx : -1, inf);
         }
+    } else if (L <= ws.seg) {
+        // one non-empty segment: its list is the row's Top-T in position order
+        const int32_t* pos = ws.pos + ws.at(row, 0);
+        const uint32_t* keys = ws.keys + ws.at(row, 0);
+        for (int tx = threadIdx.x; tx < T; tx += kBlock) v1_emit(p, row, ri, tx, pos[tx], keys[tx] == kNegInfKey);
     } else {
         const int32_t* pos = ws.pos + ws.at(row, 0);
         select_stream(cand_source(ws, row), (uint32_t)T, sm, [&](const auto& at, const auto& q, const auto& key) {
@@ -1010,6 +1028,11 @@ __global__ __launch_bounds__(kBlock, 8) void transform_merge(TransformParams p, 
         return;
     }
     const int32_t* pos = ws.pos + ws.at(row, 0);
+    if (L <= ws.seg) {
+        // one non-empty segment: its list is the row's Top-T in position order
+        for (int tx = threadIdx.x; tx < T; tx += kBlock) transform_emit(p, row, tx, pos[tx]);
+        return;
+    }
     const int32_t nq = ws.nseg * T;
     select_stream(cand_source(ws, row), (uint32_t)T, sm, [&](const auto& at, const auto& q, const auto&) {
         constexpr int N = sizeof(at) / sizeof(at[0]);
@@ -1106,6 +1129,7 @@ int launch_topk(void (*single)(P), void (*seg)(P, Workspace), void (*merge)(P, W
     }
     V1_REQUIRE(wsp != nullptr && ws_bytes >= need, "%s: rows longer than %d columns need a workspace of %lld bytes",
                name, kSpan, (long long)need);
+    V1_REQUIRE((reinterpret_cast<uintptr_t>(wsp) & 15) == 0, "%s: the workspace must be 16-byte aligned", name);
     const Workspace ws = make_workspace(wsp, batch, plan, topk);
     V1_REQUIRE((int64_t)ws.nseg * topk <= kSpan, "%s: %d columns exceed the %lld supported at topk %d", name, cols,
                (long long)(kSpan / topk) * kSpan, topk);

@@ -302,7 +302,8 @@ def test_fused_topk_rejects_like_reference(dev):
                z(B, 16), z(B, 16), 64, True, e, True, True, z(B, 4), False)
 
 
-@pytest.mark.parametrize("B,cols,topk", [(16, 5000, 2048), (128, 131072, 2048), (3, 100000, 64), (600, 3000, 700)])
+@pytest.mark.parametrize("B,cols,topk", [(16, 5000, 2048), (128, 131072, 2048), (3, 100000, 64), (600, 3000, 700),
+                                         (6, 70000, 2047)])
 def test_topk_transform_vs_oracle(dev, B, cols, topk):
     g = np.random.default_rng(B * cols)
     scores = np.round(g.standard_normal((B, cols)) * 50).astype(np.float32)
