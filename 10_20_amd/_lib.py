@@ -74,6 +74,11 @@ _SIGNATURES = {
     "v1_gather_rows": (_c_i32, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i32, _vp, _c_i64, _c_i32,
                                 _c_i32, _vp, _vp]),
     "v1_sort_f32": (_c_i32, [_vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i64, _vp]),
+    "v1_build_initialize": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _vp]),
+    "v1_group_dots": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
+    "v1_group_anchor": (_c_i32, [_vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
+    "v1_build_assemble": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _vp]),
+    "v1_build_buckets": (_c_i32, [_vp, _c_i64, _vp, _vp, _c_i32, _vp, _vp, _vp, _vp, _vp]),
     "v1_sort_i64": (_c_i32, [_vp, _vp, _vp, _vp, _c_i32, _c_i32, _vp]),
     "v1_fingerprint": (_c_i32, [_vp, _vp, _vp, _vp, _c_i32, _c_i64, _vp]),
     "v1_match_pages": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i64, _vp]),

@@ -106,4 +106,28 @@ inline uint32_t small_div_magic(uint32_t d) {
     return (uint32_t)((((uint64_t)1 << 32) + d - 1) / d);
 }
 
+// OCP e4m3fn byte -> float (exact; codes 0x7f / 0xff, NaN in the format, read
+// as +-480, which no encoder here produces).
+__device__ __forceinline__ float e4m3_value(uint32_t c) {
+    const uint32_t e = (c >> 3) & 15, m = c & 7;
+    const float v = e == 0 ? (float)m * 0.001953125f : __builtin_ldexpf((float)(8 + m), (int)e - 10);
+    return (c & 0x80) ? -v : v;
+}
+
+// Round-to-nearest-even encoding of |x| <= 448 as OCP e4m3fn.
+__device__ __forceinline__ uint32_t e4m3_code(float x) {
+    const float a = fabsf(x);
+    uint32_t code;
+    if (a < 0.015625f) {  // below 2^-6: subnormal quanta of 2^-9 (8 quanta = the first normal)
+        code = (uint32_t)rintf(a * 512.0f);
+    } else {
+        int e;
+        frexpf(a, &e);  // a = f * 2^e, f in [0.5, 1)
+        e -= 1;         // a in [2^e, 2^(e+1))
+        const uint32_t m = (uint32_t)rintf(__builtin_ldexpf(a, -e) * 8.0f - 8.0f);  // 0..8
+        code = (uint32_t)((e + 7) << 3) + m;  // m == 8 carries into the exponent
+    }
+    return code | (x < 0.f ? 0x80u : 0u);
+}
+
 }  // namespace v1

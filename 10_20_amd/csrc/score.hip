@@ -87,28 +87,6 @@ constexpr int kRecWeights = kRecScales + kPieces * 4;
 constexpr int64_t kPieceRowBytes = kRecWeights + 64 * 4;
 static_assert(kRecWeights % 16 == 0 && kPieceRowBytes % 16 == 0, "16-byte aligned record fields");
 
-__device__ __forceinline__ float e4m3_value(uint32_t c) {
-    const uint32_t e = (c >> 3) & 15, m = c & 7;
-    const float v = e == 0 ? (float)m * 0.001953125f : __builtin_ldexpf((float)(8 + m), (int)e - 10);
-    return (c & 0x80) ? -v : v;
-}
-
-// Round-to-nearest-even encoding of |x| <= 448 as OCP e4m3fn.
-__device__ __forceinline__ uint32_t e4m3_code(float x) {
-    const float a = fabsf(x);
-    uint32_t code;
-    if (a < 0.015625f) {  // below 2^-6: subnormal quanta of 2^-9 (8 quanta = the first normal)
-        code = (uint32_t)rintf(a * 512.0f);
-    } else {
-        int e;
-        frexpf(a, &e);  // a = f * 2^e, f in [0.5, 1)
-        e -= 1;         // a in [2^e, 2^(e+1))
-        const uint32_t m = (uint32_t)rintf(__builtin_ldexpf(a, -e) * 8.0f - 8.0f);  // 0..8
-        code = (uint32_t)((e + 7) << 3) + m;  // m == 8 carries into the exponent
-    }
-    return code | (x < 0.f ? 0x80u : 0u);
-}
-
 // One wave per query row: q' = sum_h w_h q_h split into its pieces, and the
 // record described above.
 __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float* w, int32_t rows, int32_t heads,

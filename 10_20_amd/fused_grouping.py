@@ -1,4 +1,12 @@
-"""Drop-in `_sort` of sglang/srt/layers/attention/v1_native/fused_grouping.py:64-76.
+"""Drop-ins `_dots`, `_anchor` and `_sort` of
+sglang/srt/layers/attention/v1_native/fused_grouping.py:38-76.
+
+`_dots[(programs, heads)](U, P, A, S, FLAG, N, START, MODE)`: 16 positions per
+program; the score of position i is the dot of member P[i] with its group's
+first member (MODE 0) or anchor A[group, MODE-1] (MODE 1, 2), minus the
+previous score for MODE 2 (four-partial fp32 sums, no fused multiply-add).
+`_anchor[(groups, heads)](P, A, S, FLAG, N, SLOT)`: A[group, SLOT] = the member
+at the group's leftmost minimum score.
 
 `_sort[(groups, heads)](P, O, S, FLAG, N)`: when FLAG < 0, every group g of N
 members of head h (offset h*4096, as in the reference) is reordered by
@@ -26,6 +34,26 @@ def _sort_launch(grid, P, O, S, FLAG, N):
 
 
 _sort = _Kernel("_sort", _sort_launch)
+
+
+def _dots_launch(grid, U, P, A, S, FLAG, N, START, MODE):
+    _lib.require_gpu(U, P, A, S, FLAG)
+    if U.dtype != torch.float32 or S.dtype != torch.float32 or P.dtype != torch.int32 or A.dtype != torch.int32:
+        raise ValueError("_dots: U/S must be float32 and P/A int32")
+    _lib.call("v1_group_dots", _lib.ptr(U), _lib.ptr(P), _lib.ptr(A), _lib.ptr(S), _lib.ptr(FLAG), int(N),
+              int(START), int(MODE), grid[0], grid[1] if len(grid) > 1 else 1, _lib.stream_of(U))
+
+
+def _anchor_launch(grid, P, A, S, FLAG, N, SLOT):
+    _lib.require_gpu(P, A, S, FLAG)
+    if S.dtype != torch.float32 or P.dtype != torch.int32 or A.dtype != torch.int32:
+        raise ValueError("_anchor: S must be float32 and P/A int32")
+    _lib.call("v1_group_anchor", _lib.ptr(P), _lib.ptr(A), _lib.ptr(S), _lib.ptr(FLAG), int(N), int(SLOT), grid[0],
+              grid[1] if len(grid) > 1 else 1, _lib.stream_of(S))
+
+
+_dots = _Kernel("_dots", _dots_launch)
+_anchor = _Kernel("_anchor", _anchor_launch)
 
 
 def sort_groups_i64(perm, out, keys, n, flag=None):

@@ -96,6 +96,27 @@ def _release(grid, TABLE, REFS, FREE, COUNT):
     _lib.call("v1_release", _lib.ptr(TABLE), _lib.ptr(REFS), _lib.ptr(FREE), _lib.ptr(COUNT), 16, _stream(TABLE))
 
 
+# -------------------------------------------------------------- index build
+def _initialize(grid, K, KS, TABLE, META, UNIT, PERM, FLAG):
+    """kernels.py:9-30: 16 tokens per program; FLAG = -1 when META[2] else 0."""
+    _lib.require_gpu(K, KS, TABLE, META, UNIT, PERM, FLAG)
+    if UNIT.dtype != torch.float32 or PERM.dtype != torch.int32:
+        raise ValueError("initialize: UNIT must be float32 and PERM int32")
+    _lib.call("v1_build_initialize", _lib.ptr(K), _lib.ptr(KS), _lib.ptr(TABLE), _lib.ptr(META), _lib.ptr(UNIT),
+              _lib.ptr(PERM), _lib.ptr(FLAG), grid[0], _stream(UNIT))
+
+
+def _assemble(grid, K, KS, TABLE, META, IDS, TMP, TMPS, CENTERS, CS, MAP):
+    """kernels.py:33-54: program (page, g) copies members g*8..g*8+7 of page
+    and writes their FP8 center."""
+    _lib.require_gpu(K, KS, TABLE, META, IDS, TMP, TMPS, CENTERS, CS, MAP)
+    _lib.call("v1_build_assemble", _lib.ptr(K), _lib.ptr(KS), _lib.ptr(TABLE), _lib.ptr(META), _lib.ptr(IDS),
+              _lib.ptr(TMP), _lib.ptr(TMPS), _lib.ptr(CENTERS), _lib.ptr(CS), _lib.ptr(MAP), grid[0],
+              grid[1] if len(grid) > 1 else 1, _stream(TMP))
+
+
+initialize = _Kernel("initialize", _initialize)
+assemble = _Kernel("assemble", _assemble)
 fingerprint = _Kernel("fingerprint", _fingerprint)
 match_pages = _Kernel("match_pages", _match_pages)
 allocate = _Kernel("allocate", _allocate)

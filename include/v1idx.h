@@ -217,6 +217,42 @@ int v1_sort_i64(const int32_t* perm, int32_t* out, const int64_t* keys, const in
                 int32_t n, int32_t groups, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Index-build producer (the pages the query path reads): per 1024-token
+ * bucket of 16 native pages, unit vectors, a balanced cosine bisection into
+ * groups of 8, then the permuted pages, member map and FP8 centers.
+ * Arithmetic: every 128-wide fp32 sum keeps four partial sums (dims d = r
+ * mod 4, ascending d, no fused multiply-add) then (p0 + p1) + (p2 + p3);
+ * unit_d = c_d * (s / max(||x||, 1e-12)); center means add the 8 members in
+ * order, times 1/8.  K / KS and TMP / TMPS and CENTERS / CS are byte / fp32
+ * views of the same pages, indexed as in the reference.
+ * ---------------------------------------------------------------------- */
+/* initialize: sglang/srt/layers/attention/v1_deepseek/kernels.py:9-30 (grid
+ * (programs,), 16 tokens each; FLAG = meta[2] ? -1 : 0). */
+int v1_build_initialize(const void* K, const float* KS, const int32_t* table, const int32_t* meta, float* unit,
+                        int32_t* perm, int32_t* flag, int32_t programs, void* stream);
+/* _dots: sglang/srt/layers/attention/v1_native/fused_grouping.py:38-52 (grid
+ * (programs, heads), 16 positions each; runs when *flag < 0). */
+int v1_group_dots(const float* U, const int32_t* P, const int32_t* A, float* S, const int32_t* flag, int32_t N,
+                  int32_t start, int32_t mode, int32_t programs, int32_t heads, void* stream);
+/* _anchor: fused_grouping.py:54-61 (grid (groups, heads); leftmost minimum). */
+int v1_group_anchor(const int32_t* P, int32_t* A, const float* S, const int32_t* flag, int32_t N, int32_t slot,
+                    int32_t groups, int32_t heads, void* stream);
+/* assemble: sglang/srt/layers/attention/v1_deepseek/kernels.py:33-54 (grid
+ * (pages, groups) = (16, 8); runs when meta[2] != 0). */
+int v1_build_assemble(const void* K, const float* KS, const int32_t* table, const int32_t* meta,
+                      const int32_t* ids, void* tmp, float* tmps, void* centers, float* cs, int32_t* map,
+                      int32_t pages, int32_t groups, void* stream);
+/* The chain initialize -> 7 x (3 _dots, 2 _anchor, _sort) -> assemble of
+ * sglang/srt/layers/attention/v1_deepseek/runtime.py:171-216 for a batch of
+ * buckets in one launch: bucket b reads pages tables[b*16 .. b*16+15] of the
+ * pool and writes perm [b, 1024] (token order, 0..1023), tmp [b, 16 pages],
+ * mapping [b, 1024] = starts[b] + perm and centers [b, 2 pages].  Identical
+ * results to the chain of the entry points above.  Table entries outside
+ * [0, pool_pages) read page 0. */
+int v1_build_buckets(const void* pool, int64_t pool_pages, const int32_t* tables, const int32_t* starts,
+                     int32_t buckets, int32_t* perm, void* tmp, int32_t* mapping, void* centers, void* stream);
+
+/* ------------------------------------------------------------------------
  * Page manager: sglang/srt/layers/attention/v1_deepseek/kernels.py:57-179
  * (fingerprint 57-69, match_pages 72-113, allocate 116-131, publish 134-167,
  * release 170-179).  Each call handles one 16-page bucket record gated by

@@ -539,3 +539,155 @@ def paged_logits(q8, w, native, block_table, lens, max_len, relu=True, clean=Tru
             dots = np.maximum(dots, 0.0)
         out[r, :n] = (w[r].astype(np.float64)[:, None] * dots).sum(axis=0) * s
     return out
+
+
+# ------------------------------------------------------------ index build
+# The producer of the pages the query path reads: per 1024-token bucket
+# (16 native pages), unit vectors, a balanced cosine bisection into groups of
+# 8 (runtime.py:171-216), then the permuted pages, member map and FP8 group
+# centers (kernels.py:33-54).  The reference's 128-wide fp32 sums are Triton
+# reductions whose order is not specified; this build fixes its own order
+# (reduce128 below) and the GPU kernels reproduce it bit for bit.
+BUILD_TOKENS = 1024
+BUILD_LEVELS = (1024, 512, 256, 128, 64, 32, 16)
+
+
+def reduce128(prod):
+    """Sum over the last axis (a multiple of 4 wide) in this build's order:
+    four partial sums over dims d = r (mod 4), each taken in ascending d with
+    one fp32 rounding per addition, then (p0 + p1) + (p2 + p3)."""
+    prod = np.asarray(prod, dtype=np.float32)
+    acc = np.zeros(prod.shape[:-1] + (4,), dtype=np.float32)
+    for d in range(0, prod.shape[-1], 4):
+        acc = (acc + prod[..., d:d + 4]).astype(np.float32)
+    return ((acc[..., 0] + acc[..., 1]) + (acc[..., 2] + acc[..., 3])).astype(np.float32)
+
+
+def bucket_tokens(native, table):
+    """FP8 key bytes [1024, 128] and fp32 scales [1024] of a bucket's tokens:
+    token i lives in native page table[i // 64], slot i % 64."""
+    pages = np.asarray(table, dtype=np.int64)[np.arange(BUILD_TOKENS) // 64]
+    slot = np.arange(BUILD_TOKENS) % 64
+    codes = native[pages[:, None], slot[:, None] * 128 + np.arange(128)[None, :]]
+    scales = native[:, 8192:].copy().view(np.float32)[pages, slot]
+    return codes, scales
+
+
+def unit_vectors(codes, scales):
+    """kernels.py:9-30 (x = fp8 * scale, x / max(||x||, 1e-12)), in this
+    build's rounding: x_d = fl(c_d * s), ||x|| = sqrt(reduce128(x * x)),
+    f = fl(s / max(||x||, 1e-12)), unit_d = fl(c_d * f)."""
+    c = e4m3_decode(codes)
+    s = np.asarray(scales, dtype=np.float32)
+    x = (c * s[:, None]).astype(np.float32)
+    norm = np.sqrt(reduce128((x * x).astype(np.float32))).astype(np.float32)
+    f = (s / np.maximum(norm, np.float32(1e-12))).astype(np.float32)
+    return (c * f[:, None]).astype(np.float32)
+
+
+def build_initialize(native, table):
+    """kernels.py:9-30 for one active bucket: unit [1024, 128], perm = 0..1023."""
+    codes, scales = bucket_tokens(native, table)
+    return unit_vectors(codes, scales), np.arange(BUILD_TOKENS, dtype=np.int32)
+
+
+def group_dots(unit, perm, anchor, scores, n, start, mode):
+    """fused_grouping.py:38-52 (one head, len(perm) positions), in place on scores:
+    mode 0 dots each member with its group's first member, modes 1 / 2 with
+    anchor[group, mode - 1]; mode 2 subtracts the previous scores."""
+    i = np.arange(len(perm))
+    group = i // n
+    ids = np.asarray(perm, dtype=np.int64)[i] - start
+    if mode == 0:
+        anc = np.asarray(perm, dtype=np.int64)[group * n] - start
+    else:
+        anc = np.asarray(anchor, dtype=np.int64)[group, mode - 1] - start
+    value = reduce128((unit[ids] * unit[anc]).astype(np.float32))
+    if mode == 2:
+        value = (value - np.asarray(scores, dtype=np.float32)).astype(np.float32)
+    scores[:] = value
+
+
+def group_anchor(perm, anchor, scores, n, slot):
+    """fused_grouping.py:54-61: anchor[g, slot] = member at the group's first
+    minimum score (-0.0 == +0.0)."""
+    for g in range(len(perm) // n):
+        sc = np.asarray(scores[g * n:(g + 1) * n], dtype=np.float32)
+        anchor[g, slot] = perm[g * n + int(np.argmin(sc))]
+
+
+def group_bisect(unit, start=0):
+    """runtime.py:183-215: for n = 1024 .. 16, three dots / two anchors per
+    group of n, then a stable descending sort of each group by the last
+    scores (so the next level's groups are its halves).  Returns the final
+    member order (start + token index) and the anchors [levels, groups, 2]."""
+    perm = (start + np.arange(BUILD_TOKENS)).astype(np.int32)
+    scores = np.zeros(BUILD_TOKENS, dtype=np.float32)
+    anchors = np.full((len(BUILD_LEVELS), 64, 2), -1, dtype=np.int32)
+    for li, n in enumerate(BUILD_LEVELS):
+        anchor = np.zeros((BUILD_TOKENS // n, 2), dtype=np.int32)
+        for mode in (0, 1, 2):
+            group_dots(unit, perm, anchor, scores, n, start, mode)
+            if mode < 2:
+                group_anchor(perm, anchor, scores, n, mode)
+        anchors[li, :BUILD_TOKENS // n] = anchor
+        perm = sort_f32(perm, scores, n, BUILD_TOKENS // n)
+    return perm, anchors
+
+
+_E4M3_POS = np.where(np.arange(127) >> 3 == 0, (np.arange(127) & 7) / 8.0 * 2.0 ** -6,
+                     (1 + (np.arange(127) & 7) / 8.0) * 2.0 ** ((np.arange(127) >> 3) - 7.0))
+
+
+def e4m3_encode(x):
+    """Round-to-nearest-even float32 -> e4m3fn byte (|x| <= 448)."""
+    x = np.asarray(x, dtype=np.float32)
+    a = np.abs(x).astype(np.float64)
+    assert a.size == 0 or float(a.max()) <= 448.0
+    hi = np.clip(np.searchsorted(_E4M3_POS, a, side="left"), 0, 126)
+    lo = np.clip(hi - 1, 0, 126)
+    dl, dh = a - _E4M3_POS[lo], _E4M3_POS[hi] - a
+    pick_hi = (dh < dl) | ((dh == dl) & ((hi & 1) == 0))
+    return np.where(pick_hi, hi, lo).astype(np.uint8) | (np.signbit(x).astype(np.uint8) << 7)
+
+
+def center_scale(amax):
+    """Smallest power of two >= fl(max(amax, 1e-4) / 448) (the exp2(ceil(log2(.)))
+    of kernels.py:46-48, exactly)."""
+    v = (np.maximum(np.asarray(amax, dtype=np.float32), np.float32(1e-4)) / np.float32(448.0)).astype(np.float32)
+    m, e = np.frexp(v)
+    e = np.where(m == 0.5, e - 1, e)
+    return np.ldexp(np.float32(1.0), e).astype(np.float32)
+
+
+def build_assemble(native, table, ids, start):
+    """kernels.py:33-54 for one active bucket: TMP [16, 8448] (page p slot i =
+    token ids[p*64 + i] with its scale), MAP [16, 64] = start + id, and 128
+    FP8 centers (mean of 8 consecutive members, power-of-two scale) packed as
+    CENTERS [2, 8448].  The mean is the sum over the 8 members in order, one
+    fp32 rounding per product and per addition, times 1/8."""
+    codes, scales = bucket_tokens(native, table)
+    ids = np.asarray(ids, dtype=np.int64)
+    tmp = np.zeros((16, 8448), dtype=np.uint8)
+    tmp[:, :8192] = codes[ids].reshape(16, 8192)
+    tmp[:, 8192:] = scales[ids].astype(np.float32).reshape(16, 64).view(np.uint8)
+    mapping = (start + ids).astype(np.int32).reshape(16, 64)
+    x = (e4m3_decode(codes[ids]) * scales[ids][:, None]).astype(np.float32).reshape(128, 8, 128)
+    acc = x[:, 0]
+    for j in range(1, 8):
+        acc = (acc + x[:, j]).astype(np.float32)
+    mean = (acc * np.float32(0.125)).astype(np.float32)
+    cs = center_scale(np.abs(mean).max(axis=1))
+    centers = np.zeros((2, 8448), dtype=np.uint8)
+    centers[:, :8192] = e4m3_encode((mean / cs[:, None]).astype(np.float32)).reshape(2, 8192)
+    centers[:, 8192:] = cs.reshape(2, 64).view(np.uint8)
+    return tmp, mapping, centers
+
+
+def index_build(native, table, start):
+    """One bucket's producer chain (runtime.py:171-228 up to assemble):
+    returns (perm, tmp, mapping, centers)."""
+    unit, _ = build_initialize(native, table)
+    perm, _ = group_bisect(unit, 0)
+    tmp, mapping, centers = build_assemble(native, table, perm, start)
+    return perm, tmp, mapping, centers

@@ -1,0 +1,174 @@
+"""Index-build producer on the GPU against the oracle: the per-kernel drop-ins
+(kernels.initialize / assemble, fused_grouping._dots / _anchor / _sort) with
+the reference's launch shapes, their chain as runtime.py:171-216 runs it, and
+the batched one-launch build (indexbuild.build_buckets), bit for bit."""
+import importlib
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+from oracle import v1 as O  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+W = importlib.import_module("10_20_amd.workloads")
+
+
+@pytest.fixture(scope="module")
+def mods():
+    return (importlib.import_module("10_20_amd.kernels"), importlib.import_module("10_20_amd.fused_grouping"),
+            importlib.import_module("10_20_amd.indexbuild"))
+
+
+def T(a, dev="cuda:0"):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def H(t):
+    return t.detach().cpu().numpy()
+
+
+def _pool(seed, pages=24, data=None, codes=None):
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((pages * 64, 128)).astype(np.float32) if data is None else data
+    k8, ks = W.quantize_rows(x)
+    if codes is not None:
+        k8[:codes.shape[0]] = codes
+    return W.pack_pages(k8, ks)
+
+
+def _chain(mods, native_d, table_d, meta_d):
+    K, FG, _ = mods
+    dev = native_d.device
+    unit = torch.empty((1024, 128), device=dev, dtype=torch.float32)
+    perm = [torch.empty(1024, device=dev, dtype=torch.int32) for _ in range(2)]
+    anchor = torch.empty((64, 2), device=dev, dtype=torch.int32)
+    scores = torch.empty(1024, device=dev, dtype=torch.float32)
+    flag = torch.zeros((), device=dev, dtype=torch.int32)
+    tmp = torch.zeros((16, 8448), device=dev, dtype=torch.uint8)
+    centers = torch.zeros((2, 8448), device=dev, dtype=torch.uint8)
+    mapping = torch.empty((16, 64), device=dev, dtype=torch.int32)
+    K.initialize[(64,)](native_d, native_d.view(torch.float32), table_d, meta_d, unit, perm[0], flag, num_warps=4)
+    cur = 0
+    for n in O.BUILD_LEVELS:
+        for mode in (0, 1, 2):
+            FG._dots[(64, 1)](unit, perm[cur], anchor, scores, flag, n, 0, mode, num_warps=4, enable_fp_fusion=False)
+            if mode < 2:
+                FG._anchor[(1024 // n, 1)](perm[cur], anchor, scores, flag, n, mode, num_warps=4)
+        FG._sort[(1024 // n, 1)](perm[cur], perm[1 - cur], scores, flag, n, num_warps=4)
+        cur = 1 - cur
+    K.assemble[(16, 8)](native_d, native_d.view(torch.float32), table_d, meta_d, perm[cur], tmp, tmp.view(torch.float32),
+                        centers, centers.view(torch.float32), mapping, num_warps=4)
+    return unit, perm[cur], tmp, mapping, centers, flag
+
+
+def test_initialize_vs_oracle(mods):
+    K, _, _ = mods
+    every = np.arange(256, dtype=np.uint8)
+    every = every[(every & 0x7f) != 0x7f]  # all finite codes, subnormals and -0 included
+    codes = np.resize(every, (64, 128))
+    native = _pool(1, codes=codes)
+    table = np.array([0] + list(np.random.default_rng(1).permutation(np.arange(1, 24))[:15]), np.int32)
+    nd, td = T(native), T(table)
+    unit = torch.full((1024, 128), 7.0, device="cuda:0")
+    perm = torch.full((1024,), -5, device="cuda:0", dtype=torch.int32)
+    flag = torch.zeros((), device="cuda:0", dtype=torch.int32)
+    K.initialize[(64,)](nd, nd.view(torch.float32), td, T(np.int32([4096, 0, 1])), unit, perm, flag)
+    e_unit, e_perm = O.build_initialize(native, table)
+    assert np.array_equal(H(unit).view(np.int32), e_unit.view(np.int32))
+    assert np.array_equal(H(perm), e_perm) and int(flag) == -1
+    unit.fill_(7.0)
+    K.initialize[(64,)](nd, nd.view(torch.float32), td, T(np.int32([4096, 0, 0])), unit, perm, flag)
+    assert int(flag) == 0 and bool((unit == 7.0).all())
+
+
+def test_dots_and_anchor_kats(mods):
+    _, FG, _ = mods
+    dev = "cuda:0"
+    start = 100
+    unit = torch.zeros((16, 128), device=dev)
+    signs = torch.tensor([1.0, -1.0] * 8, device=dev)
+    unit[:, 0] = signs
+    order = [2, 1, 4, 3, 6, 5, 8, 7, 10, 9, 12, 11, 14, 13, 0, 15]
+    perm = torch.tensor([start + i for i in order], device=dev, dtype=torch.int32)
+    anchor = torch.tensor([[start + 1, start + 2]], device=dev, dtype=torch.int32)
+    scores = torch.empty(16, device=dev)
+    flag = torch.tensor(-1, device=dev, dtype=torch.int32)
+    for mode in (0, 1, 2):
+        scores.copy_(-signs[torch.tensor(order, device=dev)] if mode == 2 else torch.zeros_like(scores))
+        FG._dots[(1, 1)](unit, perm, anchor, scores, flag, 16, start, mode, num_warps=4, enable_fp_fusion=False)
+        assert H(scores).tolist() == [(1 if i % 2 == 0 else -1) * [1, -1, 2][mode] for i in order]
+        flag.fill_(0)
+        scores.fill_(77)
+        FG._dots[(1, 1)](unit, perm, anchor, scores, flag, 16, start, mode)
+        assert H(scores).tolist() == [77] * 16
+        flag.fill_(-1)
+    perm = torch.tensor([115, 101, 102, 100] + list(range(103, 115)), device=dev, dtype=torch.int32)
+    scores = torch.tensor([4, -3, 2, -3] + [5] * 12, device=dev, dtype=torch.float32)
+    anchor = torch.full((1, 2), -99, device=dev, dtype=torch.int32)
+    for slot in (0, 1):
+        FG._anchor[(1, 1)](perm, anchor, scores, flag, 16, slot, num_warps=4)
+    assert H(anchor).tolist() == [[101, 101]]
+    flag.fill_(0)
+    anchor.fill_(-99)
+    FG._anchor[(1, 1)](perm, anchor, scores, flag, 16, 0)
+    assert H(anchor).tolist() == [[-99, -99]]
+
+
+def _cases():
+    g = np.random.default_rng(21)
+    random = _pool(2)
+    dup = np.repeat(g.standard_normal((64, 128)).astype(np.float32), 24, axis=0)  # each token 24 times: ties
+    dups = _pool(3, data=dup)
+    label = g.permutation(np.arange(24 * 64) % 8)
+    x = g.standard_normal((24 * 64, 128)).astype(np.float32) * 0.05
+    x[:, 0] += 4 * np.where(label & 4, -1.0, 1.0)
+    x[:, 16] += 2 * np.where(label & 2, -1.0, 1.0)
+    x[:, 32] += np.where(label & 1, -1.0, 1.0)
+    clusters = _pool(4, data=x)
+    zeros = _pool(5)
+    zeros[3, :8192] = 0  # a page of zero keys: unit vectors of zeros
+    return [("random", random), ("duplicates", dups), ("clusters", clusters), ("zero_page", zeros)]
+
+
+@pytest.mark.parametrize("case", [c[0] for c in _cases()])
+def test_chain_vs_oracle(mods, case):
+    native = dict(_cases())[case]
+    table = np.random.default_rng(len(case)).permutation(24)[:16].astype(np.int32)
+    nd = T(native)
+    unit, perm, tmp, mapping, centers, flag = _chain(mods, nd, T(table), T(np.int32([8192, 1, 1])))
+    e_perm, e_tmp, e_map, e_centers = O.index_build(native, table, 8192)
+    assert np.array_equal(H(perm), e_perm)
+    assert np.array_equal(H(tmp), e_tmp)
+    assert np.array_equal(H(mapping), e_map)
+    assert np.array_equal(H(centers), e_centers)
+
+
+def test_build_buckets_vs_oracle_and_chain(mods):
+    _, _, IB = mods
+    cases = _cases()
+    g = np.random.default_rng(9)
+    # one pool holding every case's pages; buckets draw their 16 pages from one case each
+    pool = np.concatenate([c[1] for c in cases])
+    tables, starts = [], []
+    for rep in range(2):
+        for ci in range(len(cases)):
+            tables.append(ci * 24 + g.permutation(24)[:16])
+            starts.append(int(g.integers(0, 1 << 20)) * 64)
+    tables = np.array(tables, np.int32)
+    starts = np.array(starts, np.int32)
+    pd = T(pool)
+    perm, tmp, mapping, centers = IB.build_buckets(pd, T(tables), T(starts))
+    for b in range(len(tables)):
+        e_perm, e_tmp, e_map, e_centers = O.index_build(pool, tables[b], int(starts[b]))
+        assert np.array_equal(H(perm[b]), e_perm), b
+        assert np.array_equal(H(tmp[b]), e_tmp), b
+        assert np.array_equal(H(mapping[b]), e_map), b
+        assert np.array_equal(H(centers[b]), e_centers), b
+    # the per-kernel chain gives the same bytes
+    c = _chain(mods, pd, T(tables[1]), T(np.int32([int(starts[1]), 0, 1])))
+    assert torch.equal(c[1], perm[1]) and torch.equal(c[2], tmp[1]) and torch.equal(c[4], centers[1])

@@ -1,0 +1,203 @@
+"""Oracle of the index-build producer (initialize, dots / anchor / sort
+bisection, assemble) pinned against the reference's own known answers
+(sglang/srt/layers/attention/v1_native/test_fused_grouping_small.py) and
+against properties that a wrong sign, order, anchor or reduction would break."""
+import importlib
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+from oracle import v1 as O  # noqa: E402
+
+W = importlib.import_module("10_20_amd.workloads")
+
+
+def test_dots_three_modes_kat():
+    # test_fused_grouping_small.py:57-76: member ids (not positions) select vectors
+    start = 100
+    unit = np.zeros((16, 128), np.float32)
+    signs = np.array([1, -1] * 8, np.float32)
+    unit[:, 0] = signs
+    order = [2, 1, 4, 3, 6, 5, 8, 7, 10, 9, 12, 11, 14, 13, 0, 15]
+    perm = np.array([start + i for i in order], np.int32)
+    anchor = np.array([[start + 1, start + 2]], np.int32)
+    for mode in (0, 1, 2):
+        scores = (-signs[order]).astype(np.float32) if mode == 2 else np.zeros(16, np.float32)
+        O.group_dots(unit, perm, anchor, scores, 16, start, mode)
+        expected = [(1 if i % 2 == 0 else -1) * [1, -1, 2][mode] for i in order]
+        assert scores.tolist() == expected
+
+
+def test_anchor_left_tie_kat():
+    # test_fused_grouping_small.py:78-89: leftmost minimum, not the smaller id
+    perm = np.array([115, 101, 102, 100] + list(range(103, 115)), np.int32)
+    scores = np.array([4, -3, 2, -3] + [5] * 12, np.float32)
+    anchor = np.full((1, 2), -99, np.int32)
+    for slot in (0, 1):
+        O.group_anchor(perm, anchor, scores, 16, slot)
+    assert anchor.tolist() == [[101, 101]]
+    anchor[:] = -99
+    O.group_anchor(perm, anchor, np.array([0.0, -0.0] + [1.0] * 14, np.float32), 16, 0)
+    assert anchor[0, 0] == 115  # -0.0 == +0.0: the first one
+
+
+def test_one_split_chain_kat():
+    # test_fused_grouping_small.py:104-118: 16 members -> two groups of 8
+    unit = np.zeros((16, 128), np.float32)
+    unit[:, 0] = [1, -1] * 8
+    perm = np.arange(100, 116, dtype=np.int32)
+    anchor = np.zeros((1, 2), np.int32)
+    scores = np.zeros(16, np.float32)
+    for mode in (0, 1, 2):
+        O.group_dots(unit, perm, anchor, scores, 16, 100, mode)
+        if mode < 2:
+            O.group_anchor(perm, anchor, scores, 16, mode)
+    out = O.sort_f32(perm, scores, 16, 1)
+    assert anchor.tolist() == [[101, 100]]
+    assert out.tolist() == list(range(100, 116, 2)) + list(range(101, 116, 2))
+
+
+def test_reduce128_order():
+    # lane 0 gets 2^24, 1, 1 (dims 0, 4, 8): each +1 rounds away, lane 1 gets 2
+    prod = np.zeros((1, 128), np.float32)
+    prod[0, 0], prod[0, 4], prod[0, 8], prod[0, 1] = 2.0 ** 24, 1.0, 1.0, 2.0
+    got = float(O.reduce128(prod)[0])
+    assert got == 2.0 ** 24 + 2
+    seq = np.float32(0)
+    for v in prod[0]:
+        seq = np.float32(seq + v)
+    assert float(seq) != got  # a sequential order gives another value
+    tree = prod[0].copy()
+    while tree.size > 1:
+        tree = (tree[0::2] + tree[1::2]).astype(np.float32)
+    assert float(tree[0]) != got  # and so does a pairwise tree
+    # the last step pairs (p0 + p1) + (p2 + p3): 2^24 + 1 rounds to 2^24,
+    # -2^24 + 1 is exact, so the sum is 1; pairing (p0 + p2) + (p1 + p3) gives 2
+    prod = np.zeros((1, 128), np.float32)
+    prod[0, :4] = [2.0 ** 24, 1.0, -(2.0 ** 24), 1.0]
+    assert float(O.reduce128(prod)[0]) == 1.0
+
+
+def _bucket(seed, pages=24, data=None):
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((pages * 64, 128)).astype(np.float32) if data is None else data
+    k8, ks = W.quantize_rows(x)
+    native = W.pack_pages(k8, ks)
+    table = g.permutation(pages)[:16].astype(np.int32)
+    return native, table
+
+
+def test_unit_vectors_kat_and_norm():
+    # test_fused_grouping_small.py:35-50 with FP8 keys: (3, 4) * 2^k -> (0.6, 0.8)
+    codes = np.zeros((16, 128), np.uint8)
+    codes[:, 0] = O.e4m3_encode(np.float32(3.0) * 2.0 ** np.arange(-9, 7).astype(np.float32))
+    codes[:, 1] = O.e4m3_encode(np.float32(4.0) * 2.0 ** np.arange(-9, 7).astype(np.float32))
+    unit = O.unit_vectors(codes, np.full(16, 0.5, np.float32))
+    np.testing.assert_allclose(unit[:, :2], np.tile([0.6, 0.8], (16, 1)), rtol=2e-7)
+    assert (unit[:, 2:] == 0).all()
+    native, table = _bucket(3)
+    unit, perm = O.build_initialize(native, table)
+    assert perm.tolist() == list(range(1024))
+    np.testing.assert_allclose(np.linalg.norm(unit.astype(np.float64), axis=1), 1.0, rtol=1e-6)
+    codes, scales = O.bucket_tokens(native, table)
+    x = O.e4m3_decode(codes).astype(np.float64) * scales[:, None]
+    np.testing.assert_allclose(unit, x / np.linalg.norm(x, axis=1, keepdims=True), rtol=0, atol=3e-7)
+
+
+def test_e4m3_encode_matches_torch():
+    g = np.random.default_rng(0)
+    x = np.concatenate([g.standard_normal(20000) * 50, g.uniform(-448, 448, 20000),
+                        O.e4m3_decode(np.arange(256, dtype=np.uint8)[np.arange(256) % 128 != 127]),
+                        [0.0, -0.0, 448.0, -448.0, 2.0 ** -10, 3 * 2.0 ** -11]]).astype(np.float32)
+    x = x[np.abs(x) <= 448]
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(O.e4m3_encode(x), ref)
+
+
+def test_bisection_splits_hierarchical_clusters():
+    """Eight clusters of 128 tokens at +-4 e0 +- 2 e1 +- e2 (plus small noise):
+    each split projects on the line between the group's two anchors, which is
+    dominated by the largest component the group still mixes, so the first
+    three levels split by the sign of e0, then e1, then e2, and every group of
+    128 is one cluster."""
+    g = np.random.default_rng(5)
+    label = g.permutation(np.arange(1024) % 8)
+    sign = lambda bit: np.where((label >> bit) & 1, -1.0, 1.0)
+    x = g.standard_normal((1024, 128)).astype(np.float32) * 0.05
+    x[:, 0] += 4 * sign(2)
+    x[:, 16] += 2 * sign(1)
+    x[:, 32] += 1 * sign(0)
+    data = np.zeros((24 * 64, 128), np.float32)
+    data[:1024] = x
+    native, _ = _bucket(5, data=data)
+    table = np.arange(16, dtype=np.int32)
+    unit, _ = O.build_initialize(native, table)
+    perm, anchors = O.group_bisect(unit, 0)
+    assert sorted(perm.tolist()) == list(range(1024))
+    lab = label[perm]
+    for half in lab.reshape(2, 512):  # level 1: one sign of e0 per half
+        assert len({int(v) >> 2 for v in half}) == 1
+    for g128 in lab.reshape(8, 128):
+        assert (g128 == g128[0]).all()
+    assert len({int(v) for v in lab.reshape(8, 128)[:, 0]}) == 8
+
+
+@pytest.mark.parametrize("seed", [11, 12, 13])
+def test_bisection_matches_float64_where_decided(seed):
+    """An independent float64 bisection gives the same order on random data
+    when no decision of the chain lies within 1e-5 of a tie.  The decisions:
+    both argmins, the boundary between the halves, the leading member of each
+    half (the next level's first member) and, at the last level, the whole
+    order of each group of 16."""
+    native, table = _bucket(seed)
+    unit, _ = O.build_initialize(native, table)
+    perm32, _ = O.group_bisect(unit, 0)
+    u = unit.astype(np.float64)
+    perm = np.arange(1024)
+    margin = np.inf
+    gap = lambda v, i: float(v[i + 1] - v[i])
+    for n in O.BUILD_LEVELS:
+        new = np.empty_like(perm)
+        for gi in range(1024 // n):
+            mem = perm[gi * n:(gi + 1) * n]
+            s0 = u[mem] @ u[mem[0]]
+            b = mem[int(np.argmin(s0))]
+            sb = u[mem] @ u[b]
+            a = mem[int(np.argmin(sb))]
+            score = u[mem] @ u[a] - sb
+            margin = min(margin, gap(np.sort(s0), 0), gap(np.sort(sb), 0))
+            desc = np.sort(score)[::-1]
+            h = n // 2
+            margin = min(margin, float(desc[h - 1] - desc[h]), float(desc[0] - desc[1]), float(desc[h] - desc[h + 1]))
+            if n == O.BUILD_LEVELS[-1]:
+                margin = min(margin, float(np.min(desc[:-1] - desc[1:])))
+            new[gi * n:(gi + 1) * n] = mem[np.argsort(-score, kind="stable")]
+        perm = new
+    if margin < 1e-5:
+        pytest.skip(f"a decision within {margin:.1e} of a tie")
+    assert np.array_equal(perm32, perm)
+
+
+def test_assemble_copies_and_centers():
+    native, table = _bucket(7)
+    g = np.random.default_rng(7)
+    ids = g.permutation(1024)
+    tmp, mapping, centers = O.build_assemble(native, table, ids, 5120)
+    codes, scales = O.bucket_tokens(native, table)
+    assert np.array_equal(tmp[:, :8192].reshape(1024, 128), codes[ids])
+    assert np.array_equal(tmp[:, 8192:].copy().view(np.float32).reshape(1024), scales[ids])
+    assert np.array_equal(mapping.reshape(-1), 5120 + ids)
+    cs = centers[:, 8192:].copy().view(np.float32).reshape(128)
+    m, e = np.frexp(cs)
+    assert (m == 0.5).all()  # powers of two
+    x = O.e4m3_decode(codes[ids]).astype(np.float64) * scales[ids][:, None]
+    mean = x.reshape(128, 8, 128).mean(axis=1)
+    dec = O.e4m3_decode(centers[:, :8192].reshape(128, 128)).astype(np.float64) * cs[:, None]
+    assert (np.abs(mean) / cs[:, None] <= 448).all()
+    np.testing.assert_allclose(dec, mean, rtol=2.0 ** -4, atol=2.0 ** -9 * cs.max())
+    amax = np.abs(mean).max(axis=1)
+    assert (amax / cs > 224).all() | (amax < 1e-4 * 448).any()  # the scale is the smallest power of two
