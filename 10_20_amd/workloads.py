@@ -268,6 +268,21 @@ def config5(seed=5, rows=128, heads=64, pool_pages=32768, lo=4096, hi=131072):
                          max_ctx=int(ctx.max())))
 
 
+def config6(seed=6, pool_pages=32768, buckets=2048):
+    """Index build: every complete 1024-token bucket of a 2M-token pool, each
+    bucket's 16 pages a distinct slice of a random permutation of the pool's
+    pages (every page built once), bucket b starting at logical token b*1024."""
+    g = rng(seed)
+    if buckets * 16 > pool_pages:
+        raise ValueError("buckets need 16 distinct pages each")
+    tables = g.permutation(pool_pages)[:buckets * 16].astype(np.int32).reshape(buckets, 16)
+    starts = (np.arange(buckets, dtype=np.int64) * 1024).astype(np.int32)
+    k8, ks = quantize_rows(g.standard_normal((pool_pages * PAGE, DIM), dtype=np.float32))
+    native = pack_pages(k8, ks)
+    return Workload("config6", seed, dict(native=native, tables=tables, starts=starts),
+                    dict(buckets=buckets, pool_pages=pool_pages))
+
+
 def decode_table():
     """float32 value of each of the 256 e4m3fn codes (NaN for 0x7f / 0xff)."""
     vals = np.concatenate([_E4M3_POS, [np.nan]]).astype(np.float32)

@@ -17,6 +17,8 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
                512-page windows of a 1M-token pool of 656-byte rows
   5            decode batch: 128 requests x 64 heads, contexts 4K..128K tokens with
                their own page tables in a 2M-token pool -> Top-2048 -> gather
+  6            index build: every 1024-token bucket of a 2M-token FP8 pool (2048 buckets)
+               -> member order, reordered pages and FP8 centers, one launch
 
 Prints one JSON line: queries/sec, per-stage times, the roofline of the
 dominant kernel and the CPU baseline (the reference's torch expressions on
@@ -80,7 +82,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES bytes (HBM counter calibration) and exit")
@@ -101,7 +103,8 @@ def copy_calibration(nbytes):
 
 class Pkg:
     def __init__(self):
-        for name in ("workloads", "scoring", "topk", "native_kernels", "query_fused", "kernels", "pagepool"):
+        for name in ("workloads", "scoring", "topk", "native_kernels", "query_fused", "kernels", "pagepool",
+                     "indexbuild"):
             setattr(self, name, importlib.import_module(f"10_20_amd.{name}"))
 
 
@@ -346,7 +349,41 @@ def setup_pages(P, dev, torch, np):
     return R, stages, work_units, cpu, meta, "synthetic (PCG64 seed 2; page bytes from a seeded torch generator)"
 
 
-SETUPS = {1: setup_example, 2: setup_pages, 3: setup_gather, 4: setup_prefill, 5: setup_decode}
+# one bucket of the index build: 16 source pages read and 16 member pages written (8448 B each), two
+# center pages, the 64x16 mapping and the 1024-entry order (int32), the 16-entry table and the start
+BUILD_BUCKET_BYTES = 16 * 8448 * 2 + 2 * 8448 + 4 * 1024 * 2 + 4 * 16 + 4
+
+
+def setup_build(P, dev, torch, np):
+    """Configuration 6: index build of every bucket of a 2M-token pool."""
+    wl = P.workloads.config6()
+    a, prm = wl.arrays, wl.params
+    B = prm["buckets"]
+    pool = torch.from_numpy(a["native"]).to(dev)
+    tables = torch.from_numpy(a["tables"]).to(dev)
+    starts = torch.from_numpy(a["starts"]).to(dev)
+    out = (torch.empty((B, 1024), device=dev, dtype=torch.int32),
+           torch.empty((B, 16, 8448), device=dev, dtype=torch.uint8),
+           torch.empty((B, 16, 64), device=dev, dtype=torch.int32),
+           torch.empty((B, 2, 8448), device=dev, dtype=torch.uint8))
+    stages = [("build", lambda: P.indexbuild.build_buckets(pool, tables, starts, out=out))]
+    work_units = {"build": (BUILD_BUCKET_BYTES * B / 1e9, "GB/s", PEAK_HBM_GBS, "hbm")}
+
+    def cpu(budget):
+        from oracle import cpu_baseline
+        tps, n, threads = cpu_baseline.build_tokens_per_second(a["native"], a["tables"], a["starts"], budget)
+        return tps, threads, f"{n} of {B} buckets (initialize -> 7 bisection levels -> assemble, numpy)"
+
+    meta = {"workload": f"index build: {B} buckets of 1024 tokens (16 pages each, every page of a "
+                        f"{prm['pool_pages'] * 64 // (1 << 20)}M-token FP8 pool once) -> member order, "
+                        "reordered pages, 128 FP8 centers per bucket",
+            "global_batch": B, "seq_len": 1024, "parallelism": "single GPU"}
+    return B * 1024, stages, work_units, cpu, meta, "synthetic (PCG64 seed 6)"
+
+
+SETUPS = {1: setup_example, 2: setup_pages, 3: setup_gather, 4: setup_prefill, 5: setup_decode, 6: setup_build}
+RATE_UNITS = {2: "requests/s", 6: "tokens/s"}
+METRICS = {6: "index-build tokens/sec (initialize+bisection+assemble) and % of HBM roofline"}
 
 
 def main():
@@ -403,7 +440,7 @@ def main():
     amount, unit, peak, bound = work_units[dom]
     achieved = amount / (stage_ms[dom] / 1e3)
 
-    rate_unit = "requests/s" if args.config == 2 else "queries/s"
+    rate_unit = RATE_UNITS.get(args.config, "queries/s")
     cpu = None
     if args.cpu_budget > 0:
         qps_cpu, threads, sample = cpu_fn(args.cpu_budget)
@@ -412,7 +449,7 @@ def main():
 
     qps = rows * args.steps / (t1 - t0)
     line = {
-        "metric": "indexed queries/sec (score+Top2048+gather) and % of FP8-MFMA/HBM roofline",
+        "metric": METRICS.get(args.config, "indexed queries/sec (score+Top2048+gather) and % of FP8-MFMA/HBM roofline"),
         "value": round(qps, 1), "unit": rate_unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8-e4m3 score / fp32 accumulate / int32 indices / u8 rows", "data": data,

@@ -8,6 +8,8 @@ torch expressions for the query path, run with torch on the host cores.
   gather fancy indexing, sglang/srt/layers/attention/v1_native/test_gather_slots_small.py:18-24
   pages  the oracle's page manager, request after request (a host port of
          sglang/srt/layers/attention/v1_deepseek/kernels.py:72-167)
+  build  the oracle's index build, bucket after bucket (a host port of
+         sglang/srt/layers/attention/v1_deepseek/runtime.py:171-216)
 """
 import time
 
@@ -172,3 +174,16 @@ def pages_requests_per_second(keys, draws, lens, capacity, page_bytes, budget_s=
                                          starts[done + 1], table)
         done += 1
     return done / (time.perf_counter() - t0), done, 1
+
+
+def build_tokens_per_second(native, tables, starts, budget_s=10.0, min_buckets=2):
+    """The index build bucket after bucket on the host (the oracle's
+    initialize -> seven bisection levels -> assemble, runtime.py:171-216),
+    until the time budget ends; returns (tokens/s, buckets, threads).  numpy's
+    element-wise passes run on one thread."""
+    from . import v1 as O
+    done, t0 = 0, time.perf_counter()
+    while done < len(tables) and (done < min_buckets or time.perf_counter() - t0 < budget_s):
+        O.index_build(native, tables[done], int(starts[done]))
+        done += 1
+    return 1024.0 * done / (time.perf_counter() - t0), done, 1
