@@ -17,9 +17,10 @@
 // Two forms: per-kernel drop-ins with the reference's launch shapes, and one
 // fused kernel that builds a batch of buckets, one 1024-thread work-group per
 // bucket (thread = position in the bucket's order): the token's FP8 key stays
-// in registers, the group anchors go through LDS, each group's argmin is a
-// wave reduction plus one LDS atomic per wave, and the stable sort of a group
-// is a rank count over the group's (key, position) words.
+// in registers, an argmin winner stages its key in LDS for the lanes that
+// expand the anchor, each group is sorted by a bitonic network over its
+// unique (score, -position) words, and members move through LDS (groups
+// larger than a wave) or lane shuffles.
 #include "common.h"
 
 // No contraction in this file: every product and every sum written here rounds
@@ -198,17 +199,58 @@ __global__ __launch_bounds__(128) void assemble_kernel(const uint8_t* __restrict
 }
 
 // ------------------------------------------------------------- fused
-constexpr int kLevels = 7;  // groups of 1024, 512, ..., 16
+constexpr int kLevels = 7;      // groups of 1024, 512, ..., 16
+constexpr int kSlots = 64;      // anchor and stage slots: four per wave
+constexpr int kAncStride = 33;  // float4 per anchor slot, one of padding
+
+// A token's FP8 key and unit factor, staged for the lanes that expand it.
+struct Stage {
+    uint32_t c[kWords];
+    float f;
+    uint32_t pad[3];
+};
 
 struct BuildSmem {
-    float4 anc[kTokens / 16][kWords];         // one anchor vector per group (<= 64 groups)
-    unsigned long long rank_key[kTokens];     // (descending sort key, ~position) per position
-    unsigned long long amin[2][kTokens / 16]; // argmin words per group, modes 0 and 1
-    int32_t xtok[kTokens];                    // token at each new position
-    float xf[kTokens];                        // and its unit factor
+    union {
+        struct {
+            float4 anc[kSlots][kAncStride];  // anchor unit vectors: one per wave (groups >= 64) or group
+            Stage st[2][kSlots];             // argmin winners of the first and second dot
+        } d;                                 // live from a level's first anchor to its last dot
+        struct {
+            uint2 c[kWords / 2][kTokens];    // keys by position, 8 bytes of every row per plane
+            int32_t tok[kTokens];
+            float f[kTokens];
+        } x;                                 // live during a block-wide exchange and the final assembly
+    } u1;
+    union {
+        unsigned long long k[2][kTokens];    // sort keys crossing waves, double-buffered
+        Stage st0[kSlots];                   // first members of the next level's groups
+    } u2;
+    unsigned long long amin[2][kSlots];      // group argmin words (groups above one wave)
 };
-static_assert(sizeof(BuildSmem) <= 64 * 1024, "two work-groups per CU");
+static_assert(sizeof(BuildSmem) <= 160 * 1024, "one work-group per CU");
 
+// Orders this wave's LDS accesses across its lanes (a wave's LDS operations
+// complete in order; the wait and the empty barrier keep the compiler from
+// moving accesses across the point).
+__device__ __forceinline__ void wave_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// FP8 bytes 2H and 2H+1 of a packed word, as fp32 (exact).
+template <bool H>
+__device__ __forceinline__ float2 fp8_pair(uint32_t w) {
+    const auto v = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, H);
+    return make_float2(v[0], v[1]);
+}
+
+// One 1024-thread work-group per bucket; thread = position in the bucket's
+// current order.  Per level (groups of n): three dots against the group's
+// anchors (first member, b = argmin s0, a = argmin sb), score = dot_a - sb,
+// and a stable descending sort of every group by (score, -position).
+// Groups of at most one wave run without block barriers; larger groups
+// reduce their argmin through LDS atomics and exchange members through LDS.
 __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* __restrict__ pool, int64_t pool_pages,
                                                                 const int32_t* __restrict__ tables,
                                                                 const int32_t* __restrict__ starts,
@@ -217,123 +259,185 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
                                                                 int32_t* __restrict__ map_out,
                                                                 uint8_t* __restrict__ centers_out) {
     __shared__ BuildSmem sm;
-    const int32_t p = threadIdx.x;  // position in the bucket's current order
+    const int32_t p = threadIdx.x;
     const int64_t b = blockIdx.x;
     const int32_t* table = tables + b * 16;
     const float* pool_f = reinterpret_cast<const float*>(pool);
+    auto page_of = [&](int32_t t) __attribute__((always_inline)) {
+        int64_t page = table[t / 64];
+        if ((uint64_t)page >= (uint64_t)pool_pages) page = 0;  // ids outside the pool read page 0
+        return page;
+    };
 
     int32_t tok = p;
     uint32_t c[kWords];
-    float s, f;
-    auto fetch = [&]() __attribute__((always_inline)) {
-        int64_t page = table[tok / 64];
-        if ((uint64_t)page >= (uint64_t)pool_pages) page = 0;  // ids outside the pool read page 0
+    float f;
+    {
+        const int64_t page = page_of(tok);
         load_key(pool + page * V1_PAGE_BYTES + (tok % 64) * 128, c);
-        s = pool_f[page * kPageWords + kScaleWord + tok % 64];
-    };
-    fetch();
-    f = unit_factor(c, s);
+        f = unit_factor(c, pool_f[page * kPageWords + kScaleWord + tok % 64]);
+    }
 
-    // unit vector of this thread's token into anchor slot g
-    auto put_anchor = [&](int32_t g) __attribute__((always_inline)) {
-#pragma unroll
-        for (int w = 0; w < kWords; ++w)
-            sm.anc[g][w] = make_float4((fp8_at<0>(c[w]) * f), (fp8_at<1>(c[w]) * f),
-                                       (fp8_at<2>(c[w]) * f), (fp8_at<3>(c[w]) * f));
+    // slot of position q's group within q's wave (groups of `width` <= 64
+    // lanes): every wave owns slots 4w .. 4w+3 at every level, so levels run
+    // without block barriers never touch another wave's slots
+    auto wslot = [](int32_t q, int32_t width) __attribute__((always_inline)) {
+        return (q >> 6) * 4 + (q & (kWave - 1)) / width;
     };
-    auto dot = [&](int32_t g) __attribute__((always_inline)) {
+    auto stage_put = [&](Stage& st) __attribute__((always_inline)) {
+        uint4* dst = reinterpret_cast<uint4*>(st.c);
+#pragma unroll
+        for (int i = 0; i < kWords / 4; ++i) dst[i] = make_uint4(c[4 * i], c[4 * i + 1], c[4 * i + 2], c[4 * i + 3]);
+        st.f = f;
+    };
+    // anchor slot `slot` <- unit vector of the staged token; the `width`
+    // lanes sharing the slot expand one or two key words each
+    auto expand = [&](const Stage& st, int32_t slot, int32_t width) __attribute__((always_inline)) {
+        const int32_t j = p & (width - 1);
+        const int32_t per = width >= 32 ? 1 : 32 / width;  // 1 or 2 (width >= 16)
+        if (j * per < kWords) {
+            const float fa = st.f;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                if (q < per) {
+                    const int32_t w = j * per + q;
+                    const uint32_t cw = st.c[w];
+                    const float2 lo = fp8_pair<false>(cw), hi = fp8_pair<true>(cw);
+                    sm.u1.d.anc[slot][w] = make_float4((lo.x * fa), (lo.y * fa), (hi.x * fa), (hi.y * fa));
+                }
+            }
+        }
+    };
+    auto dot = [&](int32_t slot) __attribute__((always_inline)) {
         // the unit components are recomputed per dot: kept across the three
         // dots of a level they would need 128 more registers
 #pragma unroll
         for (int w = 0; w < kWords; ++w) asm volatile("" : "+v"(c[w]));
+        const float4* a = sm.u1.d.anc[slot];
         Acc4 acc;
 #pragma unroll 4
         for (int w = 0; w < kWords; ++w) {
-            const float4 a = sm.anc[g][w];
-            acc.add(((fp8_at<0>(c[w]) * f) * a.x), ((fp8_at<1>(c[w]) * f) * a.y),
-                    ((fp8_at<2>(c[w]) * f) * a.z), ((fp8_at<3>(c[w]) * f) * a.w));
+            const float4 av = a[w];
+            const float2 lo = fp8_pair<false>(c[w]), hi = fp8_pair<true>(c[w]);
+            acc.add(((lo.x * f) * av.x), ((lo.y * f) * av.y), ((hi.x * f) * av.z), ((hi.y * f) * av.w));
         }
         return acc.total();
     };
-    // group argmin (leftmost minimum, -0.0 == +0.0) into sm.amin[m][g]:
-    // reduce over the wave's lanes of the group, then one atomic per wave
-    auto argmin = [&](float v, int32_t n, int32_t g, int32_t m) __attribute__((always_inline)) {
+    // group argmin (leftmost minimum, -0.0 == +0.0): the winner stages its
+    // key in st[m][its slot]; returns the winner's position
+    auto argmin = [&](float v, int32_t n, int32_t width, int32_t m) __attribute__((always_inline)) {
         uint64_t k = ((uint64_t)score_key(v) << 32) | (uint32_t)p;
-        const int width = n < kWave ? n : kWave;
         for (int off = 1; off < width; off <<= 1) k = umin64(k, shfl_xor64(k, off));
-        if ((p & (width - 1)) == 0) atomicMin(&sm.amin[m][g], (unsigned long long)k);
+        if ((uint32_t)k == (uint32_t)p) stage_put(sm.u1.d.st[m][wslot(p, width)]);
+        if (n > kWave) {
+            if ((p & (kWave - 1)) == 0) atomicMin(&sm.amin[m][p / n], (unsigned long long)k);
+            __syncthreads();
+            k = sm.amin[m][p / n];
+        } else {
+            wave_sync();
+        }
+        return (int32_t)(uint32_t)k;
     };
+    // descending bitonic sort of every group of n (unique keys); strides of
+    // a wave or more go through LDS
+    auto sort_desc = [&](uint64_t key, int32_t n) __attribute__((always_inline)) {
+        const int32_t i = p & (n - 1);
+        int32_t buf = 0;
+        for (int32_t s = 2; s <= n; s <<= 1) {
+            for (int32_t j = s >> 1; j > 0; j >>= 1) {
+                uint64_t other;
+                if (j >= kWave) {
+                    sm.u2.k[buf][p] = key;
+                    __syncthreads();
+                    other = sm.u2.k[buf][p ^ j];
+                    buf ^= 1;
+                } else {
+                    other = shfl_xor64(key, j);
+                }
+                const bool take_max = ((i & j) == 0) == ((i & s) == 0);
+                key = take_max ? (key > other ? key : other) : (key < other ? key : other);
+            }
+        }
+        return key;
+    };
+
+    if (p < 2 * kSlots) (&sm.amin[0][0])[p] = ~0ull;
+    if (p == 0) stage_put(sm.u2.st0[0]);
+    __syncthreads();
 
 #pragma unroll 1
     for (int level = 0; level < kLevels; ++level) {
         const int32_t n = kTokens >> level;
-        const int32_t g = p / n, gs = g * n;
-        if (p == gs) {
-            put_anchor(g);  // mode 0: the group's first member
-            sm.amin[0][g] = ~0ull;
-            sm.amin[1][g] = ~0ull;
+        const int32_t width = n < kWave ? n : kWave;
+        const int32_t slot = wslot(p, width);
+        expand(sm.u2.st0[n > kWave ? p / n : slot], slot, width);  // the group's first member
+        wave_sync();
+        const float s0 = dot(slot);
+        const int32_t bpos = argmin(s0, n, width, 0);
+        expand(sm.u1.d.st[0][wslot(bpos, width)], slot, width);
+        wave_sync();
+        const float sb = dot(slot);
+        const int32_t apos = argmin(sb, n, width, 1);
+        expand(sm.u1.d.st[1][wslot(apos, width)], slot, width);
+        wave_sync();
+        const float score = (dot(slot) - sb);
+        const uint64_t key = sort_desc(((uint64_t)score_key(score) << 32) | (0xffffffffu - (uint32_t)p), n);
+        const int32_t from = (int32_t)(0xffffffffu - (uint32_t)key);  // old position of the new member
+        const int32_t half = n >> 1;
+        if (n > kWave) {
+            // every wave is past its last dot (the sort crossed a barrier):
+            // the exchange area may overwrite the anchors
+#pragma unroll
+            for (int w = 0; w < kWords / 2; ++w) sm.u1.x.c[w][p] = make_uint2(c[2 * w], c[2 * w + 1]);
+            sm.u1.x.tok[p] = tok;
+            sm.u1.x.f[p] = f;
+            __syncthreads();
+#pragma unroll
+            for (int w = 0; w < kWords / 2; ++w) {
+                const uint2 v = sm.u1.x.c[w][from];
+                c[2 * w] = v.x;
+                c[2 * w + 1] = v.y;
+            }
+            tok = sm.u1.x.tok[from];
+            f = sm.u1.x.f[from];
+            if (p < 2 * kSlots) (&sm.amin[0][0])[p] = ~0ull;
+            if (level + 1 < kLevels && (p & (half - 1)) == 0)
+                stage_put(sm.u2.st0[half > kWave ? p / half : wslot(p, half)]);
+            __syncthreads();
+        } else {
+            const int32_t src = from & (kWave - 1);  // same wave
+#pragma unroll
+            for (int w = 0; w < kWords; ++w) c[w] = (uint32_t)__shfl((int)c[w], src, kWave);
+            tok = __shfl(tok, src, kWave);
+            f = __shfl(f, src, kWave);
+            if (level + 1 < kLevels && (p & (half - 1)) == 0) stage_put(sm.u2.st0[wslot(p, half)]);
+            wave_sync();
         }
-        __syncthreads();
-        const float s0 = dot(g);
-        argmin(s0, n, g, 0);
-        __syncthreads();
-        if (p == (int32_t)(uint32_t)sm.amin[0][g]) put_anchor(g);  // mode 1: b = argmin s0
-        __syncthreads();
-        const float sb = dot(g);
-        argmin(sb, n, g, 1);
-        __syncthreads();
-        if (p == (int32_t)(uint32_t)sm.amin[1][g]) put_anchor(g);  // mode 2: a = argmin sb
-        __syncthreads();
-        const float score = (dot(g) - sb);
-        // stable descending sort of the group: rank = members with a larger
-        // (key, ~position) word
-        const uint64_t key = ((uint64_t)score_key(score) << 32) | (0xffffffffu - (uint32_t)p);
-        sm.rank_key[p] = key;
-        __syncthreads();
-        int32_t rank = 0;
-        const ulonglong2* rk = reinterpret_cast<const ulonglong2*>(&sm.rank_key[gs]);
-        for (int32_t q = 0; q < n / 2; ++q) {
-            const ulonglong2 v = rk[q];
-            rank += (v.x > key) + (v.y > key);
-        }
-        sm.xtok[gs + rank] = tok;
-        sm.xf[gs + rank] = f;
-        __syncthreads();
-        tok = sm.xtok[p];
-        f = sm.xf[p];
-        fetch();
     }
 
     // final order: perm, the assembled pages, member map and centers
+    const int64_t page = page_of(tok);
+    const float s = pool_f[page * kPageWords + kScaleWord + tok % 64];
     perm_out[b * kTokens + p] = tok;
     map_out[b * kTokens + p] = starts[b] + tok;
-    const int32_t page = p / 64, slot = p % 64;
-    uint8_t* tp = tmp_out + (b * 16 + page) * V1_PAGE_BYTES;
-    uint4* row = reinterpret_cast<uint4*>(tp + slot * 128);
+    uint8_t* tp = tmp_out + (b * 16 + p / 64) * V1_PAGE_BYTES;
+    uint4* row = reinterpret_cast<uint4*>(tp + (p % 64) * 128);
 #pragma unroll
     for (int i = 0; i < kWords / 4; ++i) row[i] = make_uint4(c[4 * i], c[4 * i + 1], c[4 * i + 2], c[4 * i + 3]);
-    reinterpret_cast<float*>(tp)[kScaleWord + slot] = s;
-    // center p / 8: lane r of the 8 members computes dims 16r .. 16r+15 from
-    // the members' key words 4r .. 4r+3 (lanes 8k .. 8k+7 of the wave)
-    const int32_t r = p & 7, base = __lane_id() & ~7;
+    reinterpret_cast<float*>(tp)[kScaleWord + p % 64] = s;
+    __syncthreads();  // every wave is past its last dot
+#pragma unroll
+    for (int w = 0; w < kWords / 2; ++w) sm.u1.x.c[w][p] = make_uint2(c[2 * w], c[2 * w + 1]);
+    sm.u1.x.f[p] = s;
+    wave_sync();  // a center's 8 members are rows of this wave
+    // center p / 8: lane r of the 8 members computes dims 16r .. 16r+15
+    const int32_t r = p & 7, m0 = p & ~7;
     float mean[16];
-#pragma unroll 1
+#pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int src = base + j;
-        const float sj = __shfl(s, src, kWave);
-        uint32_t words[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            // member j's word 4r+q: the word index depends on the reading
-            // lane, so all eight candidates are shuffled and r picks one
-            uint32_t w = 0;
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const uint32_t cand = (uint32_t)__shfl((int)c[4 * rr + q], src, kWave);
-                w = r == rr ? cand : w;
-            }
-            words[q] = w;
-        }
+        const uint2 w01 = sm.u1.x.c[2 * r][m0 + j], w23 = sm.u1.x.c[2 * r + 1][m0 + j];
+        const float sj = sm.u1.x.f[m0 + j];
+        const uint32_t words[4] = {w01.x, w01.y, w23.x, w23.y};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float x0 = (fp8_at<0>(words[q]) * sj), x1 = (fp8_at<1>(words[q]) * sj);
