@@ -245,6 +245,51 @@ __device__ __forceinline__ float2 fp8_pair(uint32_t w) {
     return make_float2(v[0], v[1]);
 }
 
+// Lane p ^ J's value (J < 64, every lane active): DPP quad permutes and a
+// row rotate for 1, 2 and 8, swizzle bit masks for 4 and 16, a permute for 32.
+template <int J>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    if constexpr (J == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (J == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (J == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);
+    else if constexpr (J == 4 || J == 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (J << 10) | 0x1F);
+    else return (uint32_t)__shfl_xor((int)v, J, kWave);
+}
+
+// One compare-exchange step of a descending bitonic network over groups of
+// N (i = position in the group, partner i ^ J, merge size S).
+template <int N, int S, int J>
+__device__ __forceinline__ uint64_t bitonic_step(uint64_t key, int32_t p, uint64_t (*buf)[kTokens], int32_t& nb) {
+    uint64_t other;
+    if constexpr (J >= kWave) {
+        buf[nb][p] = key;
+        __syncthreads();
+        other = buf[nb][p ^ J];
+        nb ^= 1;
+    } else {
+        other = ((uint64_t)lane_xor<J>((uint32_t)(key >> 32)) << 32) | lane_xor<J>((uint32_t)key);
+    }
+    const int32_t i = p & (N - 1);
+    const bool take_max = ((i & J) == 0) == ((i & S) == 0);
+    return take_max ? (key > other ? key : other) : (key < other ? key : other);
+}
+
+template <int N, int S, int J>
+__device__ __forceinline__ uint64_t bitonic_merge(uint64_t key, int32_t p, uint64_t (*buf)[kTokens], int32_t& nb) {
+    key = bitonic_step<N, S, J>(key, p, buf, nb);
+    if constexpr (J > 1) key = bitonic_merge<N, S, J / 2>(key, p, buf, nb);
+    return key;
+}
+
+// Descending sort of every aligned group of N keys (unique); strides of a
+// wave or more exchange through buf (double-buffered, barriers between).
+template <int N, int S = 2>
+__device__ __forceinline__ uint64_t bitonic_sort(uint64_t key, int32_t p, uint64_t (*buf)[kTokens], int32_t& nb) {
+    key = bitonic_merge<N, S, S / 2>(key, p, buf, nb);
+    if constexpr (S < N) key = bitonic_sort<N, S * 2>(key, p, buf, nb);
+    return key;
+}
+
 // One 1024-thread work-group per bucket; thread = position in the bucket's
 // current order.  Per level (groups of n): three dots against the group's
 // anchors (first member, b = argmin s0, a = argmin sb), score = dot_a - sb,
@@ -338,29 +383,6 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
         }
         return (int32_t)(uint32_t)k;
     };
-    // descending bitonic sort of every group of n (unique keys); strides of
-    // a wave or more go through LDS
-    auto sort_desc = [&](uint64_t key, int32_t n) __attribute__((always_inline)) {
-        const int32_t i = p & (n - 1);
-        int32_t buf = 0;
-        for (int32_t s = 2; s <= n; s <<= 1) {
-            for (int32_t j = s >> 1; j > 0; j >>= 1) {
-                uint64_t other;
-                if (j >= kWave) {
-                    sm.u2.k[buf][p] = key;
-                    __syncthreads();
-                    other = sm.u2.k[buf][p ^ j];
-                    buf ^= 1;
-                } else {
-                    other = shfl_xor64(key, j);
-                }
-                const bool take_max = ((i & j) == 0) == ((i & s) == 0);
-                key = take_max ? (key > other ? key : other) : (key < other ? key : other);
-            }
-        }
-        return key;
-    };
-
     if (p < 2 * kSlots) (&sm.amin[0][0])[p] = ~0ull;
     if (p == 0) stage_put(sm.u2.st0[0]);
     __syncthreads();
@@ -381,7 +403,20 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
         expand(sm.u1.d.st[1][wslot(apos, width)], slot, width);
         wave_sync();
         const float score = (dot(slot) - sb);
-        const uint64_t key = sort_desc(((uint64_t)score_key(score) << 32) | (0xffffffffu - (uint32_t)p), n);
+        uint64_t key = ((uint64_t)score_key(score) << 32) | (0xffffffffu - (uint32_t)p);
+        {
+            auto* kb = reinterpret_cast<uint64_t (*)[kTokens]>(sm.u2.k);
+            int32_t nb = 0;
+            switch (level) {
+                case 0: key = bitonic_sort<1024>(key, p, kb, nb); break;
+                case 1: key = bitonic_sort<512>(key, p, kb, nb); break;
+                case 2: key = bitonic_sort<256>(key, p, kb, nb); break;
+                case 3: key = bitonic_sort<128>(key, p, kb, nb); break;
+                case 4: key = bitonic_sort<64>(key, p, kb, nb); break;
+                case 5: key = bitonic_sort<32>(key, p, kb, nb); break;
+                default: key = bitonic_sort<16>(key, p, kb, nb); break;
+            }
+        }
         const int32_t from = (int32_t)(0xffffffffu - (uint32_t)key);  // old position of the new member
         const int32_t half = n >> 1;
         if (n > kWave) {
