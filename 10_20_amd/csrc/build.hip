@@ -256,6 +256,11 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
     else return (uint32_t)__shfl_xor((int)v, J, kWave);
 }
 
+template <int J>
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
+    return ((uint64_t)lane_xor<J>((uint32_t)(v >> 32)) << 32) | lane_xor<J>((uint32_t)v);
+}
+
 // One compare-exchange step of a descending bitonic network over groups of
 // N (i = position in the group, partner i ^ J, merge size S).
 template <int N, int S, int J>
@@ -267,7 +272,7 @@ __device__ __forceinline__ uint64_t bitonic_step(uint64_t key, int32_t p, uint64
         other = buf[nb][p ^ J];
         nb ^= 1;
     } else {
-        other = ((uint64_t)lane_xor<J>((uint32_t)(key >> 32)) << 32) | lane_xor<J>((uint32_t)key);
+        other = lane_xor64<J>(key);
     }
     const int32_t i = p & (N - 1);
     const bool take_max = ((i & J) == 0) == ((i & S) == 0);
@@ -372,7 +377,12 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
     // key in st[m][its slot]; returns the winner's position
     auto argmin = [&](float v, int32_t n, int32_t width, int32_t m) __attribute__((always_inline)) {
         uint64_t k = ((uint64_t)score_key(v) << 32) | (uint32_t)p;
-        for (int off = 1; off < width; off <<= 1) k = umin64(k, shfl_xor64(k, off));
+        k = umin64(k, lane_xor64<1>(k));  // width >= 16
+        k = umin64(k, lane_xor64<2>(k));
+        k = umin64(k, lane_xor64<4>(k));
+        k = umin64(k, lane_xor64<8>(k));
+        if (width > 16) k = umin64(k, lane_xor64<16>(k));
+        if (width > 32) k = umin64(k, lane_xor64<32>(k));
         if ((uint32_t)k == (uint32_t)p) stage_put(sm.u1.d.st[m][wslot(p, width)]);
         if (n > kWave) {
             if ((p & (kWave - 1)) == 0) atomicMin(&sm.amin[m][p / n], (unsigned long long)k);
