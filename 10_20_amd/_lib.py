@@ -106,6 +106,7 @@ _SIGNATURES = {
     "v1_output_ids": (_c_i32, [_vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i32,
                                _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                _vp]),
+    "v1_expand_logical": (_c_i32, [_vp, _vp, _c_i32, _c_i32, _c_i64, _c_i32, _vp]),
 }
 
 _lock = threading.Lock()

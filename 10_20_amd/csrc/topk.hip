@@ -1140,6 +1140,32 @@ int launch_topk(void (*single)(P), void (*seg)(P, Workspace), void (*merge)(P, W
     return V1_LAUNCHED(name);
 }
 
+// kernels.py:594-600 (expand_logical): out[row, j] = 4 * logical[row, j / 4]
+// + j % 4 for j < 4 * topk with a valid (>= 0) index, else -1, for j < cols;
+// rows of out are `stride` ints apart.  One thread per 4 output ints;
+// int32 arithmetic wraps as the reference's does.
+__global__ __launch_bounds__(256) void expand_logical_kernel(const int32_t* __restrict__ logical,
+                                                             int32_t* __restrict__ out, int32_t topk,
+                                                             int64_t stride, int32_t cols, int32_t vec) {
+    const int64_t row = blockIdx.y;
+    const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (4 * (int64_t)i >= cols) return;
+    const int32_t v = i < topk ? logical[row * topk + i] : -1;
+    const uint32_t base = (uint32_t)v * 4u;
+    const int4 r = v >= 0 ? make_int4((int32_t)base, (int32_t)(base + 1), (int32_t)(base + 2), (int32_t)(base + 3))
+                          : make_int4(-1, -1, -1, -1);
+    int32_t* dst = out + row * stride + 4 * (int64_t)i;
+    if (vec) {
+        *reinterpret_cast<int4*>(dst) = r;
+    } else {
+        const int32_t n = cols - 4 * i < 4 ? cols - 4 * i : 4;
+        dst[0] = r.x;
+        if (n > 1) dst[1] = r.y;
+        if (n > 2) dst[2] = r.z;
+        if (n > 3) dst[3] = r.w;
+    }
+}
+
 }  // namespace
 }  // namespace v1
 
@@ -1207,4 +1233,14 @@ extern "C" int v1_output_ids(const int32_t* raw, const float* scores, int64_t sc
                        raw, scores, score_stride, members, rt, nt, selected, selected_bits == 64, lens, takes, out,
                        logical, ft, maxp, np, take_stride, width, topk, sink, window, map_physical, direct_fine, fp);
     return V1_LAUNCHED("output_ids");
+}
+
+extern "C" int v1_expand_logical(const int32_t* logical, int32_t* out, int32_t rows, int32_t topk, int64_t stride,
+                                 int32_t cols, void* stream) {
+    V1_REQUIRE(rows >= 0 && topk >= 0 && cols >= 0 && stride >= cols, "expand_logical: bad shape");
+    if (rows == 0 || cols == 0) return V1_OK;
+    const int32_t vec = (cols % 4 == 0 && stride % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(expand_logical_kernel, dim3((uint32_t)cdiv(cdiv(cols, 4), 256), rows), dim3(256), 0,
+                       as_stream(stream), logical, out, topk, stride, cols, vec);
+    return V1_LAUNCHED("expand_logical");
 }

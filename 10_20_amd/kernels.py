@@ -196,5 +196,19 @@ def _output_ids(grid, RAW, SCORES, MEMBERS, RT, NT, SELECTED, LENS, TAKES, OUT, 
               int(SINK), int(WINDOW), int(bool(MAP_PHYSICAL)), int(bool(DIRECT_FINE)), int(FP), _stream(SCORES))
 
 
+def _expand_logical(grid, LOGICAL, OUT, TOPK, STRIDE, BLOCK):
+    """kernels.py:594-600: program r writes columns j < min(STRIDE, BLOCK) of
+    OUT row r (rows STRIDE ints apart) from LOGICAL row r (TOPK ints)."""
+    _lib.require_gpu(LOGICAL, OUT)
+    if LOGICAL.dtype != torch.int32 or OUT.dtype != torch.int32:
+        raise ValueError("expand_logical: LOGICAL and OUT must be int32")
+    rows, topk, stride = grid[0], int(TOPK), int(STRIDE)
+    if rows > 0 and (LOGICAL.numel() < rows * topk or OUT.numel() < (rows - 1) * stride + min(stride, int(BLOCK))):
+        raise ValueError("expand_logical: tensors smaller than the grid addresses")
+    _lib.call("v1_expand_logical", _lib.ptr(LOGICAL), _lib.ptr(OUT), rows, topk, stride, min(stride, int(BLOCK)),
+              _stream(OUT))
+
+
 mask_fine = _Kernel("mask_fine", _mask_fine)
 output_ids = _Kernel("output_ids", _output_ids)
+expand_logical = _Kernel("expand_logical", _expand_logical)

@@ -9,7 +9,8 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
                slot mapping -> 656-byte latent-row gather into a reused workspace
   1            the reference example shape: 1024 queries x 1 head; coarse score over
                centers -> route (40 of 64 pages, fine table) -> shared tail staging ->
-               fine score over 2688 candidates -> fused Top-2048 with mask -> gather
+               fine score over 2688 candidates -> fused Top-2048 with mask -> C4 x4
+               expansion (the unfused fallback) -> gather
   2            page management: 4096 requests (~132 K Zipf page keys) -> stable key grouping,
                match -> allocate -> publish into a 65536-page pool of 41984-byte pages,
                128-token tail staging for owner pairs, release of half the requests
@@ -188,6 +189,7 @@ def setup_example(P, dev, torch, np):
     logical = torch.empty_like(physical)
     raw = torch.empty_like(physical)
     no_exp = torch.empty_strided((B, 0), (0, 1), device=dev, dtype=torch.int32)
+    expanded = torch.empty((B, 4 * T + 64), device=dev, dtype=torch.int32)  # C4 indices (x4 per token)
     work = torch.empty((B, T, P.workloads.MLA_ROW_BYTES), device=dev, dtype=torch.uint8)
     fused = P.query_fused.module()
     stages = [
@@ -202,6 +204,8 @@ def setup_example(P, dev, torch, np):
         ("topk", lambda: fused.topk(logits, d["fine_lens"], d["members"], d["rt"], d["nt"], sel, d["lens"],
                                     d["takes"], physical, logical, raw, prm["WINDOW"], True, no_exp, True, True, ft,
                                     False)),
+        ("expand", lambda: P.kernels.expand_logical[(B,)](logical, expanded, T, expanded.shape[1],
+                                                          1 << (expanded.shape[1] - 1).bit_length())),
         ("gather", lambda: P.native_kernels.gather_rows(d["latent"], physical, work)),
     ]
     fl = a["fine_lens"].astype(np.int64)
@@ -212,6 +216,7 @@ def setup_example(P, dev, torch, np):
         "stage": (2.0 * 2 * 8448 / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
         "score": (_score_flops(1, fl) / 1e12, "TFLOP/s", PEAK_FP8_TFLOPS, "mfma"),
         "topk": ((4.0 * fl.sum() + 12.0 * B * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "expand": ((4.0 * B * T + 4.0 * expanded.numel()) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
         "gather": (lambda: _gather_gb(torch, physical, rb, d["latent"].shape[0]), "GB/s", PEAK_HBM_GBS, "hbm"),
     }
 
@@ -221,7 +226,7 @@ def setup_example(P, dev, torch, np):
         return qps, threads, f"{n} of {B} queries (score over the 2688 candidates + top2048 + slot map + gather)"
 
     meta = {"workload": "reference example query chain: 1024 queries x 1 head, route 40 of 64 pages, "
-                        "2688 candidates, fused Top-2048 with mask, 656-byte row gather",
+                        "2688 candidates, fused Top-2048 with mask, unfused C4 x4 expansion, 656-byte row gather",
             "global_batch": B, "seq_len": WIDTH, "parallelism": "single GPU"}
     return B, stages, work_units, cpu, meta, "synthetic (PCG64 seed 19)"
 

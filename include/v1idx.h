@@ -363,6 +363,13 @@ int v1_output_ids(const int32_t* raw, const float* scores, int64_t score_stride,
                   int32_t topk, int32_t sink, int32_t window, int32_t map_physical,
                   int32_t direct_fine, int32_t fp, void* stream);
 
+/* expand_logical, sglang/srt/layers/attention/v1_deepseek/kernels.py:594-600
+ * (the unfused C4 x4 expansion, runtime.py:638-641): out[r, j] = 4*logical[r, j/4]
+ * + j%4 for j < 4*topk and logical >= 0, else -1, for columns j < cols (the
+ * reference's min(STRIDE, BLOCK)); logical is [rows, topk] contiguous, out rows
+ * are `stride` ints apart (stride >= cols). */
+int v1_expand_logical(const int32_t* logical, int32_t* out, int32_t rows, int32_t topk, int64_t stride,
+                      int32_t cols, void* stream);
 #ifdef __cplusplus
 }
 #endif

@@ -168,6 +168,24 @@ def transform_topk(scores, seq_lens, page_table, T, page_bits):
 
 
 # ------------------------------------------------------ unfused mask / map
+def expand_logical(logical, out, block=None):
+    """kernels.py:594-600 (the unfused C4 x4 expansion, runtime.py:638-641), in
+    place on out [rows, stride]: columns j < min(stride, block) become
+    4 * logical[r, j // 4] + j % 4 when j < 4 * topk and that index is >= 0,
+    else -1 (int32, wrapping); columns past block are left as they are."""
+    logical = np.asarray(logical, np.int32)
+    rows, topk = logical.shape
+    stride = out.shape[1]
+    cols = stride if block is None else min(stride, block)
+    j = np.arange(cols)
+    src = np.full((rows, cols), -1, np.int64)
+    inside = j < 4 * topk
+    src[:, inside] = logical[:, j[inside] // 4]
+    val = ((src.astype(np.uint32) * np.uint32(4)) + (j % 4).astype(np.uint32)).view(np.int32)
+    out[:, :cols] = np.where(src >= 0, val, -1)
+    return out
+
+
 def mask_fine(scores, selected, rt, members, lens, takes, width, sink_cap, window):
     """sglang/srt/layers/attention/v1_deepseek/kernels.py:444-472 (in place)."""
     B = scores.shape[0]

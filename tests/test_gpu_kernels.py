@@ -691,3 +691,25 @@ def test_topk_adversarial_rows(dev, kind, cols):
     TK.topk_transform_512_v2(T(scores, dev)[:, :cols], T(lens, dev), T(table, dev), out, 64, None, raw)
     e_out, e_raw = O.transform_topk(scores[:, :cols], lens, table, 2048, 6)
     assert np.array_equal(H(raw), e_raw) and np.array_equal(H(out), e_out)
+
+
+# ------------------------------------------------- unfused C4 x4 expansion
+@pytest.mark.parametrize("rows,topk,stride,block,offset", [
+    (64, 2048, 4 * 2048 + 64, 16384, 0),   # runtime.py:638-641 shape (BLOCK = next power of two)
+    (7, 5, 23, 32, 0),                     # odd stride: scalar stores
+    (5, 6, 40, 16, 0),                     # BLOCK < STRIDE: columns past BLOCK untouched
+    (9, 10, 12, 16, 0),                    # stride < 4 * topk: truncated
+    (33, 300, 4 * 300 + 64, 2048, 1),      # output rows not 16-byte aligned
+])
+def test_expand_logical_vs_oracle(dev, rows, topk, stride, block, offset):
+    g = np.random.default_rng(rows * 1000 + topk)
+    logical = g.integers(0, 1 << 20, (rows, topk)).astype(np.int32)
+    logical[g.random((rows, topk)) < 0.1] = -1
+    logical[0, :2] = [2 ** 29 + 1, np.iinfo(np.int32).max]  # int32 wrap of 4 * index
+    backing = torch.full((rows * stride + offset,), 7, device=dev, dtype=torch.int32)
+    out = backing[offset:].view(rows, stride)
+    K.expand_logical[(rows,)](T(logical, dev), out, topk, stride, block)
+    exp = np.full((rows, stride), 7, np.int32)
+    O.expand_logical(logical, exp, block)
+    assert np.array_equal(H(out), exp)
+    assert int(backing[:offset].ne(7).sum()) == 0 if offset else True

@@ -552,3 +552,31 @@ def test_stage_tail_rows_equals_native_layout(kats):
         touched = ~(a == 255).all(axis=1)
         assert np.array_equal(touched, ~(b == 255).all(axis=1))
         assert np.array_equal(_as_rows(a[touched]), b[touched])
+
+
+def test_expand_logical_kat_and_fused_equality(example_after_route):
+    # hand-computed: index 3 -> 12..15, -1 -> four -1s, 0 -> 0..3, padding -1
+    out = np.full((1, 16), 7, np.int32)
+    O.expand_logical(np.array([[3, -1, 0]], np.int32), out)
+    assert out.tolist() == [[12, 13, 14, 15, -1, -1, -1, -1, 0, 1, 2, 3, -1, -1, -1, -1]]
+    # BLOCK below STRIDE: columns past BLOCK keep their contents
+    out = np.full((1, 16), 7, np.int32)
+    O.expand_logical(np.array([[3, -1, 0]], np.int32), out, block=8)
+    assert out.tolist() == [[12, 13, 14, 15, -1, -1, -1, -1] + [7] * 8]
+    # int32 wraps like the reference's tl arithmetic
+    out = np.zeros((1, 4), np.int32)
+    O.expand_logical(np.array([[2 ** 29 + 1]], np.int32), out)
+    assert out.tolist() == [[-2 ** 31 + 4, -2 ** 31 + 5, -2 ** 31 + 6, -2 ** 31 + 7]]
+    # the unfused expansion of the fused Top-K's logical ids equals its fused expansion
+    # (v1_query.cuh:143-151 vs kernels.py:594-600), on the reference example
+    d, sel, ft, f = example_after_route
+    rows = 32
+    args = lambda a: a[:rows]
+    work = f["fine_scores"].numpy()[:rows].copy()
+    res = O.fused_topk(work, f["fine_lens"].numpy()[:rows], d["members"].numpy(), args(d["rt"].numpy()),
+                       args(d["nt"].numpy()), args(sel), args(d["lens"].numpy()), args(d["takes"].numpy()), RX.TOP,
+                       RX.WINDOW, True, 4 * RX.TOP + 64, True, True, args(ft), False)
+    assert (res["logical"] >= 0).any() and (res["expanded"][:, 4 * RX.TOP:] == -1).all()
+    out = np.full(res["expanded"].shape, 7, np.int32)
+    O.expand_logical(res["logical"], out)
+    assert np.array_equal(out, res["expanded"])
