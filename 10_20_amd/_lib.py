@@ -107,6 +107,16 @@ _SIGNATURES = {
                                _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                _vp]),
     "v1_expand_logical": (_c_i32, [_vp, _vp, _c_i32, _c_i32, _c_i64, _c_i32, _vp]),
+    "v1_stage_tail_published": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                         _c_i32, _c_i64, _c_i64, _vp]),
+    "v1_stage_union": (_c_i32, [_vp, _c_i64, _vp, _c_i32, _vp, _c_i32, _vp, _vp, _c_i32, _vp, _vp, _c_i32,
+                                _c_i32, _vp]),
+    "v1_union_tables": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32,
+                                 _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
+    "v1_union_normalize": (_c_i32, [_vp, _c_i64, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _c_i32,
+                                    _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
+    "v1_union_map_topk": (_c_i32, [_vp, _c_i32, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _vp, _vp,
+                                   _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
 }
 
 _lock = threading.Lock()

@@ -289,16 +289,21 @@ __global__ void fine_table_kernel(const int32_t* rt, const void* selected, int32
 // kernels.py:518-564 (tail_rows == NULL: every row owns its scratch, :407-441).
 // Block (row, p): copies tail-candidate page p of an owner row, 64 tokens x
 // (128 FP8 bytes + fp32 scale); slots past the candidate count become zero.
+// With indexed_end, the tail starts at the published index end instead of the
+// last whole 1024-token bucket (experiments/tail_union_lab_20261021/
+// baseline_published.py:21-61).
 __global__ __launch_bounds__(256) void stage_tail_kernel(const uint8_t* native, const int32_t* nt, const int32_t* lens,
-                                                         uint8_t* fine, const int32_t* tail_rows, int32_t capacity,
-                                                         int32_t np, int32_t scratch, int32_t sink_cap, int32_t window,
+                                                         const int32_t* indexed_end, uint8_t* fine,
+                                                         const int32_t* tail_rows, int32_t capacity, int32_t np,
+                                                         int32_t scratch, int32_t sink_cap, int32_t window,
                                                          int64_t native_pages, int64_t fine_pages) {
     const int64_t row = blockIdx.x;
     const int32_t p = blockIdx.y;
     if (tail_rows != nullptr && tail_rows[row] != row) return;
     const int32_t n = lens[row];
     const int32_t sink = min(n, sink_cap);
-    const int32_t tail = max(sink, min(max(n - 1, 0) / 1024 * 1024, max(sink, n - window)));
+    const int32_t indexed = indexed_end ? min(max(*indexed_end, 0), n) : max(n - 1, 0) / 1024 * 1024;
+    const int32_t tail = max(sink, min(indexed, max(sink, n - window)));
     const int32_t count = sink + n - tail;
     if (!(p * 64 < count || p == 0)) return;
     const int64_t dst = capacity + row * scratch + p;
@@ -462,9 +467,24 @@ extern "C" int v1_stage_tail(const uint8_t* native, const int32_t* nt, const int
     V1_REQUIRE((reinterpret_cast<uintptr_t>(native) & 15) == 0 && (reinterpret_cast<uintptr_t>(fine) & 15) == 0,
                "stage_tail: pools must be 16-byte aligned");
     if (rows == 0) return V1_OK;
-    hipLaunchKernelGGL(stage_tail_kernel, dim3(rows, scratch), dim3(256), 0, as_stream(stream), native, nt, lens, fine,
-                       tail_rows, capacity, np, scratch, sink, window, native_pages, fine_pages);
+    hipLaunchKernelGGL(stage_tail_kernel, dim3(rows, scratch), dim3(256), 0, as_stream(stream), native, nt, lens,
+                       static_cast<const int32_t*>(nullptr), fine, tail_rows, capacity, np, scratch, sink, window,
+                       native_pages, fine_pages);
     return V1_LAUNCHED("stage_tail");
+}
+
+extern "C" int v1_stage_tail_published(const uint8_t* native, const int32_t* nt, const int32_t* lens,
+                                       const int32_t* indexed_end, uint8_t* fine, const int32_t* tail_rows,
+                                       int32_t rows, int32_t capacity, int32_t np, int32_t scratch, int32_t sink,
+                                       int32_t window, int64_t native_pages, int64_t fine_pages, void* stream) {
+    V1_REQUIRE(rows >= 0 && np > 0 && scratch > 0, "stage_tail_published: bad shape");
+    V1_REQUIRE(indexed_end != nullptr, "stage_tail_published: indexed_end is required");
+    V1_REQUIRE((reinterpret_cast<uintptr_t>(native) & 15) == 0 && (reinterpret_cast<uintptr_t>(fine) & 15) == 0,
+               "stage_tail_published: pools must be 16-byte aligned");
+    if (rows == 0) return V1_OK;
+    hipLaunchKernelGGL(stage_tail_kernel, dim3(rows, scratch), dim3(256), 0, as_stream(stream), native, nt, lens,
+                       indexed_end, fine, tail_rows, capacity, np, scratch, sink, window, native_pages, fine_pages);
+    return V1_LAUNCHED("stage_tail_published");
 }
 
 extern "C" int v1_stage_tail_rows(const uint8_t* native, const int32_t* nt, const int32_t* lens, uint8_t* fine,

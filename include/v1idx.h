@@ -370,6 +370,42 @@ int v1_output_ids(const int32_t* raw, const float* scores, int64_t score_stride,
  * are `stride` ints apart (stride >= cols). */
 int v1_expand_logical(const int32_t* logical, int32_t* out, int32_t rows, int32_t topk, int64_t stride,
                       int32_t cols, void* stream);
+/* ------------------------------------------------------------------------
+ * Shared sink + tail staging with a published index end (one request's causal
+ * chunk, rows with non-decreasing lengths; no host reads, graph-capturable):
+ * stage_tail_published  experiments/tail_union_lab_20261021/baseline_published.py:4-61
+ *                       (stage_tail_shared with the tail starting at indexed_end)
+ * stage_union           experiments/tail_union_lab_20261021/union.py:10-42
+ * union_tables          experiments/fine_pool_shared_20261021/kernels.py:13-35 (tables)
+ * union_normalize       kernels.py:38-59 (normalize)
+ * union_map_topk        kernels.py:62-76 (map_topk)
+ * Row bounds: s = min(n, sink), t = max(s, min(min(max(end, 0), n),
+ * max(s, n - window))), count = s + n - t.  stage_union copies the union of all
+ * rows' sink and tail pages once into dst (pages past its capacity are not
+ * copied), writes meta [rows, 3] = (s, t, count) and desc = (sp, tp, ep, total).
+ * ---------------------------------------------------------------------- */
+int v1_stage_tail_published(const uint8_t* native, const int32_t* nt, const int32_t* lens,
+                            const int32_t* indexed_end, uint8_t* fine, const int32_t* tail_rows,
+                            int32_t rows, int32_t capacity, int32_t np, int32_t scratch, int32_t sink,
+                            int32_t window, int64_t native_pages, int64_t fine_pages, void* stream);
+int v1_stage_union(const void* src, int64_t src_pages, const int32_t* nt, int32_t nt_len,
+                   const int32_t* lens, int32_t rows, const int32_t* indexed_end, void* dst,
+                   int32_t dst_pages, int32_t* meta, int32_t* desc, int32_t sink, int32_t window,
+                   void* stream);
+int v1_union_tables(const int32_t* lens, const int32_t* indexed_end, const int32_t* takes,
+                    const int32_t* selected, const int32_t* desc, int32_t* ft, int32_t* dg_lens,
+                    int32_t* clens, int32_t rows, int32_t cap, int32_t max_take, int32_t scratch,
+                    int32_t fp, int32_t sink, int32_t window, int32_t shared, void* stream);
+int v1_union_normalize(const float* raw, int64_t raw_stride, int32_t raw_cols, const int32_t* lens,
+                       const int32_t* indexed_end, const int32_t* takes, const int32_t* selected,
+                       const int32_t* members, int64_t members_pages, float* out, int32_t rows,
+                       int32_t max_take, int32_t width, int32_t sink, int32_t window, int32_t shared,
+                       void* stream);
+int v1_union_map_topk(const void* ids, int32_t ids_bits, const float* values, const int32_t* lens,
+                      const int32_t* indexed_end, const int32_t* takes, const int32_t* selected,
+                      const int32_t* members, int64_t members_pages, const int32_t* nt, int32_t nt_len,
+                      int32_t* logical, int32_t* slots, int32_t rows, int32_t max_take, int32_t top,
+                      int32_t sink, int32_t window, void* stream);
 #ifdef __cplusplus
 }
 #endif

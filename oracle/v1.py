@@ -274,9 +274,11 @@ def fine_table(rt, selected, takes, fp, capacity, scratch, tail_rows=None):
     return ft
 
 
-def stage_tail(native, nt, lens, fine, capacity, scratch, sink_cap, window, tail_rows=None, rows=None):
+def stage_tail(native, nt, lens, fine, capacity, scratch, sink_cap, window, tail_rows=None, rows=None,
+               indexed_end=None):
     """kernels.py:518-564 (tail_rows None: :407-441) on byte pools [pages, 8448]
-    (in place on fine)."""
+    (in place on fine).  With indexed_end the tail starts at the published index
+    end (experiments/tail_union_lab_20261021/baseline_published.py:38-41)."""
     B = nt.shape[0] if rows is None else rows
     nat_k = native[:, :8192].reshape(-1, 64, 128)
     nat_s = native[:, 8192:].copy().view(np.float32).reshape(-1, 64)
@@ -284,7 +286,10 @@ def stage_tail(native, nt, lens, fine, capacity, scratch, sink_cap, window, tail
         if tail_rows is not None and int(tail_rows[row]) != row:
             continue
         n = int(lens[row])
-        sink, tail = _bounds(n, window, sink_cap)
+        if indexed_end is None:
+            sink, tail = _bounds(n, window, sink_cap)
+        else:
+            sink, tail, _ = union_bounds(n, int(indexed_end), sink_cap, window)
         count = sink + n - tail
         for p in range(scratch):
             if not (p * 64 < count or p == 0):
@@ -709,3 +714,143 @@ def index_build(native, table, start):
     perm, _ = group_bisect(unit, 0)
     tmp, mapping, centers = build_assemble(native, table, perm, start)
     return perm, tmp, mapping, centers
+
+
+# ------------------------------------------------- shared sink + tail union
+def union_bounds(n, end, S, W):
+    """experiments/tail_union_lab_20261021/union.py:10-14: (s, t, count)."""
+    s = min(n, S)
+    t = max(s, min(min(max(end, 0), n), max(s, n - W)))
+    return s, t, s + n - t
+
+
+def union_pages(lens, end, S, W):
+    """union.py:18-24: (sp, tp, ep, total) of the union of every row's pages."""
+    first, last = int(lens[0]), int(lens[-1])
+    sp = (min(last, S) + 63) // 64
+    tp = max(sp, union_bounds(first, end, S, W)[1] // 64)
+    ep = (last + 63) // 64
+    return sp, tp, ep, sp + max(ep - tp, 0)
+
+
+def stage_union(src, nt, lens, end, dst, S, W):
+    """union.py:16-40 on byte pools [pages, 8448]: union page b <- source page
+    nt[b if b < sp else tp + b - sp] for b < min(total, capacity), in place on
+    dst; returns (meta [rows, 3], desc [4])."""
+    sp, tp, ep, total = union_pages(lens, end, S, W)
+    for b in range(min(total, dst.shape[0])):
+        lp = b if b < sp else tp + b - sp
+        dst[b] = src[int(nt[lp])]
+    meta = np.array([union_bounds(int(n), end, S, W) for n in lens], np.int32).reshape(-1, 3)
+    return meta, np.array([sp, tp, ep, total], np.int32)
+
+
+def union_reconstruct(union, meta, desc, scratch):
+    """union.py:26-42 (reconstruct_for_test): each row's candidates read from the
+    union into its own scratch pages (row * scratch + p), the layout the per-row
+    staging writes; pages past the count are not written (None)."""
+    rows = meta.shape[0]
+    uk = union[:, :8192].reshape(-1, 64, 128)
+    us = union[:, 8192:].copy().view(np.float32).reshape(-1, 64)
+    out = {}
+    sp, tp = int(desc[0]), int(desc[1])
+    for r in range(rows):
+        s, t, c = (int(v) for v in meta[r])
+        for p in range(scratch):
+            if not (p * 64 < c or p == 0):
+                continue
+            kb = np.zeros((64, 128), np.uint8)
+            sb = np.zeros(64, np.float32)
+            for o in range(64):
+                i = p * 64 + o
+                if i < c:
+                    lg = i if i < s else t + i - s
+                    lp = lg // 64
+                    up = lp if lp < sp else sp + lp - tp
+                    kb[o] = uk[up, lg % 64]
+                    sb[o] = us[up, lg % 64]
+            out[r * scratch + p] = np.concatenate([kb.reshape(-1), sb.view(np.uint8)])
+    return out
+
+
+def union_tables(lens, end, takes, selected, desc, cap, max_take, scratch, fp, S, W, shared):
+    """experiments/fine_pool_shared_20261021/kernels.py:13-35: (ft [rows, fp],
+    dg_lens [rows], canonical lens [rows])."""
+    rows = len(lens)
+    ft = np.zeros((rows, fp), np.int32)
+    dg = np.zeros(rows, np.int32)
+    cl = np.zeros(rows, np.int32)
+    for r in range(rows):
+        n, take = int(lens[r]), int(takes[r])
+        s, t, c = union_bounds(n, end, S, W)
+        if shared:
+            sp = (s + 63) // 64
+            tp = max(sp, t // 64)
+            ep = (n + 63) // 64
+            gsp, gtp = int(desc[0]), int(desc[1])
+            pages = sp + max(ep - tp, 0)
+            span = sp * 64 + n - tp * 64 if ep > tp else n
+        else:
+            pages, span = (c + 63) // 64, c
+        for j in range(fp):
+            if j < take:
+                ft[r, j] = selected[r, j] if j < max_take else 0
+            else:
+                k = j - take
+                if shared:
+                    page = cap + k if k < sp else cap + gsp + tp - gtp + k - sp
+                else:
+                    page = cap + r * scratch + k
+                ft[r, j] = page if 0 <= k < pages else 0
+        dg[r] = max(take * 64 + span, 1)
+        cl[r] = take * 64 + c
+    return ft, dg, cl
+
+
+def union_normalize(raw, lens, end, takes, selected, members, max_take, width, S, W, shared):
+    """kernels.py:38-59: scores in canonical candidate order (history members,
+    sink, tail), -inf where masked; raw [rows, >= span]."""
+    rows = len(lens)
+    out = np.full((rows, width), NEG_INF, np.float32)
+    for r in range(rows):
+        n, take = int(lens[r]), int(takes[r])
+        s, t, c = union_bounds(n, end, S, W)
+        hist = take * 64
+        sp = (s + 63) // 64
+        tp = max(sp, t // 64)
+        for j in range(width):
+            if j < hist:
+                page = int(selected[r, j // 64])
+                m = int(members[page, j % 64])
+                ok = s <= m < t and m < n and m < end
+                src = j
+            else:
+                x = j - hist
+                ok = x < c
+                lg = x if x < s else t + x - s
+                src = hist + (lg if lg < sp * 64 else sp * 64 + lg - tp * 64) if shared else j
+            if ok:
+                out[r, j] = raw[r, src]
+    return out
+
+
+def union_map_topk(ids, values, lens, end, takes, selected, members, nt, S, W):
+    """kernels.py:62-76: (logical, slots) [rows, top] of Top-K candidate ids."""
+    rows, top = ids.shape
+    logical = np.full((rows, top), -1, np.int32)
+    slots = np.full((rows, top), -1, np.int32)
+    for r in range(rows):
+        n, take = int(lens[r]), int(takes[r])
+        s, t, c = union_bounds(n, end, S, W)
+        for i in range(top):
+            rank = int(ids[r, i])
+            if rank < take * 64:
+                lg = int(members[int(selected[r, rank // 64]), rank % 64])
+            else:
+                x = rank - take * 64
+                lg = x if x < s else t + x - s
+            if values[r, i] != NEG_INF and 0 <= lg < n:
+                logical[r, i] = lg
+                slots[r, i] = int(nt[lg // 64]) * 64 + lg % 64
+    return logical, slots
+
