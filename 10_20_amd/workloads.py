@@ -283,6 +283,38 @@ def config6(seed=6, pool_pages=32768, buckets=2048):
                     dict(buckets=buckets, pool_pages=pool_pages))
 
 
+def config7(seed=7, history=65536, rows=4096, heads=32, sink=64, window=2048, max_take=40):
+    """Shared sink + tail chunk (experiments/fine_pool_shared_20261021/
+    experiment.py:15-46 shape): one request with `history` published tokens,
+    `rows` causal queries (lengths history+1 .. history+rows), `heads` FP8 query
+    heads, sink / window, `max_take` history pages per row (64 reordered pages
+    whose members are distinct logical positions, the first page the sink),
+    indexed_end = history."""
+    g = rng(seed)
+    pages = -(-(history + rows) // PAGE)
+    cap = max(64, max_take)
+    k8, ks = quantize_rows(g.standard_normal((pages * PAGE, DIM), dtype=np.float32))
+    native = pack_pages(k8, ks)
+    nt = g.permutation(pages).astype(np.int32)
+    members = np.concatenate([np.arange(64), 64 + g.permutation(history - 64)[:cap * 64 - 64]]).astype(np.int32)
+    members = members.reshape(cap, 64)
+    nk = native[:, :8192].reshape(-1, PAGE, DIM)
+    ns = native[:, 8192:].copy().view(np.float32).reshape(-1, PAGE)
+    page, off = nt[members // PAGE], members % PAGE
+    reordered = np.zeros((cap, PAGE_BYTES), np.uint8)
+    reordered[:, :8192] = nk[page, off].reshape(cap, 8192)
+    reordered[:, 8192:] = ns[page, off].view(np.uint8).reshape(cap, 256)
+    q8, _ = quantize_rows(g.standard_normal((rows * heads, DIM), dtype=np.float32))
+    w = (g.random((rows, heads), dtype=np.float32) / heads).astype(np.float32)
+    selected = ((np.arange(max_take)[None] + np.arange(rows)[:, None]) % cap).astype(np.int32)
+    return Workload("config7", seed, dict(native=native, nt=nt, members=members, reordered=reordered,
+                                          q8=q8.reshape(rows, heads, DIM), w=w, selected=selected,
+                                          lens=np.arange(history + 1, history + rows + 1, dtype=np.int32),
+                                          takes=np.full(rows, max_take, np.int32)),
+                    dict(history=history, rows=rows, heads=heads, sink=sink, window=window, max_take=max_take,
+                         cap=cap, pages=pages, indexed_end=history, topk=TOPK))
+
+
 def decode_table():
     """float32 value of each of the 256 e4m3fn codes (NaN for 0x7f / 0xff)."""
     vals = np.concatenate([_E4M3_POS, [np.nan]]).astype(np.float32)

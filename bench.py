@@ -20,6 +20,10 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
                their own page tables in a 2M-token pool -> Top-2048 -> gather
   6            index build: every 1024-token bucket of a 2M-token FP8 pool (2048 buckets)
                -> member order, reordered pages and FP8 centers, one launch
+  7            shared sink+tail chunk: 64K published tokens, 4096 causal queries x 32 heads,
+               sink 64 / window 2048, 40 history pages per query: one union of sink+tail
+               pages -> FP8 score -> canonical order -> Top-2048 -> slots (per-row staging
+               of the same candidates timed beside it)
 
 Prints one JSON line: queries/sec, per-stage times, the roofline of the
 dominant kernel and the CPU baseline (the reference's torch expressions on
@@ -84,7 +88,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6])
+    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6, 7])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES bytes (HBM counter calibration) and exit")
@@ -106,7 +110,7 @@ def copy_calibration(nbytes):
 class Pkg:
     def __init__(self):
         for name in ("workloads", "scoring", "topk", "native_kernels", "query_fused", "kernels", "pagepool",
-                     "indexbuild"):
+                     "indexbuild", "tailunion"):
             setattr(self, name, importlib.import_module(f"10_20_amd.{name}"))
 
 
@@ -387,7 +391,100 @@ def setup_build(P, dev, torch, np):
     return B * 1024, stages, work_units, cpu, meta, "synthetic (PCG64 seed 6)"
 
 
-SETUPS = {1: setup_example, 2: setup_pages, 3: setup_gather, 4: setup_prefill, 5: setup_decode, 6: setup_build}
+def setup_union(P, dev, torch, np):
+    """Configuration 7: shared sink + tail chunk with a published index end."""
+    wl = P.workloads.config7()
+    a, prm = wl.arrays, wl.params
+    rows, heads, S, W, end = prm["rows"], prm["heads"], prm["sink"], prm["window"], prm["indexed_end"]
+    cap, mt, T, npg = prm["cap"], prm["max_take"], prm["topk"], prm["pages"]
+    TU = P.tailunion
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in a.items()}
+    q = d["q8"].view(torch.float8_e4m3fn)
+    d_end = torch.tensor([end], device=dev, dtype=torch.int32)
+    last = prm["history"] + rows
+    c_max = min(last, S) + last - max(min(last, S), min(min(end, last), max(min(last, S), last - W)))
+    first = prm["history"] + 1
+    first_tail = max(min(first, S), min(min(end, first), max(min(first, S), first - W)))
+    union_cap = min(npg, -(-S // 64) + -(-last // 64) - first_tail // 64 + 2)
+    scratch = -(-c_max // 64)
+    width = -(-(mt * 64 + c_max + 128) // 256) * 256
+    fine = torch.zeros((cap + union_cap, 8448), device=dev, dtype=torch.uint8)
+    fine[:cap] = d["reordered"]
+    meta_t = torch.empty((rows, 3), device=dev, dtype=torch.int32)
+    desc = torch.zeros(4, device=dev, dtype=torch.int32)
+    table = torch.empty((rows, width // 64), device=dev, dtype=torch.int32)
+    dglens = torch.empty((rows, 1), device=dev, dtype=torch.int32)
+    clens = torch.empty(rows, device=dev, dtype=torch.int32)
+    raw = torch.empty((rows, width), device=dev)
+    scores = torch.empty((rows, width), device=dev)
+    ids = torch.empty((rows, T), device=dev, dtype=torch.int32)
+    ids_pages = torch.empty_like(ids)
+    identity = torch.arange(width // 64, device=dev, dtype=torch.int32)[None].expand(rows, -1).contiguous()
+    values = torch.empty((rows, T), device=dev)
+    logical = torch.empty_like(ids)
+    slots = torch.empty_like(ids)
+    plan = TU.PreparedStage(d["native"], d["nt"], d["lens"], d_end, fine[cap:], meta_t, desc, S, W)
+    fine4 = fine.view(-1, 64, 1, 132)
+
+    def prepare():
+        plan()
+        TU.tables[(rows,)](d["lens"], d_end, d["takes"], d["selected"], desc, table, dglens, clens, cap, mt, scratch,
+                           width // 64, S, W, 256, True)
+
+    def select():
+        P.topk.topk_transform_512_v2(scores, clens, identity, ids_pages, 64, None, ids)
+        torch.gather(scores, 1, ids.clamp_min(0).long(), out=values)
+        TU.map_topk[(rows,)](ids, values, d["lens"], d_end, d["takes"], d["selected"], d["members"], d["nt"],
+                             logical, slots, mt, T, S, W, T)
+
+    stages = [
+        ("prepare", prepare),
+        ("score", lambda: P.scoring.fp8_paged_mqa_logits(q, fine4, d["w"], dglens, table, None, width,
+                                                          clean_logits=False, out=raw)),
+        ("normalize", lambda: TU.normalize[(rows, width // 256)](raw, d["lens"], d_end, d["takes"], d["selected"],
+                                                                 d["members"], scores, mt, width, raw.stride(0), S, W,
+                                                                 256, True)),
+        ("select", select),
+    ]
+    # per-row staging with the same candidates (baseline_published.py), timed beside the chain
+    per_row = torch.empty((cap + rows * scratch, 8448), device=dev, dtype=torch.uint8)
+    per_row[:cap] = d["reordered"]
+    nts = d["nt"][None].expand(rows, -1).contiguous()
+    owners = torch.arange(rows, device=dev, dtype=torch.int32)
+    table_r = torch.empty_like(table)
+
+    def prepare_per_row():
+        TU.stage_tail_shared[(rows, scratch)](d["native"], d["native"].view(torch.float32), nts, d["lens"], d_end,
+                                              per_row, per_row.view(torch.float32), owners, cap, npg, scratch, S, W,
+                                              rows, 1)
+        TU.tables[(rows,)](d["lens"], d_end, d["takes"], d["selected"], desc, table_r, dglens, clens, cap, mt,
+                           scratch, width // 64, S, W, 256, False)
+
+    work_units = {
+        # union pages read and written once (97 here), meta and tables
+        "prepare": (lambda: (2.0 * 8448 * int(desc[3]) + 12.0 * rows + 4.0 * rows * (width // 64 + 2)) / 1e9,
+                    "GB/s", PEAK_HBM_GBS, "hbm"),
+        "score": (lambda: 2.0 * heads * 128 * float(dglens.sum()) / 1e12, "TFLOP/s", PEAK_FP8_TFLOPS, "mfma"),
+        "normalize": ((4.0 * rows * width * 2) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "select": (lambda: (4.0 * float(clens.sum()) + 4.0 * rows * T * 6) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+    }
+
+    def cpu(budget):
+        from oracle import cpu_baseline
+        qps, n, threads = cpu_baseline.union_queries_per_second(a, prm, budget)
+        return qps, threads, f"{n} of {rows} queries (candidates, score, Top-2048, slot map)"
+
+    meta = {"workload": f"shared sink+tail chunk: {prm['history']} published tokens, {rows} causal queries x "
+                        f"{heads} FP8 heads, sink {S} / window {W}, {mt} history pages per query, one union of "
+                        f"sink+tail pages in the fine pool -> FP8 score -> canonical order -> Top-{T} -> slots",
+            "global_batch": rows, "seq_len": width, "parallelism": "single GPU",
+            "_extra": [("prepare_per_row", prepare_per_row,
+                        (lambda: (8448.0 * 2 * rows * scratch) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"))]}
+    return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 7)"
+
+
+SETUPS = {1: setup_example, 2: setup_pages, 3: setup_gather, 4: setup_prefill, 5: setup_decode, 6: setup_build,
+          7: setup_union}
 RATE_UNITS = {2: "requests/s", 6: "tokens/s"}
 METRICS = {6: "index-build tokens/sec (initialize+bisection+assemble) and % of HBM roofline"}
 
@@ -408,6 +505,7 @@ def main():
     torch.cuda.set_device(dev)
     P = Pkg()
     rows, stages, work_units, cpu_fn, meta, data = SETUPS[args.config](P, dev, torch, np)
+    extra = meta.pop("_extra", [])
     names = [n for n, _ in stages]
     ev = {n: [] for n in names}
 
@@ -434,6 +532,22 @@ def main():
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
     stage_ms = {n: sum(x.elapsed_time(y) for x, y in ev[n]) / args.steps for n in names}
+
+    # alternatives timed beside the chain (not part of a step)
+    alternatives = {}
+    for name, fn, unit in extra:
+        for _ in range(args.warmup):
+            fn()
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record()
+        for _ in range(args.steps):
+            fn()
+        a1.record()
+        a1.synchronize()
+        ms = a0.elapsed_time(a1) / args.steps
+        amount = unit[0]() if callable(unit[0]) else unit[0]
+        alternatives[name] = {"ms": round(ms, 4), "achieved": round(amount / (ms / 1e3), 1), "unit": unit[1],
+                              "bound": unit[3], "frac": round(amount / (ms / 1e3) / unit[2], 4)}
 
     stage_info = {}
     work_units = {n: ((u[0]() if callable(u[0]) else u[0]),) + tuple(u[1:]) for n, u in work_units.items()}
@@ -466,6 +580,8 @@ def main():
                      "traffic": measured_traffic(args.config, dom)},
         "cpu_baseline": cpu,
     }
+    if alternatives:
+        line["alternatives"] = alternatives
     print(json.dumps(line), flush=True)
 
 

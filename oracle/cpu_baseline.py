@@ -187,3 +187,41 @@ def build_tokens_per_second(native, tables, starts, budget_s=10.0, min_buckets=2
         O.index_build(native, tables[done], int(starts[done]))
         done += 1
     return 1024.0 * done / (time.perf_counter() - t0), done, 1
+
+
+def union_queries_per_second(a, prm, budget_s=10.0, min_rows=4):
+    """Whole queries of the shared sink + tail chunk on the host, row after row:
+    the row's candidates (its history pages' members masked to [s, t), < n and
+    < the published end; sink; tail from the published end), scored with the
+    reference's torch expression (experiments/fine_pool_shared_20261021/
+    test_and_bench.py:25-38), Top-2048 and the slot map (kernels.py:62-76).
+    Returns (q/s, rows, threads)."""
+    from . import v1 as O
+    threads = torch.get_num_threads()
+    nk = torch.from_numpy(a["native"][:, :8192].reshape(-1, 64, 128)).view(torch.float8_e4m3fn)
+    ns = torch.from_numpy(a["native"][:, 8192:].copy().view(np.float32).reshape(-1, 64))
+    nt = torch.from_numpy(a["nt"].astype(np.int64))
+    members = a["members"]
+    S, W, end, T = prm["sink"], prm["window"], prm["indexed_end"], prm["topk"]
+    rows = len(a["lens"])
+    order = np.random.default_rng(0).permutation(rows)
+    done, t0 = 0, time.perf_counter()
+    while done < rows and (done < min_rows or time.perf_counter() - t0 < budget_s):
+        r = int(order[done])
+        n, take = int(a["lens"][r]), int(a["takes"][r])
+        s, t, c = O.union_bounds(n, end, S, W)
+        hist = members[a["selected"][r, :take]].reshape(-1)
+        keep = torch.from_numpy((hist >= s) & (hist < t) & (hist < n) & (hist < end))
+        ids = torch.from_numpy(np.concatenate([hist, np.arange(s), np.arange(t, n)]).astype(np.int64))
+        k = nk[nt[ids // 64], ids % 64].float()
+        sc = ns[nt[ids // 64], ids % 64]
+        q = torch.from_numpy(a["q8"][r]).view(torch.float8_e4m3fn).float()
+        score = (torch.relu(q @ k.T) * torch.from_numpy(a["w"][r])[:, None]).sum(0) * sc
+        score[:take * 64].masked_fill_(~keep, -float("inf"))
+        vals, top = score.topk(min(T, score.numel()))
+        logical = ids[top]
+        valid = (vals != -float("inf")) & (logical < n)
+        slots = torch.where(valid, nt[logical // 64] * 64 + logical % 64, -1)
+        del slots
+        done += 1
+    return done / (time.perf_counter() - t0), done, threads
