@@ -115,7 +115,8 @@ _SIGNATURES = {
                                  _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
     "v1_union_normalize": (_c_i32, [_vp, _c_i64, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _c_i32,
                                     _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
-    "v1_union_map_topk": (_c_i32, [_vp, _c_i32, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _vp, _vp,
+    "v1_union_map_topk": (_c_i32, [_vp, _c_i32, _vp, _vp, _c_i64, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp,
+                                   _c_i32, _vp, _vp,
                                    _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
 }
 

@@ -144,6 +144,8 @@ __global__ __launch_bounds__(256) void union_tables_kernel(const int32_t* __rest
 // kernels.py:38-59: canonical candidate j of row r (history member, sink,
 // tail) <- its raw score (shared: the tail's place in the union's span),
 // -inf where the member is outside [s, t) or past n / end, or j >= count.
+// Four consecutive candidates per thread (one 16-byte store when the row
+// allows it).
 __global__ __launch_bounds__(256) void union_normalize_kernel(const float* __restrict__ raw, int64_t raw_stride,
                                                               int32_t raw_cols, const int32_t* __restrict__ lens,
                                                               const int32_t* __restrict__ indexed_end,
@@ -152,41 +154,55 @@ __global__ __launch_bounds__(256) void union_normalize_kernel(const float* __res
                                                               const int32_t* __restrict__ members,
                                                               int64_t members_pages, float* __restrict__ out,
                                                               int32_t max_take, int32_t width, int32_t S, int32_t W,
-                                                              int32_t shared) {
+                                                              int32_t shared, int32_t vec) {
     const int64_t r = blockIdx.y;
-    const int32_t j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= width) return;
+    const int32_t j0 = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (j0 >= width) return;
     const int32_t n = lens[r], end = *indexed_end, take = takes[r];
     const UnionBounds x = union_bounds(n, end, S, W);
     const int32_t hist = take * 64;
-    bool valid;
-    int32_t source;
-    if (j < hist) {
-        const int32_t pi = j / 64;
-        const int64_t page = pi < max_take ? selected[r * max_take + pi] : -1;
-        const int32_t member = (page >= 0 && page < members_pages) ? members[page * 64 + j % 64] : -1;
-        valid = member >= x.s && member < x.t && member < n && member < end;
-        source = j;
-    } else {
-        const int32_t k = j - hist;
-        valid = k < x.c;
-        source = j;
-        if (shared) {
-            const int32_t logical = k < x.s ? k : x.t + k - x.s;
-            const int32_t sp = (x.s + 63) / 64, tp = max(sp, x.t / 64);
-            source = hist + (logical < sp * 64 ? logical : sp * 64 + logical - tp * 64);
+    const int32_t sp = (x.s + 63) / 64, tp = max(sp, x.t / 64);
+    const float* row = raw + r * raw_stride;
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int32_t j = j0 + q;
+        bool valid;
+        int32_t source = j;
+        if (j < hist) {
+            const int32_t pi = j / 64;
+            const int64_t page = pi < max_take ? selected[r * max_take + pi] : -1;
+            const int32_t member = (page >= 0 && page < members_pages) ? members[page * 64 + j % 64] : -1;
+            valid = member >= x.s && member < x.t && member < n && member < end;
+        } else {
+            const int32_t k = j - hist;
+            valid = k < x.c;
+            if (shared) {
+                const int32_t logical = k < x.s ? k : x.t + k - x.s;
+                source = hist + (logical < sp * 64 ? logical : sp * 64 + logical - tp * 64);
+            }
         }
+        v[q] = (valid && j < width && source >= 0 && source < raw_cols) ? row[source] : -__builtin_inff();
     }
-    float v = -__builtin_inff();
-    if (valid && source >= 0 && source < raw_cols) v = raw[r * raw_stride + source];
-    out[r * width + j] = v;
+    float* dst = out + r * width + j0;
+    if (vec) {
+        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (j0 + q < width) dst[q] = v[q];
+    }
 }
 
 // kernels.py:62-76: Top-K candidate ids -> logical token (history member,
 // sink or tail position) -> physical slot nt[logical / 64] * 64 + logical % 64;
-// -1 for -inf values and positions outside [0, n).
+// -1 for -inf values and positions outside [0, n).  Without `values`, the
+// value of id i is read from the canonical scores (scores[r, i], -inf past
+// score_cols), which is what the Top-K selected it from.
 __global__ __launch_bounds__(256) void union_map_topk_kernel(const void* __restrict__ ids, int32_t ids64,
                                                              const float* __restrict__ values,
+                                                             const float* __restrict__ scores, int64_t score_stride,
+                                                             int32_t score_cols,
                                                              const int32_t* __restrict__ lens,
                                                              const int32_t* __restrict__ indexed_end,
                                                              const int32_t* __restrict__ takes,
@@ -201,7 +217,8 @@ __global__ __launch_bounds__(256) void union_map_topk_kernel(const void* __restr
     if (i >= top) return;
     const int64_t at = r * top + i;
     const int32_t rank = ids64 ? (int32_t)static_cast<const int64_t*>(ids)[at] : static_cast<const int32_t*>(ids)[at];
-    const float value = values[at];
+    const float value = values ? values[at]
+                               : (rank >= 0 && rank < score_cols ? scores[r * score_stride + rank] : -__builtin_inff());
     const int32_t take = takes[r], n = lens[r];
     const UnionBounds x = union_bounds(n, *indexed_end, S, W);
     int32_t logical;
@@ -261,22 +278,26 @@ extern "C" int v1_union_normalize(const float* raw, int64_t raw_stride, int32_t 
                                   void* stream) {
     V1_REQUIRE(rows >= 0 && width >= 0 && raw_cols >= 0 && max_take >= 0, "normalize: bad shape");
     if (rows == 0 || width == 0) return V1_OK;
-    hipLaunchKernelGGL(union_normalize_kernel, dim3((uint32_t)cdiv(width, 256), (uint32_t)rows), dim3(256), 0,
-                       as_stream(stream), raw, raw_stride, raw_cols, lens, indexed_end, takes, selected, members,
-                       members_pages, out, max_take, width, sink, window, shared);
+    const int32_t vec = (width % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(union_normalize_kernel, dim3((uint32_t)cdiv(cdiv(width, 4), 256), (uint32_t)rows), dim3(256),
+                       0, as_stream(stream), raw, raw_stride, raw_cols, lens, indexed_end, takes, selected, members,
+                       members_pages, out, max_take, width, sink, window, shared, vec);
     return V1_LAUNCHED("normalize");
 }
 
-extern "C" int v1_union_map_topk(const void* ids, int32_t ids_bits, const float* values, const int32_t* lens,
+extern "C" int v1_union_map_topk(const void* ids, int32_t ids_bits, const float* values, const float* scores,
+                                 int64_t score_stride, int32_t score_cols, const int32_t* lens,
                                  const int32_t* indexed_end, const int32_t* takes, const int32_t* selected,
                                  const int32_t* members, int64_t members_pages, const int32_t* nt, int32_t nt_len,
                                  int32_t* logical, int32_t* slots, int32_t rows, int32_t max_take, int32_t top,
                                  int32_t sink, int32_t window, void* stream) {
     V1_REQUIRE(rows >= 0 && top >= 0 && max_take >= 0 && nt_len >= 0, "map_topk: bad shape");
     V1_REQUIRE(ids_bits == 32 || ids_bits == 64, "map_topk: ids must be int32 or int64");
+    V1_REQUIRE(values || scores, "map_topk: values or canonical scores are required");
     if (rows == 0 || top == 0) return V1_OK;
     hipLaunchKernelGGL(union_map_topk_kernel, dim3((uint32_t)cdiv(top, 256), (uint32_t)rows), dim3(256), 0,
-                       as_stream(stream), ids, ids_bits == 64 ? 1 : 0, values, lens, indexed_end, takes, selected,
+                       as_stream(stream), ids, ids_bits == 64 ? 1 : 0, values, scores, score_stride, score_cols,
+                       lens, indexed_end, takes, selected,
                        members, members_pages, nt, nt_len, logical, slots, max_take, top, sink, window);
     return V1_LAUNCHED("map_topk");
 }

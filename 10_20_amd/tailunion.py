@@ -132,10 +132,29 @@ def _map_topk(grid, IDS, VALUES, LENS, END, TAKES, SELECTED, MEMBERS, NT, LOGICA
     rows, top = grid[0], int(TOP)
     if rows > 0 and min(IDS.numel(), VALUES.numel(), LOGICAL.numel(), SLOTS.numel()) < rows * top:
         raise ValueError("map_topk: tensors smaller than rows x TOP")
-    _lib.call("v1_union_map_topk", _lib.ptr(IDS), 64 if IDS.dtype == torch.int64 else 32, _lib.ptr(VALUES),
-              _lib.ptr(LENS), _lib.ptr(END), _lib.ptr(TAKES), _lib.ptr(SELECTED), _lib.ptr(MEMBERS),
+    _lib.call("v1_union_map_topk", _lib.ptr(IDS), 64 if IDS.dtype == torch.int64 else 32, _lib.ptr(VALUES), 0, 0,
+              0, _lib.ptr(LENS), _lib.ptr(END), _lib.ptr(TAKES), _lib.ptr(SELECTED), _lib.ptr(MEMBERS),
               MEMBERS.numel() // 64, _lib.ptr(NT), NT.numel(), _lib.ptr(LOGICAL), _lib.ptr(SLOTS), rows, int(MAXTAKE),
               top, int(S), int(W), _lib.stream_of(LOGICAL))
+
+
+def map_topk_scores(ids, scores, lens, indexed_end, takes, selected, members, nt, logical, slots, max_take, sink,
+                    window):
+    """map_topk with each id's value read from the canonical scores it was
+    selected from (scores[r, id]) instead of a separate values tensor: the
+    form a Top-K that returns ids only (topk.topk_transform_512_v2's raw
+    indices) hands over without a gather."""
+    _lib.require_gpu(ids, scores, lens, indexed_end, takes, selected, members, nt, logical, slots)
+    _i32(ids, lens, indexed_end, takes, selected, members, nt, logical, slots)
+    if scores.dtype != torch.float32 or scores.dim() != 2 or scores.stride(1) != 1:
+        raise ValueError("map_topk_scores: scores must be float32 [rows, cols] with unit inner stride")
+    rows, top = ids.shape
+    if scores.shape[0] != rows or logical.shape != ids.shape or slots.shape != ids.shape:
+        raise ValueError("map_topk_scores: ids, logical, slots [rows, top] and scores [rows, *] must agree")
+    _lib.call("v1_union_map_topk", _lib.ptr(ids), 32, 0, _lib.ptr(scores), scores.stride(0), scores.shape[1],
+              _lib.ptr(lens), _lib.ptr(indexed_end), _lib.ptr(takes), _lib.ptr(selected), _lib.ptr(members),
+              members.numel() // 64, _lib.ptr(nt), nt.numel(), _lib.ptr(logical), _lib.ptr(slots), rows,
+              int(max_take), top, int(sink), int(window), _lib.stream_of(logical))
 
 
 def _stage_tail_shared(grid, NATIVE, NS, NT, LENS, INDEXED_END, K, KS, TAIL_ROWS, CAP, NP, SCRATCH, SINK, WINDOW,

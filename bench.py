@@ -420,7 +420,6 @@ def setup_union(P, dev, torch, np):
     ids = torch.empty((rows, T), device=dev, dtype=torch.int32)
     ids_pages = torch.empty_like(ids)
     identity = torch.arange(width // 64, device=dev, dtype=torch.int32)[None].expand(rows, -1).contiguous()
-    values = torch.empty((rows, T), device=dev)
     logical = torch.empty_like(ids)
     slots = torch.empty_like(ids)
     plan = TU.PreparedStage(d["native"], d["nt"], d["lens"], d_end, fine[cap:], meta_t, desc, S, W)
@@ -433,9 +432,8 @@ def setup_union(P, dev, torch, np):
 
     def select():
         P.topk.topk_transform_512_v2(scores, clens, identity, ids_pages, 64, None, ids)
-        torch.gather(scores, 1, ids.clamp_min(0).long(), out=values)
-        TU.map_topk[(rows,)](ids, values, d["lens"], d_end, d["takes"], d["selected"], d["members"], d["nt"],
-                             logical, slots, mt, T, S, W, T)
+        TU.map_topk_scores(ids, scores, d["lens"], d_end, d["takes"], d["selected"], d["members"], d["nt"], logical,
+                           slots, mt, S, W)
 
     stages = [
         ("prepare", prepare),

@@ -401,7 +401,10 @@ int v1_union_normalize(const float* raw, int64_t raw_stride, int32_t raw_cols, c
                        const int32_t* members, int64_t members_pages, float* out, int32_t rows,
                        int32_t max_take, int32_t width, int32_t sink, int32_t window, int32_t shared,
                        void* stream);
-int v1_union_map_topk(const void* ids, int32_t ids_bits, const float* values, const int32_t* lens,
+/* values == NULL: the value of id i is scores[r * score_stride + i] (the
+ * canonical scores the Top-K selected from; -inf past score_cols). */
+int v1_union_map_topk(const void* ids, int32_t ids_bits, const float* values, const float* scores,
+                      int64_t score_stride, int32_t score_cols, const int32_t* lens,
                       const int32_t* indexed_end, const int32_t* takes, const int32_t* selected,
                       const int32_t* members, int64_t members_pages, const int32_t* nt, int32_t nt_len,
                       int32_t* logical, int32_t* slots, int32_t rows, int32_t max_take, int32_t top,

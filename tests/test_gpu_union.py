@@ -265,9 +265,8 @@ class Chain:
 
     def select(self):
         TK.topk_transform_512_v2(self.scores, self.clens, self.identity, self.slots_raw, 64, None, self.ids)
-        values = self.scores.gather(1, self.ids.clamp_min(0).long())
-        TU.map_topk[(self.rows,)](self.ids, values, self.d_lens, self.d_end, self.d_takes, self.d_sel, self.d_mem,
-                                  self.d_nt, self.logical, self.slots, self.max_take, 2048, self.S, self.W, 2048)
+        TU.map_topk_scores(self.ids, self.scores, self.d_lens, self.d_end, self.d_takes, self.d_sel, self.d_mem,
+                           self.d_nt, self.logical, self.slots, self.max_take, self.S, self.W)
 
     def run(self):
         self.prepare()
@@ -290,6 +289,14 @@ def test_chain_shared_equals_per_row(case):
     assert torch.equal(a.clens, b.clens)
     assert torch.equal(a.scores, b.scores)
     assert torch.equal(a.logical, b.logical) and torch.equal(a.slots, b.slots)
+    # the values form of map_topk (kernels.py:62-76) agrees with values read from the scores
+    values = b.scores.gather(1, b.ids.clamp_min(0).long())
+    lg2, sl2 = torch.empty_like(b.logical), torch.empty_like(b.slots)
+    TU.map_topk[(rows,)](b.ids, values, b.d_lens, b.d_end, b.d_takes, b.d_sel, b.d_mem, b.d_nt, lg2, sl2, b.max_take,
+                         2048, S, W, 2048)
+    assert torch.equal(lg2, b.logical) and torch.equal(sl2, b.slots)
+    e_lg, e_sl = O.union_map_topk(H(b.ids), H(values), b.lens, end, b.takes, b.selected, b.members, b.nt, S, W)
+    assert np.array_equal(H(b.logical), e_lg) and np.array_equal(H(b.slots), e_sl)
     scores, lens = H(b.scores), b.lens
     q = H(b.q.view(torch.uint8)).reshape(rows, 32, 128)
     w = H(b.w)
