@@ -566,43 +566,71 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
 }
 
 // ---------------------------------------------------------------- per row
+// Work-group (x, row) takes the row's 16-page chunks x, x + gridDim.x, ...;
+// wave wv takes pages wv, wv + 4, wv + 8, wv + 12 of each, so a wave's pages
+// ascend.  The next page's key fragments and scale are loaded before the
+// current page's MFMAs (one page load always in flight), and a work-group
+// covers many pages so that work-group launches do not bound short rows.
 template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
     const int l = __lane_id(), wv = threadIdx.x / kWave;
     const int64_t row = blockIdx.y;
-    const int32_t chunk0 = blockIdx.x * kChunkPages;
     const int32_t ctx = min(p.ctx[row], p.max_context_len);
-    const int32_t npages = max(0, min(kChunkPages, (ctx + 63) / 64 - chunk0));
-    v8i a[HB];
-    float w[HB][4];
-    if (npages > 0) {
+    const int32_t row_pages = (ctx + 63) / 64;
+    const int32_t all_pages = (p.max_context_len + 63) / 64;
+    // page of step s of this wave (ascending in s)
+    auto page_at = [&](int32_t s) __attribute__((always_inline)) {
+        return (int32_t)(blockIdx.x + (s >> 2) * gridDim.x) * kChunkPages + wv + 4 * (s & 3);
+    };
+    int32_t s = 0;
+    if (page_at(0) < row_pages) {
+        v8i a[HB];
+        float w[HB][4];
         load_q<HB>(p, row, a);
         load_w<HB>(p, row, w);
-    }
-    for (int32_t pg = wv; pg < kChunkPages; pg += 4) {
-        const int32_t j = (chunk0 + pg) * 64 + l;
-        if (pg >= npages) {
-            if (p.clean) store_logit(p, row, j, ctx, 0.f);
-            continue;
-        }
-        const int32_t page = page_of(p, row, chunk0 + pg);
-        float out = 0.f, scale = 0.f;
-        if (page >= 0) {
+        auto fetch = [&](int32_t pg, v8i (&b)[4], float& scale) __attribute__((always_inline)) {
+            const int32_t page = page_of(p, row, pg);
+            if (page < 0) return false;
             const uint8_t* base = p.kv + (int64_t)page * V1_PAGE_BYTES;
-            v8i b[4];
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
                 const u32x4* src = reinterpret_cast<const u32x4*>(base + (kb * 16 + (l & 15)) * 128 + 32 * (l >> 4));
                 const u32x4 x = src[0], y = src[1];
                 b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
             }
-            float part[4];
-            page_partials<HB, RELU>(a, b, w, part);
-            out = reduce_scatter4(part);
             scale = reinterpret_cast<const float*>(base + 8192)[l];
+            return true;
+        };
+        auto compute = [&](int32_t pg, bool ok, const v8i (&b)[4], float scale) __attribute__((always_inline)) {
+            float out = 0.f;
+            if (ok) {
+                float part[4];
+                page_partials<HB, RELU>(a, b, w, part);
+                out = reduce_scatter4(part);
+            } else {
+                scale = 0.f;
+            }
+            store_logit(p, row, pg * 64 + l, ctx, out * scale);
+        };
+        v8i b0[4], b1[4];
+        float s0 = 0.f, s1 = 0.f;
+        bool ok0 = fetch(page_at(0), b0, s0), ok1 = false;
+        for (;;) {
+            const int32_t pg = page_at(s), nx = page_at(s + 1);
+            if (nx < row_pages) ok1 = fetch(nx, b1, s1);
+            compute(pg, ok0, b0, s0);
+            ++s;
+            if (nx >= row_pages) break;
+            const int32_t nx2 = page_at(s + 1);
+            if (nx2 < row_pages) ok0 = fetch(nx2, b0, s0);
+            compute(nx, ok1, b1, s1);
+            ++s;
+            if (nx2 >= row_pages) break;
         }
-        store_logit(p, row, j, ctx, out * scale);
     }
+    // pages past the row's context: -inf (clean) up to max_context_len
+    if (p.clean)
+        for (int32_t pg = page_at(s); pg < all_pages; pg = page_at(++s)) store_logit(p, row, pg * 64 + l, ctx, 0.f);
 }
 
 struct Shared {
@@ -698,7 +726,9 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         launch_hb<Shared>(hb, a->relu != 0, dim3((uint32_t)std::min<int64_t>(items, wgs)), st, p);
         return V1_LAUNCHED("score_shared");
     }
-    const dim3 grid(chunks, (uint32_t)a->rows);
+    // about 8 work-groups per CU in all, each striding over its row's chunks
+    const int64_t per_row = std::max<int64_t>(1, std::min<int64_t>(chunks, cdiv(8 * (int64_t)v1::device_cus(), a->rows)));
+    const dim3 grid((uint32_t)per_row, (uint32_t)a->rows);
     launch_hb<Rows>(hb, a->relu != 0, grid, st, p);
     return V1_LAUNCHED("score_rows");
 }
