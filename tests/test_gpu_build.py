@@ -172,3 +172,21 @@ def test_build_buckets_vs_oracle_and_chain(mods):
     # the per-kernel chain gives the same bytes
     c = _chain(mods, pd, T(tables[1]), T(np.int32([int(starts[1]), 0, 1])))
     assert torch.equal(c[1], perm[1]) and torch.equal(c[2], tmp[1]) and torch.equal(c[4], centers[1])
+
+
+def test_build_buckets_out_of_pool_pages_and_empty_batch(mods):
+    # page ids outside the pool read page 0 (the reference leaves them undefined): the result equals
+    # the oracle's build of the same table with those ids replaced by 0
+    _, _, IB = mods
+    pool = _pool(7)
+    table = np.random.default_rng(7).permutation(24)[:16].astype(np.int32)
+    bad = table.copy()
+    bad[[3, 11]] = [24, 1 << 20]
+    fixed = bad.copy()
+    fixed[[3, 11]] = 0
+    perm, tmp, mapping, centers = IB.build_buckets(T(pool), T(bad[None]), T(np.int32([64])))
+    e_perm, e_tmp, e_map, e_centers = O.index_build(pool, fixed, 64)
+    assert np.array_equal(H(perm[0]), e_perm) and np.array_equal(H(tmp[0]), e_tmp)
+    assert np.array_equal(H(mapping[0]), e_map) and np.array_equal(H(centers[0]), e_centers)
+    out = IB.build_buckets(T(pool), T(np.zeros((0, 16), np.int32)), T(np.zeros(0, np.int32)))
+    assert all(o.shape[0] == 0 for o in out)

@@ -342,3 +342,12 @@ def test_unindexed_token_reaches_last_row_topk():
     b.run()
     lg = H(b.logical)[-1]
     assert token in lg.tolist()
+
+
+@pytest.mark.parametrize("end", [-5, 10 ** 6])
+def test_stage_union_published_end_outside_lengths(end):
+    # a negative published end counts as 0 (every visible token is a tail candidate); one past every
+    # length leaves sink + window only (union.py:10-14)
+    c = Case(3000, 70, 17, 100, end)
+    c.plan()
+    c.check(end, c.nt)
