@@ -1,0 +1,53 @@
+"""Decode attention over the gathered workspace: the consumer after the slot
+gather.  sglang/srt/layers/attention/v1_native/backend.py:306-315 calls
+flash_attn_with_kvcache(q[:, None], kg, vg, causal=False,
+softmax_scale=layer.scaling) with q [rows, 1, 4, 128] and kg / vg
+[rows, 2048, 1, 128] from GatherWorkspace.gather; flash_attn_with_kvcache here
+keeps that call shape for one query position per row (bf16, head dim 128, at
+most 4 query heads per KV head).  With one query position, causal masking
+changes nothing, so `causal` is accepted either way.  Rows attend their first
+cache_seqlens[b] keys (all keys when it is None); a row without keys gives
+zeros.
+"""
+import math
+
+import torch
+
+from . import _lib
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None, softmax_scale=None,
+                            causal=False, out=None, **unsupported):
+    if k is not None or v is not None:
+        raise NotImplementedError("flash_attn_with_kvcache: appending k / v to the cache is not supported")
+    bad = {key: val for key, val in unsupported.items() if val not in (None, False, 0, (-1, -1), 0.0)}
+    if bad:
+        raise NotImplementedError(f"flash_attn_with_kvcache: unsupported options {sorted(bad)}")
+    _lib.require_gpu(q, k_cache, v_cache, cache_seqlens, out)
+    if q.dim() != 4 or q.shape[1] != 1:
+        raise ValueError("q must be [batch, 1, heads, 128] (one query position per row)")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache and v_cache must be [batch, keys, kv_heads, 128] of one shape")
+    if not (q.dtype == k_cache.dtype == v_cache.dtype == torch.bfloat16):
+        raise ValueError("q, k_cache and v_cache must be bfloat16")
+    B, _, Hq, D = q.shape
+    Bk, S, Hkv, Dk = k_cache.shape
+    if D != 128 or Dk != 128 or Bk != B:
+        raise ValueError("head dim must be 128 and batch sizes must agree")
+    if Hq % Hkv or Hq // Hkv > 4:
+        raise ValueError("query heads must be a multiple of KV heads, at most 4 per KV head")
+    if q.stride(3) != 1 or k_cache.stride(3) != 1 or v_cache.stride(3) != 1:
+        raise ValueError("the head dimension must be contiguous")
+    if cache_seqlens is not None and (cache_seqlens.dtype != torch.int32 or cache_seqlens.numel() != B
+                                      or not cache_seqlens.is_contiguous()):
+        raise ValueError("cache_seqlens must be a contiguous int32 [batch] tensor")
+    if out is None:
+        out = torch.empty((B, 1, Hq, D), device=q.device, dtype=torch.bfloat16)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (B, 1, Hq, D) or out.stride(3) != 1:
+        raise ValueError("out must be bfloat16 [batch, 1, heads, 128] with a contiguous head dimension")
+    scale = float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(D)
+    _lib.call("v1_decode_attention", _lib.ptr(q), q.stride(0), q.stride(2), _lib.ptr(k_cache), k_cache.stride(0),
+              k_cache.stride(1), k_cache.stride(2), _lib.ptr(v_cache), v_cache.stride(0), v_cache.stride(1),
+              v_cache.stride(2), _lib.ptr(cache_seqlens), _lib.ptr(out), out.stride(0), out.stride(2), B, Hq, Hkv, S,
+              scale, _lib.stream_of(q))
+    return out

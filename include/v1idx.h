@@ -409,6 +409,21 @@ int v1_union_map_topk(const void* ids, int32_t ids_bits, const float* values, co
                       const int32_t* members, int64_t members_pages, const int32_t* nt, int32_t nt_len,
                       int32_t* logical, int32_t* slots, int32_t rows, int32_t max_take, int32_t top,
                       int32_t sink, int32_t window, void* stream);
+/* ------------------------------------------------------------------------
+ * Decode attention over the gathered workspace (the consumer after the slot
+ * gather): sglang/srt/layers/attention/v1_native/backend.py:306-315 calls
+ * flash_attn_with_kvcache(q[:, None], kg, vg, causal=False, softmax_scale)
+ * on GatherWorkspace rows.  bf16 q [batch, heads_q, 128], k / v [batch, keys,
+ * heads_kv, 128] (element strides, inner dim contiguous, 16-byte aligned),
+ * heads_q / heads_kv <= 4 query heads per KV head, keys * group <= 12288;
+ * out[b, h] (bf16) = softmax over the first seqlens[b] keys (all keys when
+ * seqlens is NULL; zeros for a row without keys) of scale * q . k, times v.
+ * ---------------------------------------------------------------------- */
+int v1_decode_attention(const void* q, int64_t q_batch, int64_t q_head, const void* k, int64_t k_batch,
+                        int64_t k_token, int64_t k_head, const void* v, int64_t v_batch, int64_t v_token,
+                        int64_t v_head, const int32_t* seqlens, void* out, int64_t o_batch, int64_t o_head,
+                        int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t keys, float scale,
+                        void* stream);
 #ifdef __cplusplus
 }
 #endif

@@ -854,3 +854,28 @@ def union_map_topk(ids, values, lens, end, takes, selected, members, nt, S, W):
                 slots[r, i] = int(nt[lg // 64]) * 64 + lg % 64
     return logical, slots
 
+
+
+# ------------------------------------------------- attention consumer
+def decode_attention(q, k, v, scale, seqlens=None):
+    """sglang/srt/layers/attention/v1_native/backend.py:306-315
+    (flash_attn_with_kvcache(q[:, None], kg, vg, causal=False, softmax_scale)),
+    one query position per row: q [B, Hq, D], k / v [B, S, Hkv, D] (float
+    values of the bf16 inputs); out[b, h] = softmax over the first n_b keys of
+    scale * q . k, times v, in float64 (zeros for a row without keys)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    B, Hq, D = q.shape
+    S, Hkv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    out = np.zeros((B, Hq, D))
+    for b in range(B):
+        n = S if seqlens is None else min(max(int(seqlens[b]), 0), S)
+        if n == 0:
+            continue
+        for h in range(Hq):
+            s = scale * (k[b, :n, h // G] @ q[b, h])
+            p = np.exp(s - s.max())
+            out[b, h] = (p / p.sum()) @ v[b, :n, h // G]
+    return out
