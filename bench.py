@@ -20,6 +20,8 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
                their own page tables in a 2M-token pool -> Top-2048 -> gather
   6            index build: every 1024-token bucket of a 2M-token FP8 pool (2048 buckets)
                -> member order, reordered pages and FP8 centers, one launch
+  8            attention consumer: 4096 queries x 4 heads of one KV head, 2048 gathered bf16
+               K/V slots each (1M-slot pool) -> decode attention
   7            shared sink+tail chunk: 64K published tokens, 4096 causal queries x 32 heads,
                sink 64 / window 2048, 40 history pages per query: one union of sink+tail
                pages -> FP8 score -> canonical order -> Top-2048 -> slots (per-row staging
@@ -88,7 +90,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6, 7])
+    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6, 7, 8])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES bytes (HBM counter calibration) and exit")
@@ -110,7 +112,7 @@ def copy_calibration(nbytes):
 class Pkg:
     def __init__(self):
         for name in ("workloads", "scoring", "topk", "native_kernels", "query_fused", "kernels", "pagepool",
-                     "indexbuild", "tailunion"):
+                     "indexbuild", "tailunion", "attention"):
             setattr(self, name, importlib.import_module(f"10_20_amd.{name}"))
 
 
@@ -481,8 +483,52 @@ def setup_union(P, dev, torch, np):
     return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 7)"
 
 
+def setup_consumer(P, dev, torch, np):
+    """Configuration 8: the backend's inner loop for one KV head and one
+    microbatch (sglang/srt/layers/attention/v1_native/backend.py:300-315):
+    Top-2048 slot ids -> GatherWorkspace.gather (bf16 K / V) ->
+    flash_attn_with_kvcache(qs[:, None], kg, vg)."""
+    rows, T, slots, heads_kv, group = 4096, 2048, 1 << 20, 2, 4
+    g = torch.Generator(device=dev).manual_seed(8)
+    kp = torch.randn((slots, heads_kv, 128), device=dev, generator=g).to(torch.bfloat16)
+    vp = torch.randn((slots, heads_kv, 128), device=dev, generator=g).to(torch.bfloat16)
+    req = torch.randperm(slots, device=dev, generator=g).to(torch.int32)
+    ids = torch.randint(0, slots, (rows, T), device=dev, generator=g, dtype=torch.int32)
+    q3 = torch.randn((rows, heads_kv * group, 128), device=dev, generator=g).to(torch.bfloat16)
+    qs = q3[:, :group].contiguous()
+    work = P.native_kernels.GatherWorkspace(rows, dev, torch.bfloat16)
+    out = torch.empty((rows, 1, group, 128), device=dev, dtype=torch.bfloat16)
+    scale = 1.0 / 128 ** 0.5
+    kv = {}
+
+    def gather():
+        kv["k"], kv["v"] = work.gather(kp, vp, req, ids, 0)
+
+    stages = [
+        ("gather", gather),
+        ("attention", lambda: P.attention.flash_attn_with_kvcache(qs[:, None], kv["k"], kv["v"], causal=False,
+                                                                  softmax_scale=scale, out=out)),
+    ]
+    kv_bytes = 2.0 * rows * T * 256  # K and V rows of one head
+    work_units = {
+        # pool rows read (1M slots x 512 B per head pair: far above the last-level cache) and workspace written
+        "gather": ((2 * kv_bytes + 4.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "attention": ((kv_bytes + 2.0 * rows * group * 128 * 2) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+    }
+
+    def cpu(budget):
+        from oracle import cpu_baseline
+        qps, n, threads = cpu_baseline.consumer_queries_per_second(kp, vp, req, ids, qs, scale, budget)
+        return qps, threads, f"{n} of {rows} queries (2048-slot gather + 4-head attention)"
+
+    meta = {"workload": f"attention consumer: {rows} queries x {group} heads of one KV head, 2048 gathered bf16 "
+                        f"K/V slots each from a {slots >> 20}M-slot pool -> decode attention",
+            "global_batch": rows, "seq_len": T, "parallelism": "single GPU"}
+    return rows, stages, work_units, cpu, meta, "synthetic (torch generator seed 8)"
+
+
 SETUPS = {1: setup_example, 2: setup_pages, 3: setup_gather, 4: setup_prefill, 5: setup_decode, 6: setup_build,
-          7: setup_union}
+          7: setup_union, 8: setup_consumer}
 RATE_UNITS = {2: "requests/s", 6: "tokens/s"}
 METRICS = {6: "index-build tokens/sec (initialize+bisection+assemble) and % of HBM roofline"}
 

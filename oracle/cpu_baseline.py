@@ -225,3 +225,22 @@ def union_queries_per_second(a, prm, budget_s=10.0, min_rows=4):
         del slots
         done += 1
     return done / (time.perf_counter() - t0), done, threads
+
+
+def consumer_queries_per_second(kp, vp, req, ids, qs, scale, budget_s=10.0, min_rows=4):
+    """The backend's gather + attention (backend.py:300-315) for one KV head, row
+    after row, with torch on the host: K / V rows of the row's 2048 slots, then
+    softmax(scale q k^T) v for its query heads.  Returns (q/s, rows, threads)."""
+    threads = torch.get_num_threads()
+    kp, vp = kp[:, 0].float().cpu(), vp[:, 0].float().cpu()
+    req, ids, qs = req.cpu().long(), ids.cpu().long(), qs.float().cpu()
+    rows = ids.shape[0]
+    done, t0 = 0, time.perf_counter()
+    while done < rows and (done < min_rows or time.perf_counter() - t0 < budget_s):
+        sel = req[ids[done]]
+        k, v = kp[sel], vp[sel]
+        p = torch.softmax(qs[done] @ k.T * scale, -1)
+        out = p @ v
+        del out
+        done += 1
+    return done / (time.perf_counter() - t0), done, threads
