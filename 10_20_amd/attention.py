@@ -51,3 +51,40 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
               v_cache.stride(2), _lib.ptr(cache_seqlens), _lib.ptr(out), out.stride(0), out.stride(2), B, Hq, Hkv, S,
               scale, _lib.stream_of(q))
     return out
+
+
+def attend_slots(q, k_pool, v_pool, request_slots, ids, head, softmax_scale=None, out=None):
+    """GatherWorkspace.gather(k_pool, v_pool, request_slots, ids, head) followed by
+    flash_attn_with_kvcache(q[:, None], kg, vg) in one pass over the pools, no
+    workspace: q [rows, heads, 128] (or [rows, 1, heads, 128]) bf16 with at most
+    4 heads, pools [slots, kv_heads, 128] bf16 (head dim contiguous), ids
+    [rows, keys] int32 into request_slots.  Returns [rows, 1, heads, 128],
+    equal bit for bit to the two-step form."""
+    _lib.require_gpu(q, k_pool, v_pool, request_slots, ids, out)
+    if q.dim() == 4:
+        if q.shape[1] != 1:
+            raise ValueError("q must hold one query position per row")
+        q = q[:, 0]
+    if q.dim() != 3 or q.shape[2] != 128 or q.dtype != torch.bfloat16 or q.stride(2) != 1:
+        raise ValueError("q must be bfloat16 [rows, heads, 128] with a contiguous head dimension")
+    for pool in (k_pool, v_pool):
+        if pool.dim() != 3 or pool.shape[2] != 128 or pool.dtype != torch.bfloat16 or pool.stride(2) != 1:
+            raise ValueError("pools must be bfloat16 [slots, kv_heads, 128] with a contiguous head dimension")
+    if k_pool.shape[:2] != v_pool.shape[:2] or not 0 <= int(head) < k_pool.shape[1]:
+        raise ValueError("k_pool and v_pool must agree and head must be one of their KV heads")
+    if request_slots.dtype != torch.int32 or request_slots.dim() != 1 or not request_slots.is_contiguous():
+        raise ValueError("request_slots must be a contiguous int32 vector")
+    if ids.dtype != torch.int32 or ids.dim() != 2 or ids.shape[0] != q.shape[0] or ids.stride(1) != 1:
+        raise ValueError("ids must be int32 [rows, keys] with a contiguous inner dimension")
+    rows, heads, _ = q.shape
+    if out is None:
+        out = torch.empty((rows, 1, heads, 128), device=q.device, dtype=torch.bfloat16)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (rows, 1, heads, 128) or out.stride(3) != 1:
+        raise ValueError("out must be bfloat16 [rows, 1, heads, 128] with a contiguous head dimension")
+    scale = float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(128)
+    _lib.call("v1_decode_attention_slots", _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k_pool), k_pool.stride(0),
+              k_pool.stride(1), _lib.ptr(v_pool), v_pool.stride(0), v_pool.stride(1), k_pool.shape[0], int(head),
+              _lib.ptr(request_slots), request_slots.numel(), _lib.ptr(ids), ids.stride(0), _lib.ptr(out),
+              out.stride(0), out.stride(2), rows, heads, ids.shape[1], scale, _lib.stream_of(q))
+    return out
+

@@ -15,6 +15,14 @@
 // pass 2 streams V with p = exp(s - max) and sums p * v in registers; the 16
 // groups' partial sums are added in LDS.  K and V are each read once: the
 // kernel is bound by HBM (4 * G flops per key byte).
+//
+// Slot form: keys come straight from the K / V pools of one KV head through
+// the row's slot ids (req[ids[b, j]], the GatherWorkspace mapping of
+// sglang/srt/layers/attention/v1_native/kernels.py:62-77); an id below zero
+// or past req, or a slot outside the pool, is a zero key and value, exactly
+// what the gather writes.  Same arithmetic, without the workspace round trip;
+// the row's slots are resolved into LDS first (all keys at once), so the key
+// and value loads do not wait on the id -> slot chain.
 #include <algorithm>
 
 #include "common.h"
@@ -74,9 +82,22 @@ struct AttnParams {
     int64_t o_batch, o_head;
     int32_t keys;
     float scale;
+    // slot form
+    const int32_t* ids;
+    int64_t ids_stride;
+    const int32_t* req;
+    int64_t req_len;
+    int64_t pool_rows;
 };
 
+// Floats of LDS before the slot rows: the scores [G][keys], later reused for
+// the partial sums [16][G][128] and their weights [16][G].
 template <int G>
+__host__ __device__ constexpr int64_t attn_floats(int64_t keys) {
+    return G * keys > 16 * G * kAttnDim + 16 * G ? G * keys : 16 * G * kAttnDim + 16 * G;
+}
+
+template <int G, bool SLOTS>
 __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(AttnParams p) {
     extern __shared__ float smem[];  // scores [G][keys], later partials [16][G][128] + sums [16][G]
     __shared__ float red[16][kMaxGroup];
@@ -92,8 +113,27 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(AttnParams p)
         const uint4 w = *reinterpret_cast<const uint4*>(p.q + b * p.q_batch + (int64_t)(kvh * G + h) * p.q_head + 8 * c);
         bf16x8(w, qf[h]);
     }
-    const uint16_t* kr = p.k + b * p.k_batch + (int64_t)kvh * p.k_head + 8 * c;
-    const uint16_t* vr = p.v + b * p.v_batch + (int64_t)kvh * p.v_head + 8 * c;
+    const uint16_t* kr = p.k + (SLOTS ? 0 : b * p.k_batch) + (int64_t)kvh * p.k_head + 8 * c;
+    const uint16_t* vr = p.v + (SLOTS ? 0 : b * p.v_batch) + (int64_t)kvh * p.v_head + 8 * c;
+    // slot form: every key's pool row (-1: a zero key) into LDS past the scores / partials
+    int32_t* rows_s = reinterpret_cast<int32_t*>(smem + attn_floats<G>(S));
+    if constexpr (SLOTS) {
+        for (int32_t j = t; j < n; j += kAttnThreads) {
+            const int32_t id = p.ids[b * p.ids_stride + j];
+            int32_t slot = -1;
+            if (id >= 0 && id < p.req_len) {
+                slot = p.req[id];
+                if (slot < 0 || slot >= p.pool_rows) slot = -1;
+            }
+            rows_s[j] = slot;
+        }
+        __syncthreads();
+    }
+    // row of key j in the K / V arrays (-1: a zero key)
+    auto key_row = [&](int32_t j) __attribute__((always_inline)) -> int64_t {
+        if constexpr (!SLOTS) return j;
+        else return rows_s[j];
+    };
 
     // pass 1: scores and the group maxima
     float mx[G];
@@ -104,7 +144,8 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(AttnParams p)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int32_t j = j0 + 16 * u;
-            kw[u] = j < n ? *reinterpret_cast<const uint4*>(kr + (int64_t)j * p.k_token) : make_uint4(0, 0, 0, 0);
+            const int64_t r = j < n ? key_row(j) : -1;
+            kw[u] = r >= 0 ? *reinterpret_cast<const uint4*>(kr + r * p.k_token) : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -150,7 +191,8 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(AttnParams p)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int32_t j = j0 + 16 * u;
-            vw[u] = j < n ? *reinterpret_cast<const uint4*>(vr + (int64_t)j * p.v_token) : make_uint4(0, 0, 0, 0);
+            const int64_t r = j < n ? key_row(j) : -1;
+            vw[u] = r >= 0 ? *reinterpret_cast<const uint4*>(vr + r * p.v_token) : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -191,12 +233,22 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(AttnParams p)
     }
 }
 
-template <int G>
+template <int G, bool SLOTS>
 int launch_attn(const AttnParams& p, int32_t batch, int32_t heads_kv, hipStream_t st) {
-    const size_t lds = sizeof(float) * (size_t)std::max(G * p.keys, 16 * G * kAttnDim + 16 * G);
-    hipLaunchKernelGGL((decode_attn_kernel<G>), dim3((uint32_t)heads_kv, (uint32_t)batch), dim3(kAttnThreads), lds, st,
-                       p);
+    const size_t lds = sizeof(float) * (size_t)(attn_floats<G>(p.keys) + (SLOTS ? p.keys : 0));
+    hipLaunchKernelGGL((decode_attn_kernel<G, SLOTS>), dim3((uint32_t)heads_kv, (uint32_t)batch), dim3(kAttnThreads),
+                       lds, st, p);
     return V1_LAUNCHED("decode_attention");
+}
+
+template <bool SLOTS>
+int launch_group(int32_t G, const AttnParams& p, int32_t batch, int32_t heads_kv, hipStream_t st) {
+    switch (G) {
+        case 1: return launch_attn<1, SLOTS>(p, batch, heads_kv, st);
+        case 2: return launch_attn<2, SLOTS>(p, batch, heads_kv, st);
+        case 3: return launch_attn<3, SLOTS>(p, batch, heads_kv, st);
+        default: return launch_attn<4, SLOTS>(p, batch, heads_kv, st);
+    }
 }
 
 }  // namespace
@@ -221,12 +273,31 @@ extern "C" int v1_decode_attention(const void* q, int64_t q_batch, int64_t q_hea
     if (batch == 0) return V1_OK;
     AttnParams p{static_cast<const uint16_t*>(q), q_batch, q_head, static_cast<const uint16_t*>(k), k_batch, k_token,
                  k_head, static_cast<const uint16_t*>(v), v_batch, v_token, v_head, seqlens,
-                 static_cast<uint16_t*>(out), o_batch, o_head, keys, scale};
-    hipStream_t st = as_stream(stream);
-    switch (G) {
-        case 1: return launch_attn<1>(p, batch, heads_kv, st);
-        case 2: return launch_attn<2>(p, batch, heads_kv, st);
-        case 3: return launch_attn<3>(p, batch, heads_kv, st);
-        default: return launch_attn<4>(p, batch, heads_kv, st);
-    }
+                 static_cast<uint16_t*>(out), o_batch, o_head, keys, scale, nullptr, 0, nullptr, 0, 0};
+    return launch_group<false>(G, p, batch, heads_kv, as_stream(stream));
+}
+
+extern "C" int v1_decode_attention_slots(const void* q, int64_t q_batch, int64_t q_head, const void* k_pool,
+                                         int64_t k_slot, int64_t k_head, const void* v_pool, int64_t v_slot,
+                                         int64_t v_head, int64_t pool_slots, int32_t head, const int32_t* req,
+                                         int64_t req_len, const int32_t* ids, int64_t ids_stride, void* out,
+                                         int64_t o_batch, int64_t o_head, int32_t rows, int32_t heads_q, int32_t keys,
+                                         float scale, void* stream) {
+    V1_REQUIRE(rows >= 0 && heads_q > 0 && heads_q <= kMaxGroup && keys >= 0 && head >= 0 && pool_slots >= 0,
+               "decode_attention_slots: bad shape (at most %d query heads)", kMaxGroup);
+    V1_REQUIRE((int64_t)heads_q * keys + keys <= kMaxScores, "decode_attention_slots: keys x (heads + 1) above %d",
+               kMaxScores);
+    V1_REQUIRE(req != nullptr && req_len > 0 && ids != nullptr, "decode_attention_slots: empty slot map");
+    const int64_t strides[] = {q_batch, q_head, k_slot, k_head, v_slot, v_head, o_batch, o_head};
+    bool aligned = (reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_pool) |
+                    reinterpret_cast<uintptr_t>(v_pool)) % 16 == 0;
+    for (int64_t s : strides) aligned = aligned && s % 8 == 0;
+    V1_REQUIRE(aligned, "decode_attention_slots: q and the pools must be 16-byte aligned, strides multiples of 8");
+    if (rows == 0) return V1_OK;
+    // the chosen KV head becomes head 0 of a one-head problem
+    AttnParams p{static_cast<const uint16_t*>(q), q_batch, q_head,
+                 static_cast<const uint16_t*>(k_pool) + (int64_t)head * k_head, 0, k_slot, 0,
+                 static_cast<const uint16_t*>(v_pool) + (int64_t)head * v_head, 0, v_slot, 0, nullptr,
+                 static_cast<uint16_t*>(out), o_batch, o_head, keys, scale, ids, ids_stride, req, req_len, pool_slots};
+    return launch_group<true>(heads_q, p, rows, 1, as_stream(stream));
 }

@@ -521,9 +521,14 @@ def setup_consumer(P, dev, torch, np):
         qps, n, threads = cpu_baseline.consumer_queries_per_second(kp, vp, req, ids, qs, scale, budget)
         return qps, threads, f"{n} of {rows} queries (2048-slot gather + 4-head attention)"
 
+    fused_out = torch.empty_like(out)
     meta = {"workload": f"attention consumer: {rows} queries x {group} heads of one KV head, 2048 gathered bf16 "
                         f"K/V slots each from a {slots >> 20}M-slot pool -> decode attention",
-            "global_batch": rows, "seq_len": T, "parallelism": "single GPU"}
+            "global_batch": rows, "seq_len": T, "parallelism": "single GPU",
+            # the gather folded into the attention (same result, no workspace), timed beside the chain
+            "_extra": [("gather_fused_attention",
+                        lambda: P.attention.attend_slots(qs, kp, vp, req, ids, 0, softmax_scale=scale, out=fused_out),
+                        ((kv_bytes + 4.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"))]}
     return rows, stages, work_units, cpu, meta, "synthetic (torch generator seed 8)"
 
 

@@ -424,6 +424,19 @@ int v1_decode_attention(const void* q, int64_t q_batch, int64_t q_head, const vo
                         int64_t v_head, const int32_t* seqlens, void* out, int64_t o_batch, int64_t o_head,
                         int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t keys, float scale,
                         void* stream);
+/* The same attention with the gather folded in: key j of row b is slot
+ * req[ids[b * ids_stride + j]] of KV head `head` of the pools (k_pool[slot *
+ * k_slot + head * k_head + d]), an id < 0 or >= req_len or a slot outside
+ * [0, pool_slots) being a zero key and value (GatherWorkspace's rule,
+ * sglang/srt/layers/attention/v1_native/kernels.py:62-77): equal, bit for
+ * bit, to v1_gather_slots followed by v1_decode_attention, without the
+ * workspace.  heads_q <= 4 query heads, keys * (heads_q + 1) <= 12288. */
+int v1_decode_attention_slots(const void* q, int64_t q_batch, int64_t q_head, const void* k_pool,
+                              int64_t k_slot, int64_t k_head, const void* v_pool, int64_t v_slot,
+                              int64_t v_head, int64_t pool_slots, int32_t head, const int32_t* req,
+                              int64_t req_len, const int32_t* ids, int64_t ids_stride, void* out,
+                              int64_t o_batch, int64_t o_head, int32_t rows, int32_t heads_q, int32_t keys,
+                              float scale, void* stream);
 #ifdef __cplusplus
 }
 #endif

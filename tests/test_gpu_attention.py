@@ -102,3 +102,24 @@ def test_rejects_unsupported_shapes():
         AT.flash_attn_with_kvcache(q[:, :, :4].float(), kv, kv)
     with pytest.raises(NotImplementedError):
         AT.flash_attn_with_kvcache(q[:, :, :4], kv, kv, k=kv)
+
+
+@pytest.mark.parametrize("heads", [4, 1])
+def test_attend_slots_equals_gather_then_attention(heads):
+    # the fused form reads the pools through the slot map: bit-identical to gather + attention,
+    # including ids below zero or past the map and map entries outside the pool (zero keys)
+    g = torch.Generator(device=DEV).manual_seed(11 + heads)
+    slots, rows = 30000, 96
+    kp = torch.randn((slots, 2, 128), device=DEV, generator=g).to(torch.bfloat16)
+    vp = torch.randn((slots, 2, 128), device=DEV, generator=g).to(torch.bfloat16)
+    req = torch.randperm(slots, device=DEV, generator=g).to(torch.int32)
+    req[:50] = slots + 7        # past the pool
+    req[50:60] = -2             # negative map entries
+    ids = torch.randint(-5, slots + 100, (rows, 2048), device=DEV, generator=g, dtype=torch.int32)
+    qs = torch.randn((rows, heads, 128), device=DEV, generator=g).to(torch.bfloat16)
+    work = NK.GatherWorkspace(rows, DEV, torch.bfloat16)
+    for head in (0, 1):
+        kg, vg = work.gather(kp, vp, req, ids, head)
+        two = AT.flash_attn_with_kvcache(qs[:, None], kg, vg, causal=False, softmax_scale=0.09)
+        one = AT.attend_slots(qs, kp, vp, req, ids, head, softmax_scale=0.09)
+        assert torch.equal(one, two)
