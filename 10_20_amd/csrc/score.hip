@@ -571,16 +571,34 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
 // ascend.  The next page's key fragments and scale are loaded before the
 // current page's MFMAs (one page load always in flight), and a work-group
 // covers many pages so that work-group launches do not bound short rows.
+// The work-group first resolves the pool pages of all its chunks into LDS
+// (up to kRowPids), so a page's key loads never wait on its table entry.
+constexpr int kRowPids = 2048;
+
 template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
+    __shared__ int32_t pid_s[kRowPids];
     const int l = __lane_id(), wv = threadIdx.x / kWave;
     const int64_t row = blockIdx.y;
     const int32_t ctx = min(p.ctx[row], p.max_context_len);
     const int32_t row_pages = (ctx + 63) / 64;
     const int32_t all_pages = (p.max_context_len + 63) / 64;
-    // page of step s of this wave (ascending in s)
+    // page of step s of this wave (ascending in s); its slot in pid_s
     auto page_at = [&](int32_t s) __attribute__((always_inline)) {
         return (int32_t)(blockIdx.x + (s >> 2) * gridDim.x) * kChunkPages + wv + 4 * (s & 3);
+    };
+    const int32_t my_chunks = max(0, ((row_pages + kChunkPages - 1) / kChunkPages - (int32_t)blockIdx.x +
+                                      (int32_t)gridDim.x - 1) / (int32_t)gridDim.x);
+    const bool staged = my_chunks * kChunkPages <= kRowPids;
+    if (staged) {
+        for (int32_t li = threadIdx.x; li < my_chunks * kChunkPages; li += kThreads) {
+            const int32_t pg = (int32_t)(blockIdx.x + (li / kChunkPages) * gridDim.x) * kChunkPages + li % kChunkPages;
+            pid_s[li] = pg < row_pages ? page_of(p, row, pg) : -1;
+        }
+        __syncthreads();
+    }
+    auto pool_page = [&](int32_t s, int32_t pg) __attribute__((always_inline)) {
+        return staged ? pid_s[(s >> 2) * kChunkPages + wv + 4 * (s & 3)] : page_of(p, row, pg);
     };
     int32_t s = 0;
     if (page_at(0) < row_pages) {
@@ -588,8 +606,8 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
         float w[HB][4];
         load_q<HB>(p, row, a);
         load_w<HB>(p, row, w);
-        auto fetch = [&](int32_t pg, v8i (&b)[4], float& scale) __attribute__((always_inline)) {
-            const int32_t page = page_of(p, row, pg);
+        auto fetch = [&](int32_t s, int32_t pg, v8i (&b)[4], float& scale) __attribute__((always_inline)) {
+            const int32_t page = pool_page(s, pg);
             if (page < 0) return false;
             const uint8_t* base = p.kv + (int64_t)page * V1_PAGE_BYTES;
 #pragma unroll
@@ -614,15 +632,15 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
         };
         v8i b0[4], b1[4];
         float s0 = 0.f, s1 = 0.f;
-        bool ok0 = fetch(page_at(0), b0, s0), ok1 = false;
+        bool ok0 = fetch(0, page_at(0), b0, s0), ok1 = false;
         for (;;) {
             const int32_t pg = page_at(s), nx = page_at(s + 1);
-            if (nx < row_pages) ok1 = fetch(nx, b1, s1);
+            if (nx < row_pages) ok1 = fetch(s + 1, nx, b1, s1);
             compute(pg, ok0, b0, s0);
             ++s;
             if (nx >= row_pages) break;
             const int32_t nx2 = page_at(s + 1);
-            if (nx2 < row_pages) ok0 = fetch(nx2, b0, s0);
+            if (nx2 < row_pages) ok0 = fetch(s + 1, nx2, b0, s0);
             compute(nx, ok1, b1, s1);
             ++s;
             if (nx2 >= row_pages) break;
