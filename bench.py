@@ -386,10 +386,42 @@ def setup_build(P, dev, torch, np):
         tps, n, threads = cpu_baseline.build_tokens_per_second(a["native"], a["tables"], a["starts"], budget)
         return tps, threads, f"{n} of {B} buckets (initialize -> 7 bisection levels -> assemble, numpy)"
 
+    # the reference's per-bucket chain (runtime.py:171-216: initialize, 7 x (3 _dots + 2 _anchor + _sort),
+    # assemble; 44 launches) through the drop-in kernels, over the first 16 buckets, timed beside the batch
+    K, FG = P.kernels, importlib.import_module("10_20_amd.fused_grouping")
+    chain_buckets = 16
+    unit = torch.empty((1024, 128), device=dev)
+    cperm = [torch.empty(1024, device=dev, dtype=torch.int32) for _ in range(2)]
+    anchor = torch.empty((64, 2), device=dev, dtype=torch.int32)
+    cscores = torch.empty(1024, device=dev)
+    flag = torch.zeros((), device=dev, dtype=torch.int32)
+    ctmp = torch.empty((16, 8448), device=dev, dtype=torch.uint8)
+    ccent = torch.empty((2, 8448), device=dev, dtype=torch.uint8)
+    cmap = torch.empty((16, 64), device=dev, dtype=torch.int32)
+    metas = [torch.tensor([int(a["starts"][i]), 0, 1], device=dev, dtype=torch.int32) for i in range(chain_buckets)]
+
+    def chain():
+        for i in range(chain_buckets):
+            tab = tables[i]
+            K.initialize[(64,)](pool, pool.view(torch.float32), tab, metas[i], unit, cperm[0], flag, num_warps=4)
+            cur = 0
+            for n in (1024, 512, 256, 128, 64, 32, 16):
+                for mode in (0, 1, 2):
+                    FG._dots[(64, 1)](unit, cperm[cur], anchor, cscores, flag, n, 0, mode, num_warps=4,
+                                      enable_fp_fusion=False)
+                    if mode < 2:
+                        FG._anchor[(1024 // n, 1)](cperm[cur], anchor, cscores, flag, n, mode, num_warps=4)
+                FG._sort[(1024 // n, 1)](cperm[cur], cperm[1 - cur], cscores, flag, n, num_warps=4)
+                cur = 1 - cur
+            K.assemble[(16, 8)](pool, pool.view(torch.float32), tab, metas[i], cperm[cur], ctmp,
+                                ctmp.view(torch.float32), ccent, ccent.view(torch.float32), cmap, num_warps=4)
+
     meta = {"workload": f"index build: {B} buckets of 1024 tokens (16 pages each, every page of a "
                         f"{prm['pool_pages'] * 64 // (1 << 20)}M-token FP8 pool once) -> member order, "
                         "reordered pages, 128 FP8 centers per bucket",
-            "global_batch": B, "seq_len": 1024, "parallelism": "single GPU"}
+            "global_batch": B, "seq_len": 1024, "parallelism": "single GPU",
+            "_extra": [(f"per_kernel_chain_{chain_buckets}_buckets", chain,
+                        (BUILD_BUCKET_BYTES * chain_buckets / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"))]}
     return B * 1024, stages, work_units, cpu, meta, "synthetic (PCG64 seed 6)"
 
 
