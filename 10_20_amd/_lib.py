@@ -112,6 +112,9 @@ _SIGNATURES = {
     "v1_decode_attention_slots": (_c_i32, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64,
                                            _c_i32, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i32, _c_i32,
                                            _c_i32, ctypes.c_float, _vp]),
+    "v1_union_spans": (_c_i32, [_vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _vp]),
+    "v1_union_normalize_split": (_c_i32, [_vp, _c_i64, _c_i32, _vp, _c_i64, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i64,
+                                          _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
     "v1_stage_tail_published": (_c_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                          _c_i32, _c_i64, _c_i64, _vp]),
     "v1_stage_union": (_c_i32, [_vp, _c_i64, _vp, _c_i32, _vp, _c_i32, _vp, _vp, _c_i32, _vp, _vp, _c_i32,

@@ -239,6 +239,56 @@ __global__ __launch_bounds__(256) void union_map_topk_kernel(const void* __restr
     slots[at] = valid ? nt[logical / 64] * 64 + logical % 64 : -1;
 }
 
+// Split scoring of the shared chunk: every row scored once against all history
+// pages (hist_scores [rows, >= 64 * hist_pages], position = page * 64 + slot)
+// and once against the union in its own coordinates (union_scores
+// [rows, >= span], union position = up * 64 + slot with up = lp for sink
+// pages, sp + lp - tp for tail pages: union.py:33-35).  union_spans gives each
+// row's span there (the end of its last candidate) for the shared-table
+// scoring; normalize_split gathers the canonical candidate order from the two.
+__global__ __launch_bounds__(256) void union_spans_kernel(const int32_t* __restrict__ lens,
+                                                          const int32_t* __restrict__ indexed_end,
+                                                          const int32_t* __restrict__ desc, int32_t* __restrict__ spans,
+                                                          int32_t rows, int32_t S, int32_t W) {
+    const int32_t r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= rows) return;
+    const int32_t n = lens[r];
+    const UnionBounds x = union_bounds(n, *indexed_end, S, W);
+    const int32_t sp = desc[0], tp = desc[1], total = desc[3];
+    const int32_t span = x.t < n ? sp * 64 + n - tp * 64 : x.s;
+    spans[r] = max(1, min(max(span, x.s), total * 64));
+}
+
+__global__ __launch_bounds__(256) void union_normalize_split_kernel(
+    const float* __restrict__ hist, int64_t hist_stride, int32_t hist_cols, const float* __restrict__ uni,
+    int64_t uni_stride, int32_t uni_cols, const int32_t* __restrict__ lens, const int32_t* __restrict__ indexed_end,
+    const int32_t* __restrict__ takes, const int32_t* __restrict__ selected, const int32_t* __restrict__ members,
+    int64_t members_pages, const int32_t* __restrict__ desc, float* __restrict__ out, int32_t max_take, int32_t width,
+    int32_t S, int32_t W) {
+    const int64_t r = blockIdx.y;
+    const int32_t j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= width) return;
+    const int32_t n = lens[r], end = *indexed_end, take = takes[r];
+    const UnionBounds x = union_bounds(n, end, S, W);
+    const int32_t hist_n = take * 64;
+    float v = -__builtin_inff();
+    if (j < hist_n) {
+        const int32_t pi = j / 64;
+        const int64_t page = pi < max_take ? selected[r * max_take + pi] : -1;
+        const int32_t member = (page >= 0 && page < members_pages) ? members[page * 64 + j % 64] : -1;
+        const int64_t pos = page * 64 + j % 64;
+        if (member >= x.s && member < x.t && member < n && member < end && pos < hist_cols)
+            v = hist[r * hist_stride + pos];
+    } else if (j - hist_n < x.c) {
+        const int32_t k = j - hist_n;
+        const int32_t logical = k < x.s ? k : x.t + k - x.s;
+        const int32_t lp = logical / 64, sp = desc[0], tp = desc[1];
+        const int64_t pos = (int64_t)(lp < sp ? lp : sp + lp - tp) * 64 + logical % 64;
+        if (pos >= 0 && pos < uni_cols) v = uni[r * uni_stride + pos];
+    }
+    out[r * width + j] = v;
+}
+
 }  // namespace
 }  // namespace v1
 
@@ -300,4 +350,28 @@ extern "C" int v1_union_map_topk(const void* ids, int32_t ids_bits, const float*
                        lens, indexed_end, takes, selected,
                        members, members_pages, nt, nt_len, logical, slots, max_take, top, sink, window);
     return V1_LAUNCHED("map_topk");
+}
+
+extern "C" int v1_union_spans(const int32_t* lens, const int32_t* indexed_end, const int32_t* desc, int32_t* spans,
+                              int32_t rows, int32_t sink, int32_t window, void* stream) {
+    V1_REQUIRE(rows >= 0 && sink >= 0 && window >= 0, "union_spans: bad shape");
+    if (rows == 0) return V1_OK;
+    hipLaunchKernelGGL(union_spans_kernel, dim3((uint32_t)cdiv(rows, 256)), dim3(256), 0, as_stream(stream), lens,
+                       indexed_end, desc, spans, rows, sink, window);
+    return V1_LAUNCHED("union_spans");
+}
+
+extern "C" int v1_union_normalize_split(const float* hist, int64_t hist_stride, int32_t hist_cols, const float* uni,
+                                        int64_t uni_stride, int32_t uni_cols, const int32_t* lens,
+                                        const int32_t* indexed_end, const int32_t* takes, const int32_t* selected,
+                                        const int32_t* members, int64_t members_pages, const int32_t* desc, float* out,
+                                        int32_t rows, int32_t max_take, int32_t width, int32_t sink, int32_t window,
+                                        void* stream) {
+    V1_REQUIRE(rows >= 0 && width >= 0 && hist_cols >= 0 && uni_cols >= 0 && max_take >= 0,
+               "normalize_split: bad shape");
+    if (rows == 0 || width == 0) return V1_OK;
+    hipLaunchKernelGGL(union_normalize_split_kernel, dim3((uint32_t)cdiv(width, 256), (uint32_t)rows), dim3(256), 0,
+                       as_stream(stream), hist, hist_stride, hist_cols, uni, uni_stride, uni_cols, lens, indexed_end,
+                       takes, selected, members, members_pages, desc, out, max_take, width, sink, window);
+    return V1_LAUNCHED("normalize_split");
 }

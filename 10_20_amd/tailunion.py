@@ -173,3 +173,36 @@ tables = _Kernel("tables", _tables)
 normalize = _Kernel("normalize", _normalize)
 map_topk = _Kernel("map_topk", _map_topk)
 stage_tail_shared = _Kernel("stage_tail_shared", _stage_tail_shared)
+
+
+def union_spans(lens, indexed_end, desc, spans, sink, window):
+    """Each row's span in union coordinates (the end of its last candidate):
+    the context length for scoring every row against the union pages with one
+    shared table (stride-0 page table, see normalize_split)."""
+    _lib.require_gpu(lens, indexed_end, desc, spans)
+    _i32(lens, indexed_end, desc, spans)
+    _lib.call("v1_union_spans", _lib.ptr(lens), _lib.ptr(indexed_end), _lib.ptr(desc), _lib.ptr(spans), lens.numel(),
+              int(sink), int(window), _lib.stream_of(spans))
+    return spans
+
+
+def normalize_split(hist, uni, lens, indexed_end, takes, selected, members, desc, out, max_take, width, sink,
+                    window):
+    """normalize's canonical candidate order from two shared-table scorings:
+    hist [rows, >= 64 * history pages] (every row against every history page,
+    position page * 64 + slot) and uni [rows, >= span] (every row against the
+    union pages in union coordinates).  Same masks and order as normalize."""
+    _lib.require_gpu(hist, uni, lens, indexed_end, takes, selected, members, desc, out)
+    _i32(lens, indexed_end, takes, selected, members, desc)
+    for t in (hist, uni):
+        if t.dtype != torch.float32 or t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError("normalize_split: score arrays must be float32 [rows, cols] with unit inner stride")
+    if out.dtype != torch.float32 or not out.is_contiguous() or out.numel() < lens.numel() * int(width):
+        raise ValueError("normalize_split: out must be contiguous float32 [rows, width]")
+    rows = lens.numel()
+    _lib.call("v1_union_normalize_split", _lib.ptr(hist), hist.stride(0), hist.shape[1], _lib.ptr(uni), uni.stride(0),
+              uni.shape[1], _lib.ptr(lens), _lib.ptr(indexed_end), _lib.ptr(takes), _lib.ptr(selected),
+              _lib.ptr(members), members.numel() // 64, _lib.ptr(desc), _lib.ptr(out), rows, int(max_take),
+              int(width), int(sink), int(window), _lib.stream_of(out))
+    return out
+

@@ -506,12 +506,35 @@ def setup_union(P, dev, torch, np):
         qps, n, threads = cpu_baseline.union_queries_per_second(a, prm, budget)
         return qps, threads, f"{n} of {rows} queries (candidates, score, Top-2048, slot map)"
 
+    # split scoring: every row once against the 64 history pages and once against the union, both
+    # with one shared page table (the MFMA kernel that stages pages in LDS), then normalize_split
+    hist_tab = torch.arange(cap, device=dev, dtype=torch.int32)[None].expand(rows, -1)
+    uni_tab = (cap + torch.arange(union_cap, device=dev, dtype=torch.int32))[None].expand(rows, -1)
+    hist_s = torch.empty((rows, cap * 64), device=dev)
+    uni_s = torch.empty((rows, union_cap * 64), device=dev)
+    spans = torch.empty(rows, device=dev, dtype=torch.int32)
+    full = torch.full((rows,), cap * 64, device=dev, dtype=torch.int32)
+
+    def chain_split():
+        plan()
+        TU.union_spans(d["lens"], d_end, desc, spans, S, W)
+        P.scoring.fp8_paged_mqa_logits(q, fine4, d["w"], full, hist_tab, None, cap * 64, clean_logits=False,
+                                       out=hist_s)
+        P.scoring.fp8_paged_mqa_logits(q, fine4, d["w"], spans, uni_tab, None, union_cap * 64, clean_logits=False,
+                                       out=uni_s)
+        TU.normalize_split(hist_s, uni_s, d["lens"], d_end, d["takes"], d["selected"], d["members"], desc, scores,
+                           mt, width, S, W)
+        select()
+
     meta = {"workload": f"shared sink+tail chunk: {prm['history']} published tokens, {rows} causal queries x "
                         f"{heads} FP8 heads, sink {S} / window {W}, {mt} history pages per query, one union of "
                         f"sink+tail pages in the fine pool -> FP8 score -> canonical order -> Top-{T} -> slots",
             "global_batch": rows, "seq_len": width, "parallelism": "single GPU",
             "_extra": [("prepare_per_row", prepare_per_row,
-                        (lambda: (8448.0 * 2 * rows * scratch) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"))]}
+                        (lambda: (8448.0 * 2 * rows * scratch) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm")),
+                       ("chain_split_scoring", chain_split,
+                        (lambda: 2.0 * heads * 128 * (cap * 64 * rows + float(spans.sum())) / 1e12, "TFLOP/s",
+                         PEAK_FP8_TFLOPS, "mfma"))]}
     return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 7)"
 
 

@@ -384,6 +384,21 @@ int v1_expand_logical(const int32_t* logical, int32_t* out, int32_t rows, int32_
  * rows' sink and tail pages once into dst (pages past its capacity are not
  * copied), writes meta [rows, 3] = (s, t, count) and desc = (sp, tp, ep, total).
  * ---------------------------------------------------------------------- */
+/* Split scoring of the shared chunk (no counterpart call in the reference: its
+ * scores come from per-row tables, kernels.py:13-59; these give the same
+ * canonical candidate vector from two shared-table scorings): union_spans
+ * writes each row's span in union coordinates (positions up * 64 + slot,
+ * up = lp for sink pages and sp + lp - tp for tail pages); normalize_split
+ * builds the canonical scores from hist [rows, >= 64 * history pages]
+ * (position page * 64 + slot) and uni [rows, >= span], with normalize's masks. */
+int v1_union_spans(const int32_t* lens, const int32_t* indexed_end, const int32_t* desc, int32_t* spans,
+                   int32_t rows, int32_t sink, int32_t window, void* stream);
+int v1_union_normalize_split(const float* hist, int64_t hist_stride, int32_t hist_cols, const float* uni,
+                             int64_t uni_stride, int32_t uni_cols, const int32_t* lens,
+                             const int32_t* indexed_end, const int32_t* takes, const int32_t* selected,
+                             const int32_t* members, int64_t members_pages, const int32_t* desc, float* out,
+                             int32_t rows, int32_t max_take, int32_t width, int32_t sink, int32_t window,
+                             void* stream);
 int v1_stage_tail_published(const uint8_t* native, const int32_t* nt, const int32_t* lens,
                             const int32_t* indexed_end, uint8_t* fine, const int32_t* tail_rows,
                             int32_t rows, int32_t capacity, int32_t np, int32_t scratch, int32_t sink,

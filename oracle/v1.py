@@ -879,3 +879,30 @@ def decode_attention(q, k, v, scale, seqlens=None):
             p = np.exp(s - s.max())
             out[b, h] = (p / p.sum()) @ v[b, :n, h // G]
     return out
+
+
+def union_normalize_split(hist, uni, lens, end, takes, selected, members, desc, width, S, W):
+    """Canonical scores from split scoring: history candidate j of row r reads
+    hist[r, page * 64 + slot] (page = selected[r, j // 64]); tail candidate
+    reads uni[r, up * 64 + slot] in union coordinates (up = lp < sp ? lp :
+    sp + lp - tp, union.py:33-35); masks as union_normalize."""
+    rows = len(lens)
+    out = np.full((rows, width), NEG_INF, np.float32)
+    sp, tp = int(desc[0]), int(desc[1])
+    for r in range(rows):
+        n, take = int(lens[r]), int(takes[r])
+        s, t, c = union_bounds(n, end, S, W)
+        for j in range(width):
+            if j < take * 64:
+                page = int(selected[r, j // 64])
+                m = int(members[page, j % 64])
+                if s <= m < t and m < n and m < end:
+                    out[r, j] = hist[r, page * 64 + j % 64]
+            elif j - take * 64 < c:
+                x = j - take * 64
+                lg = x if x < s else t + x - s
+                lp = lg // 64
+                up = lp if lp < sp else sp + lp - tp
+                out[r, j] = uni[r, up * 64 + lg % 64]
+    return out
+

@@ -351,3 +351,57 @@ def test_stage_union_published_end_outside_lengths(end):
     c = Case(3000, 70, 17, 100, end)
     c.plan()
     c.check(end, c.nt)
+
+
+@pytest.mark.parametrize("case", [(65536, 300, 64, 2048, 61001), (5000, 64, 64, 200, 5000)])
+def test_spans_and_normalize_split_vs_oracle(case):
+    h, rows, S, W, end = case
+    f = _tables_inputs(h, rows, S, W, end, 40, h + rows)
+    lens = f["lens"]
+    desc = np.array(O.union_pages(lens, end, S, W), np.int32)
+    d_end, d_desc = T(np.int32([end])), T(desc)
+    spans = torch.empty(rows, device=DEV, dtype=torch.int32)
+    TU.union_spans(T(lens), d_end, d_desc, spans, S, W)
+    sp, tp, total = int(desc[0]), int(desc[1]), int(desc[3])
+    for r, n in enumerate(lens):
+        s, t, c = O.union_bounds(int(n), end, S, W)
+        # the last candidate sits at union position sp*64 + n - tp*64 - 1 (or s - 1: sink only)
+        want = max(1, min(max(sp * 64 + int(n) - tp * 64 if t < n else s, s), total * 64))
+        assert int(spans[r]) == want
+    g = np.random.default_rng(rows)
+    hist = g.standard_normal((rows, 64 * 64 + 8)).astype(np.float32)
+    uni = g.standard_normal((rows, total * 64 + 4)).astype(np.float32)
+    out = torch.full((rows, f["width"]), 3.0, device=DEV)
+    TU.normalize_split(T(hist)[:, :4096], T(uni)[:, :total * 64], T(lens), d_end, T(f["takes"]), T(f["selected"]),
+                       T(f["members"]), d_desc, out, f["max_take"], f["width"], S, W)
+    e = O.union_normalize_split(hist[:, :4096], uni[:, :total * 64], lens, end, f["takes"], f["selected"],
+                                f["members"], desc, f["width"], S, W)
+    assert np.array_equal(H(out), e)
+
+
+def test_split_scoring_chain_matches_per_row_tables():
+    # every row scored once against all 64 history pages and once against the union (two shared-table
+    # scorings) gives the canonical scores of the per-row-table chain, to the score tolerance
+    h, rows, S, W, end = 65536, 512, 64, 2048, 65536
+    b = Chain(h, rows, S, W, end, 40, True)
+    b.run()
+    cap = b.cap
+    total = int(b.desc[3])
+    ucap = b.fine.shape[0] - cap
+    hist_tab = torch.arange(64, device=DEV, dtype=torch.int32)[None].expand(rows, -1)
+    uni_tab = (cap + torch.arange(ucap, device=DEV, dtype=torch.int32))[None].expand(rows, -1)
+    hist = torch.empty((rows, 4096), device=DEV)
+    uni = torch.empty((rows, ucap * 64), device=DEV)
+    spans = torch.empty(rows, device=DEV, dtype=torch.int32)
+    full = torch.full((rows,), 4096, device=DEV, dtype=torch.int32)
+    fine4 = b.fine.view(-1, 64, 1, 132)
+    SC.fp8_paged_mqa_logits(b.q, fine4, b.w, full, hist_tab, None, 4096, clean_logits=False, out=hist)
+    TU.union_spans(b.d_lens, b.d_end, b.desc, spans, S, W)
+    SC.fp8_paged_mqa_logits(b.q, fine4, b.w, spans, uni_tab, None, ucap * 64, clean_logits=False, out=uni)
+    out = torch.empty_like(b.scores)
+    TU.normalize_split(hist, uni[:, :total * 64], b.d_lens, b.d_end, b.d_takes, b.d_sel, b.d_mem, b.desc, out,
+                       b.max_take, b.width, S, W)
+    got, ref = H(out), H(b.scores)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), fin)
+    assert (np.abs(got[fin] - ref[fin]) <= 1e-2 * np.abs(ref[fin]) + 1e-3).all()

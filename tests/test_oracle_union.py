@@ -186,3 +186,21 @@ def test_map_topk_positions_and_slots():
                 assert logical[r, i] == lg and slots[r, i] == f["nt"][lg // 64] * 64 + lg % 64
         good = logical[r][logical[r] >= 0]
         assert len(np.unique(good)) == len(good)
+
+
+@pytest.mark.parametrize("case", [(4096, 24, 64, 256, 3500), (5000, 16, 64, 200, 5000)])
+def test_split_scoring_restores_the_same_canonical_scores(case):
+    # every row scored once against all history pages and once against the union in union
+    # coordinates: normalize_split gives the canonical vector normalize gives from per-row tables
+    h, rows, S, W, end = case
+    f = _fixture(h, rows, S, W, end, 8, h + rows)
+    b, _, _, fine = _arm(f, end, S, W, True)
+    desc = np.array(O.union_pages(f["lens"], end, S, W), np.int32)
+    total = int(desc[3])
+    cap = f["cap"]
+    score = _content_score(fine)
+    hist = np.repeat(score[:cap].reshape(1, -1), rows, 0)
+    uni = np.repeat(score[cap:cap + total].reshape(1, -1), rows, 0)
+    split = O.union_normalize_split(hist, uni, f["lens"], end, f["takes"], f["selected"], f["members"], desc,
+                                    f["width"], S, W)
+    assert np.array_equal(split, b)
