@@ -16,13 +16,26 @@ import torch
 from . import _lib
 
 
-def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None, softmax_scale=None,
-                            causal=False, out=None, **unsupported):
-    if k is not None or v is not None:
-        raise NotImplementedError("flash_attn_with_kvcache: appending k / v to the cache is not supported")
-    bad = {key: val for key, val in unsupported.items() if val not in (None, False, 0, (-1, -1), 0.0)}
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,
+                            cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None, block_table=None,
+                            softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                            rotary_interleaved=True, alibi_slopes=None, num_splits=0, return_softmax_lse=False,
+                            out=None):
+    """FA3's keyword interface; `num_splits` only tunes FA3's launch and is
+    ignored, `rotary_interleaved` has no effect without rotary tables; the
+    options that change the result and are not implemented here raise."""
+    unsupported = {"k": k, "v": v, "rotary_cos": rotary_cos, "rotary_sin": rotary_sin,
+                   "cache_batch_idx": cache_batch_idx, "cache_leftpad": cache_leftpad, "block_table": block_table,
+                   "alibi_slopes": alibi_slopes}
+    bad = sorted(name for name, val in unsupported.items() if val is not None)
+    if tuple(window_size) != (-1, -1):
+        bad.append("window_size")
+    if softcap:
+        bad.append("softcap")
+    if return_softmax_lse:
+        bad.append("return_softmax_lse")
     if bad:
-        raise NotImplementedError(f"flash_attn_with_kvcache: unsupported options {sorted(bad)}")
+        raise NotImplementedError(f"flash_attn_with_kvcache: unsupported options {bad}")
     _lib.require_gpu(q, k_cache, v_cache, cache_seqlens, out)
     if q.dim() != 4 or q.shape[1] != 1:
         raise ValueError("q must be [batch, 1, heads, 128] (one query position per row)")

@@ -48,3 +48,19 @@ def test_key_order_linearity_and_shift():
     shifted = k2.copy()
     shifted[..., -1] = 5.0  # every score of every head rises by 5 * scale
     assert np.allclose(O.decode_attention(q2, shifted, v, 0.088), O.decode_attention(q2, k2, v, 0.088))
+
+
+def test_wrapper_rejects_options_it_does_not_implement():
+    # host logic only (the checks run before any device call)
+    import importlib
+    import pytest
+    import torch
+    A = importlib.import_module("10_20_amd.attention")
+    q = torch.zeros((1, 1, 4, 128), dtype=torch.bfloat16)
+    kv = torch.zeros((1, 8, 1, 128), dtype=torch.bfloat16)
+    for kw in ({"window_size": (64, 0)}, {"softcap": 30.0}, {"block_table": kv}, {"return_softmax_lse": True},
+               {"k": kv}):
+        with pytest.raises(NotImplementedError):
+            A.flash_attn_with_kvcache(q, kv, kv, **kw)
+    with pytest.raises(ValueError):  # host tensors: the operator needs the GPU
+        A.flash_attn_with_kvcache(q, kv, kv, rotary_interleaved=True, num_splits=4)
