@@ -264,29 +264,43 @@ __global__ __launch_bounds__(256) void union_normalize_split_kernel(
     int64_t uni_stride, int32_t uni_cols, const int32_t* __restrict__ lens, const int32_t* __restrict__ indexed_end,
     const int32_t* __restrict__ takes, const int32_t* __restrict__ selected, const int32_t* __restrict__ members,
     int64_t members_pages, const int32_t* __restrict__ desc, float* __restrict__ out, int32_t max_take, int32_t width,
-    int32_t S, int32_t W) {
+    int32_t S, int32_t W, int32_t vec) {
+    // four consecutive candidates per thread (one 16-byte store when the row allows it)
     const int64_t r = blockIdx.y;
-    const int32_t j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= width) return;
+    const int32_t j0 = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (j0 >= width) return;
     const int32_t n = lens[r], end = *indexed_end, take = takes[r];
     const UnionBounds x = union_bounds(n, end, S, W);
-    const int32_t hist_n = take * 64;
-    float v = -__builtin_inff();
-    if (j < hist_n) {
-        const int32_t pi = j / 64;
-        const int64_t page = pi < max_take ? selected[r * max_take + pi] : -1;
-        const int32_t member = (page >= 0 && page < members_pages) ? members[page * 64 + j % 64] : -1;
-        const int64_t pos = page * 64 + j % 64;
-        if (member >= x.s && member < x.t && member < n && member < end && pos < hist_cols)
-            v = hist[r * hist_stride + pos];
-    } else if (j - hist_n < x.c) {
-        const int32_t k = j - hist_n;
-        const int32_t logical = k < x.s ? k : x.t + k - x.s;
-        const int32_t lp = logical / 64, sp = desc[0], tp = desc[1];
-        const int64_t pos = (int64_t)(lp < sp ? lp : sp + lp - tp) * 64 + logical % 64;
-        if (pos >= 0 && pos < uni_cols) v = uni[r * uni_stride + pos];
+    const int32_t hist_n = take * 64, sp = desc[0], tp = desc[1];
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int32_t j = j0 + q;
+        v[q] = -__builtin_inff();
+        if (j >= width) continue;
+        if (j < hist_n) {
+            const int32_t pi = j / 64;
+            const int64_t page = pi < max_take ? selected[r * max_take + pi] : -1;
+            const int32_t member = (page >= 0 && page < members_pages) ? members[page * 64 + j % 64] : -1;
+            const int64_t pos = page * 64 + j % 64;
+            if (member >= x.s && member < x.t && member < n && member < end && pos < hist_cols)
+                v[q] = hist[r * hist_stride + pos];
+        } else if (j - hist_n < x.c) {
+            const int32_t k = j - hist_n;
+            const int32_t logical = k < x.s ? k : x.t + k - x.s;
+            const int32_t lp = logical / 64;
+            const int64_t pos = (int64_t)(lp < sp ? lp : sp + lp - tp) * 64 + logical % 64;
+            if (pos >= 0 && pos < uni_cols) v[q] = uni[r * uni_stride + pos];
+        }
     }
-    out[r * width + j] = v;
+    float* dst = out + r * width + j0;
+    if (vec) {
+        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (j0 + q < width) dst[q] = v[q];
+    }
 }
 
 }  // namespace
@@ -370,8 +384,10 @@ extern "C" int v1_union_normalize_split(const float* hist, int64_t hist_stride, 
     V1_REQUIRE(rows >= 0 && width >= 0 && hist_cols >= 0 && uni_cols >= 0 && max_take >= 0,
                "normalize_split: bad shape");
     if (rows == 0 || width == 0) return V1_OK;
-    hipLaunchKernelGGL(union_normalize_split_kernel, dim3((uint32_t)cdiv(width, 256), (uint32_t)rows), dim3(256), 0,
-                       as_stream(stream), hist, hist_stride, hist_cols, uni, uni_stride, uni_cols, lens, indexed_end,
-                       takes, selected, members, members_pages, desc, out, max_take, width, sink, window);
+    const int32_t vec = (width % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(union_normalize_split_kernel, dim3((uint32_t)cdiv(cdiv(width, 4), 256), (uint32_t)rows),
+                       dim3(256), 0, as_stream(stream), hist, hist_stride, hist_cols, uni, uni_stride, uni_cols, lens,
+                       indexed_end, takes, selected, members, members_pages, desc, out, max_take, width, sink, window,
+                       vec);
     return V1_LAUNCHED("normalize_split");
 }
