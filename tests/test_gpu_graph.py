@@ -1,0 +1,65 @@
+"""The entry points are stream-ordered and allocate nothing per call, so a
+chain of them captures into one HIP graph: the decode chain (FP8 scoring with
+per-row tables -> Top-2048 transform -> 656-byte row gather) captured once and
+replayed with new queries and lengths written in place, every replay equal bit
+for bit to the same chain run eagerly."""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SC = importlib.import_module("10_20_amd.scoring")
+TK = importlib.import_module("10_20_amd.topk")
+NK = importlib.import_module("10_20_amd.native_kernels")
+W = importlib.import_module("10_20_amd.workloads")
+DEV = "cuda:0"
+
+
+def test_decode_chain_replays_in_a_hip_graph():
+    g = np.random.default_rng(31)
+    rows, heads, pool_pages, max_ctx = 16, 64, 512, 20000
+    k8, ks = W.quantize_rows(g.standard_normal((pool_pages * 64, 128)).astype(np.float32))
+    native = torch.from_numpy(W.pack_pages(k8, ks)).to(DEV)
+    pages = -(-max_ctx // 64)
+    table = torch.from_numpy(np.stack([g.permutation(pool_pages)[:pages] for _ in range(rows)]).astype(np.int32)).to(DEV)
+    latent = torch.from_numpy(g.integers(0, 256, (pool_pages * 64, 656), dtype=np.uint8)).to(DEV)
+    q = torch.empty((rows, heads, 128), device=DEV, dtype=torch.uint8)
+    w = torch.empty((rows, heads), device=DEV)
+    lens = torch.empty(rows, device=DEV, dtype=torch.int32)
+    logits = torch.empty((rows, max_ctx), device=DEV)
+    slots = torch.empty((rows, 2048), device=DEV, dtype=torch.int32)
+    raw = torch.empty_like(slots)
+    work = torch.empty((rows, 2048, 656), device=DEV, dtype=torch.uint8)
+
+    def inputs(seed):
+        h = np.random.default_rng(seed)
+        q8, _ = W.quantize_rows(h.standard_normal((rows * heads, 128)).astype(np.float32))
+        q.copy_(torch.from_numpy(q8.reshape(rows, heads, 128)))
+        w.copy_(torch.from_numpy(h.random((rows, heads), dtype=np.float32)))
+        lens.copy_(torch.from_numpy(h.integers(1000, max_ctx + 1, rows).astype(np.int32)))
+
+    def chain():
+        SC.fp8_paged_mqa_logits(q.view(torch.float8_e4m3fn), native, w, lens, table, None, max_ctx,
+                                clean_logits=False, out=logits)
+        TK.topk_transform_512_v2(logits, lens, table, slots, 64, None, raw)
+        NK.gather_rows(latent, slots, work)
+
+    inputs(0)
+    chain()  # first calls size and cache the workspaces
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        chain()
+    for seed in (1, 2, 3):
+        inputs(seed)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (slots, raw, work)]
+        chain()
+        torch.cuda.synchronize()
+        for a, b in zip(got, (slots, raw, work)):
+            assert torch.equal(a, b)
+        assert int((raw >= 0).sum()) > 0
