@@ -63,3 +63,47 @@ def test_decode_chain_replays_in_a_hip_graph():
         for a, b in zip(got, (slots, raw, work)):
             assert torch.equal(a, b)
         assert int((raw >= 0).sum()) > 0
+
+
+def test_index_build_and_slot_attention_replay_in_a_hip_graph():
+    IB = importlib.import_module("10_20_amd.indexbuild")
+    AT = importlib.import_module("10_20_amd.attention")
+    g = np.random.default_rng(41)
+    k8, ks = W.quantize_rows(g.standard_normal((96 * 64, 128)).astype(np.float32))
+    pool = torch.from_numpy(W.pack_pages(k8, ks)).to(DEV)
+    tables = torch.empty((6, 16), device=DEV, dtype=torch.int32)
+    starts = torch.from_numpy((np.arange(6) * 1024).astype(np.int32)).to(DEV)
+    out = (torch.empty((6, 1024), device=DEV, dtype=torch.int32), torch.empty((6, 16, 8448), device=DEV, dtype=torch.uint8),
+           torch.empty((6, 16, 64), device=DEV, dtype=torch.int32), torch.empty((6, 2, 8448), device=DEV, dtype=torch.uint8))
+    gen = torch.Generator(device=DEV).manual_seed(41)
+    kp = torch.randn((5000, 2, 128), device=DEV, generator=gen).to(torch.bfloat16)
+    vp = torch.randn((5000, 2, 128), device=DEV, generator=gen).to(torch.bfloat16)
+    req = torch.randperm(5000, device=DEV, generator=gen).to(torch.int32)
+    ids = torch.empty((32, 2048), device=DEV, dtype=torch.int32)
+    qs = torch.randn((32, 4, 128), device=DEV, generator=gen).to(torch.bfloat16)
+    att = torch.empty((32, 1, 4, 128), device=DEV, dtype=torch.bfloat16)
+
+    def inputs(seed):
+        h = np.random.default_rng(seed)
+        tables.copy_(torch.from_numpy(h.permutation(96)[:96].reshape(6, 16).astype(np.int32)))
+        ids.copy_(torch.from_numpy(h.integers(-3, 5003, (32, 2048)).astype(np.int32)))
+
+    def work():
+        IB.build_buckets(pool, tables, starts, out=out)
+        AT.attend_slots(qs, kp, vp, req, ids, 1, softmax_scale=0.09, out=att)
+
+    inputs(0)
+    work()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        work()
+    for seed in (1, 2, 3):
+        inputs(seed)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (*out, att)]
+        work()
+        torch.cuda.synchronize()
+        for a, b in zip(got, (*out, att)):
+            assert torch.equal(a, b)
