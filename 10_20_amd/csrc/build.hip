@@ -276,7 +276,11 @@ __device__ __forceinline__ uint64_t bitonic_step(uint64_t key, int32_t p, uint64
     }
     const int32_t i = p & (N - 1);
     const bool take_max = ((i & J) == 0) == ((i & S) == 0);
-    return take_max ? (key > other ? key : other) : (key < other ? key : other);
+    // keys of a group are distinct, so one compare decides: keep the partner's
+    // key when it is the larger and this position keeps the maximum, or the
+    // smaller and it keeps the minimum
+    const bool other_gt = other > key;
+    return other_gt == take_max ? other : key;
 }
 
 template <int N, int S, int J>
