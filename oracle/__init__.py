@@ -2,8 +2,8 @@
 
 Plain numpy restatements of the reference algorithms, each citing the
 reference file:line it follows.  Only tests/, the smoke check and the CPU
-baseline leg of bench.py may import this package, and only as the checker:
-no product code path calls it.
+baseline leg of bench.py may import this package, and only to check results
+or time the host baseline: no product code path calls it.
 
 Pinning (what checks each function beyond its own text):
   fp8 decode          every code vs torch.float8_e4m3fn (tests/test_oracle_fp8.py)
@@ -20,4 +20,15 @@ Pinning (what checks each function beyond its own text):
   gather              reference KAT (test_gather_slots_small.py:26-64)
   score               fp32/fp64 dequantised formula; relu/weights/scale order checked
                       against hand-computed single-key cases
+  index build         reference KATs of _dots / _anchor (test_fused_grouping_small.py:57-86),
+                      the four-partial reduction order, unit vectors, RNE e4m3 vs torch,
+                      hierarchical clusters split exactly, float64 bisection where decided
+                      (tests/test_oracle_build.py)
+  shared tail union   the reference's 64K/4K answers (tail_union_lab README.md:54-63), the
+                      candidate-set rule, union = per-row staging byte for byte, one
+                      canonical order from shared / per-row / split scoring
+                      (tests/test_oracle_union.py)
+  expand_logical      hand KAT, int32 wrap, equal to fused_topk's expansion
+  decode_attention    closed forms: mean, one-hot, single key, key order, linearity, shift
+                      (tests/test_oracle_attention.py)
 """
