@@ -421,11 +421,11 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emi
     for (int e = 0; e < 4; ++e) key_stats(sk[e], smax, smin, scnt);
     if (t == 0) sm.ncand = 0;
     block_stats(smax, smin, scnt, sm);
-    // Pivot attempts: the first aims at 1.3 T candidates; after a miss the
+    // Pivot attempts: the first aims at 1.2 T candidates; after a miss the
     // target is corrected by the observed candidate count and the row is
     // streamed once more; a second miss takes the exact passes below.
     const int32_t steps = (n + 255) / 256;
-    float target = 1.3f;
+    float target = 1.2f;
     for (int attempt = 0; attempt < 2; ++attempt) {
         const uint32_t pivot = choose_pivot(sk, smax, smin, scnt, n, T, target, sm);
         stream_candidates(src, pivot, sm);
