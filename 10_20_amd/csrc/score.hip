@@ -65,6 +65,8 @@ struct ScoreParams {
     int32_t bulk;           // shared-table kernel: levels of full-size ranges (chunks [L*F, (L+1)*F))
     int32_t lvl_start[16];  // shared-table kernel: chunk range of each later level's items
     int32_t lvl_chunks[16];
+    uint32_t* exact_pages;  // shared-table ReLU path: per row, a bitmap of pages for score_exact
+    int32_t exact_words;    // 32-bit words per row of exact_pages (score_exact)
 };
 constexpr int kMaxLevels = 16;
 
@@ -81,22 +83,41 @@ constexpr int kPieces = 8;
 //   [0, 1024)     kPieces x 128 FP8 piece bytes
 //   [1024, 1056)  kPieces fp32 piece scales, times 1/2 (the linear-term factor)
 //   [1056, 1312)  64 fp32 head weights, times 1/2 on the ReLU path, zero past `heads`
+//   [1312, 1328)  fp32 exact-path threshold (see below), then padding
 // so the kernel reads everything with unconditional 16-byte loads.
 constexpr int kRecScales = kPieces * 128;
 constexpr int kRecWeights = kRecScales + kPieces * 4;
-constexpr int64_t kPieceRowBytes = kRecWeights + 64 * 4;
-static_assert(kRecWeights % 16 == 0 && kPieceRowBytes % 16 == 0, "16-byte aligned record fields");
+constexpr int kRecBound = kRecWeights + 64 * 4;
+constexpr int64_t kPieceRowBytes = kRecBound + 16;
+static_assert(kRecWeights % 16 == 0 && kRecBound % 16 == 0 && kPieceRowBytes % 16 == 0,
+              "16-byte aligned record fields");
+
+// Exact zeros.  The reference's sum of w * ReLU(x) is exactly 0 for a key
+// whose every head dot is <= 0 (kernels.py:310-313); the linear + |x| form
+// gives the difference of two separately rounded sums there instead.  Any FP8
+// key has |k_d| <= 448, so every head dot obeys |q_h . k| <= 448 ||q_h||_1 and
+// every fp32 rounding of the fast form (the pieces' and head MFMAs'
+// 128-product sums, the head folds) is at most ~2^-15 of
+//   B = 448 * sum_h |w_h| ||q_h||_1.
+// A key whose fast value lies within kExactFrac * B of zero (eight times that
+// worst case) is therefore recomputed the direct way, sum_h w_h * max(x_h, 0)
+// in fp32, which is exactly 0 when no head dot is positive.  Keys of many
+// heads with unrelated signs are never that close to zero; few live heads put
+// about 2^-H of the keys on the exact path.
+constexpr float kExactFrac = 1.0f / 4096.0f;
 
 // One wave per query row: q' = sum_h w_h q_h split into its pieces, and the
 // record described above.
 __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float* w, int32_t rows, int32_t heads,
-                                                  int32_t relu, uint8_t* out, uint32_t* work) {
+                                                  int32_t relu, uint8_t* out, uint32_t* work, uint32_t* exact_pages,
+                                                  int32_t exact_words) {
     const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
     const int l = __lane_id();
     if (blockIdx.x == 0 && threadIdx.x == 0) *work = 0u;  // the work counter of score_shared
     if (row >= rows) return;
+    for (int k = l; k < exact_words; k += kWave) exact_pages[row * exact_words + k] = 0u;
     // lane l owns dims 2l, 2l+1
-    float a0 = 0.f, a1 = 0.f;
+    float a0 = 0.f, a1 = 0.f, bound = 0.f;
     for (int h0 = 0; h0 < heads; h0 += 16) {
         // 16 heads' loads in flight (indices clamped, weights of missing heads zeroed)
         float wh[16];
@@ -110,10 +131,14 @@ __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float*
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            a0 = fmaf(wh[j], e4m3_value(b[j] & 0xff), a0);
-            a1 = fmaf(wh[j], e4m3_value(b[j] >> 8), a1);
+            const float x0 = e4m3_value(b[j] & 0xff), x1 = e4m3_value(b[j] >> 8);
+            a0 = fmaf(wh[j], x0, a0);
+            a1 = fmaf(wh[j], x1, a1);
+            bound = fmaf(fabsf(wh[j]), fabsf(x0) + fabsf(x1), bound);
         }
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) bound += __shfl_xor(bound, off, kWave);
     uint8_t* dst = out + row * kPieceRowBytes;
     for (int pc = 0; pc < kPieces; ++pc) {
         float m = fmaxf(fabsf(a0), fabsf(a1));
@@ -133,6 +158,7 @@ __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float*
         a1 -= sc * e4m3_value(c1);
     }
     reinterpret_cast<float*>(dst + kRecWeights)[l] = l < heads ? (relu ? 0.5f : 1.f) * w[row * heads + l] : 0.f;
+    if (l < 4) reinterpret_cast<float*>(dst + kRecBound)[l] = l == 0 ? kExactFrac * 448.f * bound : 0.f;
 }
 
 // Prologue loads are issued unconditionally, from indices clamped into range,
@@ -289,6 +315,7 @@ __device__ __forceinline__ void dma4(const i32x4& rs, int32_t voff, uint32_t lds
 // and page ids are loaded once per item; each page's logits are stored from
 // registers as soon as they are computed.
 constexpr int kMaxRangePages = 256;
+constexpr int kMarkWords = kMaxRangePages / 32 + 1;  // an item's pages start at a multiple of 16
 
 template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
@@ -298,7 +325,13 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t st3[V1_PAGE_BYTES];
     __shared__ int32_t pids[kMaxRangePages];
     __shared__ int32_t item_sh;
+    // ReLU path: per query of the group, a bitmap of the item's pages that
+    // hold a key marked for the exact form (bit (page_begin % 32) + page);
+    // all zero between items.
+    __shared__ uint32_t marks[RELU ? kQueriesPerGroup * kMarkWords : 1];
     const int t = threadIdx.x, l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (RELU)
+        for (int i = t; i < kQueriesPerGroup * kMarkWords; i += kThreads) marks[i] = 0u;
   for (;;) {
     // every wave has finished the previous item (its LDS is free) when the
     // next one is drawn
@@ -340,6 +373,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // query i/2, and coef[i] is that piece's scale.
     static_assert(kQueriesPerWave == 2, "two queries per linear-term row block");
     float coef[4];
+    float exact_thr[kQueriesPerWave];
     v8i alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int q = 0; q < kQueriesPerWave; ++q) {
@@ -356,6 +390,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
             const float2 x = *reinterpret_cast<const float2*>(rec + kRecScales + 8 * (l >> 4));
             coef[2 * q] = x.x;
             coef[2 * q + 1] = x.y;
+            exact_thr[q] = *reinterpret_cast<const float*>(rec + kRecBound);  // the same for every lane
         }
     }
     if (RELU) {
@@ -478,15 +513,32 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // nothing to write (no page, a row past the end, a column past the
     // context without clean_logits) store to the sink.  The count of vector
     // memory operations per step is then fixed, which the page wait relies on.
+    // Keys whose fast ReLU value lies within the query's exact-path threshold
+    // of zero only mark their page here (a bit per query and page in LDS, set
+    // in a rarely taken scalar branch with no vector memory operation); the
+    // item's end hands the marks to score_exact.
     auto store = [&](int32_t pg, bool live, const float (&part)[kQueriesPerWave][4], float scale) {
 #pragma unroll
         for (int q = 0; q < kQueriesPerWave; ++q) {
-            const float out = reduce_scatter4(part[q]) * scale;
+            const float v = reduce_scatter4(part[q]);
             const int64_t row = row0 + wv * kQueriesPerWave + q;
             const int32_t j = (page_begin + pg) * 64 + l;
             const bool in = live & (row < p.rows) & (j < p.max_context_len) & ((j < ctx[q]) | (p.clean != 0));
             float* dst = in ? p.logits + row * p.logits_stride + j : p.sink + l;
-            *dst = j < ctx[q] ? out : -__builtin_huge_valf();
+            *dst = j < ctx[q] ? v * scale : -__builtin_huge_valf();
+            if (RELU) {
+                // (ballots of the bare compares stay scalar masks; the
+                // uniform conditions join on the scalar side)
+                const uint64_t near = __builtin_amdgcn_ballot_w64(fabsf(v) <= exact_thr[q]) &
+                                      __builtin_amdgcn_ballot_w64(j < ctx[q]);
+                if (near != 0ull && live && row < p.rows) {
+                    // (the empty asm keeps this block's address arithmetic
+                    // from being hoisted out of the loop into live registers)
+                    int32_t bit = (page_begin & 31) + pg;
+                    asm volatile("" : "+s"(bit));
+                    if (l == 0) atomicOr(&marks[(wv * kQueriesPerWave + q) * kMarkWords + (bit >> 5)], 1u << (bit & 31));
+                }
+            }
         }
     };
 
@@ -549,6 +601,9 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // placed inside it.  (It also covers the first pages.)
     __builtin_amdgcn_s_waitcnt(0);
     V1_PAGE_BARRIER(0);
+#pragma unroll
+    for (int q = 0; q < kQueriesPerWave; ++q)
+        exact_thr[q] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, exact_thr[q])));
     load_frag(st0, fa);
     for (int32_t i = 0; i < npages; i += kStages) {
         step(i, st0, st1, fa, fb, pa, pb);
@@ -562,6 +617,22 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     }
     V1_PAGE_BARRIER(0);  // the page buffers are reused by the next item
     fill_rest(npages);
+    // Marked pages go to the per-row page bitmap that score_exact reads (an
+    // OR per word that has a mark; the words are cleared for the next item).
+    // (The bitmaps sit 256 bytes past the sink, and their row length follows
+    // from max_context_len: no more kernel arguments stay live in the loop.)
+    int lane = l;
+    asm volatile("" : "+v"(lane));  // keeps the lane arithmetic below inside the loop
+    if (RELU && lane < kQueriesPerWave * kMarkWords) {
+        const int q = lane / kMarkWords, k = lane % kMarkWords;
+        const uint32_t bits = marks[(wv * kQueriesPerWave + q) * kMarkWords + k];
+        if (bits != 0u) {
+            const int32_t words = (((p.max_context_len + 63) >> 6) + 31) >> 5;
+            uint32_t* pages = reinterpret_cast<uint32_t*>(p.sink + 64);
+            atomicOr(pages + (row0 + wv * kQueriesPerWave + q) * words + (page_begin >> 5) + k, bits);
+            marks[(wv * kQueriesPerWave + q) * kMarkWords + k] = 0u;
+        }
+    }
   }
 }
 
@@ -651,6 +722,58 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
         for (int32_t pg = page_at(s); pg < all_pages; pg = page_at(++s)) store_logit(p, row, pg * 64 + l, ctx, 0.f);
 }
 
+// The marked pages of the shared-table ReLU kernel (one wave per row): each
+// page's 64 keys recomputed the direct way, sum_h w_h * max(x_h, 0) as in
+// score_rows, replacing the fast values (the stream order after score_shared
+// makes these stores the last ones).  A page past the table or out of the pool
+// scored exactly 0 already and is skipped.
+template <int HB>
+__global__ __launch_bounds__(256) void score_exact(ScoreParams p) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    const int l = __lane_id();
+    if (row >= p.rows) return;
+    const int32_t ctx = min(p.ctx[row], p.max_context_len);
+    bool loaded = false;
+    v8i a[HB];
+    float w[HB][4];
+    for (int32_t w0 = 0; w0 < p.exact_words; w0 += kWave) {
+        const uint32_t mine = w0 + l < p.exact_words ? p.exact_pages[row * p.exact_words + w0 + l] : 0u;
+        uint64_t words = __builtin_amdgcn_ballot_w64(mine != 0u);
+        while (words) {
+            const int src = __builtin_ctzll(words);
+            words &= words - 1;
+            uint32_t bits = (uint32_t)__builtin_amdgcn_readlane((int)mine, src);
+            if (!loaded) {
+                load_q<HB>(p, row, a);
+                load_w<HB>(p, row, w);
+                loaded = true;
+            }
+            while (bits) {
+                const int32_t pg = (w0 + src) * 32 + __builtin_ctz(bits);
+                bits &= bits - 1;
+                const int32_t page = __builtin_amdgcn_readfirstlane(page_of(p, row, pg));
+                if (page < 0) continue;
+                const uint8_t* kp = p.kv + (int64_t)page * V1_PAGE_BYTES;
+                v8i b[4];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    const u32x4* src4 = reinterpret_cast<const u32x4*>(kp + (kb * 16 + (l & 15)) * 128 + 32 * (l >> 4));
+                    const u32x4 x = src4[0], y = src4[1];
+                    b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+                }
+                const float scale = reinterpret_cast<const float*>(kp + 8192)[l];
+                float part[4];
+                page_partials<HB, true>(a, b, w, part);
+                // the lane exchanges of the fold need every lane: only the
+                // store is predicated
+                const float v = reduce_scatter4(part) * scale;
+                const int32_t j = pg * 64 + l;
+                if (j < ctx) p.logits[row * p.logits_stride + j] = v;
+            }
+        }
+    }
+}
+
 struct Shared {
     template <int HB, bool RELU>
     static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
@@ -688,7 +811,16 @@ void launch_hb(int hb, bool relu, dim3 g, hipStream_t st, const ScoreParams& p) 
 using namespace v1;
 
 // per-query records, the work counter (256 bytes), the store sink (256 bytes)
-extern "C" int64_t v1_score_workspace(int32_t rows) { return rows > 0 ? (int64_t)rows * kPieceRowBytes + 512 : 0; }
+// Shared-table layout: per-query records, the work counter (256 bytes), the
+// store sink (256 bytes), then (ReLU rule) the per-row bitmaps of pages that
+// score_exact recomputes.
+static int32_t exact_words(int32_t max_context_len) { return (int32_t)cdiv(cdiv(max_context_len, 64), 32); }
+static_assert(kPieceRowBytes % 16 == 0, "the bitmaps follow the sink at a fixed offset");
+
+extern "C" int64_t v1_score_workspace(int32_t rows, int32_t max_context_len) {
+    if (rows <= 0 || max_context_len < 0) return 0;
+    return (int64_t)rows * kPieceRowBytes + 512 + (int64_t)rows * exact_words(max_context_len) * 4;
+}
 
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
     V1_REQUIRE(a != nullptr, "score: null args");
@@ -706,18 +838,10 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
     const uint32_t chunks = (uint32_t)cdiv(cdiv(a->max_context_len, 64), kChunkPages);
     hipStream_t st = as_stream(stream);
     if (a->block_table_stride == 0) {
-        const int64_t need = v1_score_workspace(a->rows);
+        const int64_t need = v1_score_workspace(a->rows, a->max_context_len);
         V1_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= need, "score: workspace of %lld bytes required",
                    (long long)need);
         V1_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 15) == 0, "score: workspace must be 16-byte aligned");
-        uint8_t* ws = static_cast<uint8_t*>(a->workspace);
-        p.pieces = ws;
-        p.work = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes);
-        p.sink = reinterpret_cast<float*>(ws + (int64_t)a->rows * kPieceRowBytes + 256);
-        hipLaunchKernelGGL(score_prep, dim3((uint32_t)cdiv(a->rows, 4)), dim3(256), 0, st, a->q, a->weights, a->rows,
-                           a->heads, a->relu, ws, p.work);
-        const int rc = V1_LAUNCHED("score_prep");
-        if (rc != V1_OK) return rc;
         // Work items: each row group's chunks cut into ranges that halve in
         // size (at most kMaxRangePages pages), all groups' largest ranges
         // first; work-groups pull them in that order, so the last ones taken
@@ -741,8 +865,27 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         const int64_t items = groups * ((int64_t)p.bulk + nlevels);
         V1_REQUIRE(items < (1ll << 31) - (1ll << 20), "score: too many work items");
         p.items = (int32_t)items;
+        uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+        p.pieces = ws;
+        p.work = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes);
+        p.sink = reinterpret_cast<float*>(ws + (int64_t)a->rows * kPieceRowBytes + 256);
+        p.exact_pages = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes + 512);
+        p.exact_words = a->relu ? exact_words(a->max_context_len) : 0;
+        const dim3 row_waves((uint32_t)cdiv(a->rows, 4));
+        hipLaunchKernelGGL(score_prep, row_waves, dim3(256), 0, st, a->q, a->weights, a->rows, a->heads, a->relu, ws,
+                           p.work, p.exact_pages, p.exact_words);
+        int rc = V1_LAUNCHED("score_prep");
+        if (rc != V1_OK) return rc;
         launch_hb<Shared>(hb, a->relu != 0, dim3((uint32_t)std::min<int64_t>(items, wgs)), st, p);
-        return V1_LAUNCHED("score_shared");
+        rc = V1_LAUNCHED("score_shared");
+        if (rc != V1_OK || !a->relu) return rc;
+        switch (hb) {
+            case 1: hipLaunchKernelGGL(score_exact<1>, row_waves, dim3(256), 0, st, p); break;
+            case 2: hipLaunchKernelGGL(score_exact<2>, row_waves, dim3(256), 0, st, p); break;
+            case 3: hipLaunchKernelGGL(score_exact<3>, row_waves, dim3(256), 0, st, p); break;
+            default: hipLaunchKernelGGL(score_exact<4>, row_waves, dim3(256), 0, st, p); break;
+        }
+        return V1_LAUNCHED("score_exact");
     }
     // about 8 work-groups per CU in all, each striding over its row's chunks
     const int64_t per_row = std::max<int64_t>(1, std::min<int64_t>(chunks, cdiv(8 * (int64_t)v1::device_cus(), a->rows)));

@@ -53,7 +53,7 @@ def fp8_paged_mqa_logits(q, kv_cache, weights, context_lens, block_table, schedu
         out = torch.empty((rows, max_context_len), dtype=torch.float32, device=q.device)
     elif out.dtype != torch.float32 or out.shape[0] != rows or out.shape[1] < max_context_len or out.stride(1) != 1:
         raise ValueError("out must be float32 [rows, >= max_context_len]")
-    ws, ws_bytes = workspace(q.device, _lib.lib().v1_score_workspace(rows), "score")
+    ws, ws_bytes = workspace(q.device, _lib.lib().v1_score_workspace(rows, int(max_context_len)), "score")
     a = _lib.ScoreArgs(_lib.ptr(q), _lib.ptr(kv), kv.numel() // PAGE_BYTES, _lib.ptr(weights), _lib.ptr(lens),
                        _lib.ptr(block_table), block_table.stride(0), block_table.shape[1], _lib.ptr(out), out.stride(0),
                        int(max_context_len), rows, heads, int(bool(relu)), int(bool(clean_logits)), ws, ws_bytes)

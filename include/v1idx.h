@@ -166,10 +166,14 @@ typedef struct {
     int32_t heads;               /* 1..64 */
     int32_t relu;                /* 1: DSA ReLU rule; 0: signed scores */
     int32_t clean_logits;
-    void* workspace;             /* >= v1_score_workspace(rows) bytes */
+    void* workspace;             /* >= v1_score_workspace(rows, max_context_len) bytes (shared tables) */
     int64_t workspace_bytes;
 } v1_score_args;
-int64_t v1_score_workspace(int32_t rows);
+/* Workspace of the shared-table path: per-query records, a work counter and,
+ * for the ReLU rule, per-row bitmaps of pages rescored exactly (keys whose
+ * fast value is within rounding of zero get the direct ReLU sum, so keys with
+ * no positive head dot score exactly 0, as kernels.py:310-313 gives). */
+int64_t v1_score_workspace(int32_t rows, int32_t max_context_len);
 int v1_score(const v1_score_args* a, void* stream);
 
 /* ------------------------------------------------------------------------

@@ -82,7 +82,7 @@ def test_workspace_sizes_are_host_arithmetic(lib):
     assert h.v1_topk_workspace(4096, 32768, 2048) == 0       # large batch: one work-group per row
     assert h.v1_topk_workspace(4096, 65536, 2048) == 4096 * 2 * (2048 * 8 + 4)
     assert h.v1_topk_workspace(128, 131072, 2048) == 128 * 4 * (2048 * 8 + 4)
-    assert h.v1_score_workspace(4096) >= 4096 * (8 * 128 + 8 * 4)
+    assert h.v1_score_workspace(4096, 32768) >= 4096 * (8 * 128 + 8 * 4 + 16 * 4)
 
 
 def test_sort_rejects_bad_group_size(lib):
