@@ -72,10 +72,13 @@ __global__ __launch_bounds__(512) void route_kernel(v1_route_args a, int n_sort)
     }
     __syncthreads();
     bitonic_desc(s, n_sort, n_sort, U64Less{});
-    for (int r = threadIdx.x; r < a.take_stride; r += blockDim.x) {
+    // selected takes ranks < take_stride; the fine table every rank < take
+    // (v1_query.cuh:44-48), bounded by the sorted pages and the table width
+    const int32_t ft_ranks = a.fill_table ? min(min(take, a.pages), a.ft_cols) : 0;
+    for (int r = threadIdx.x; r < max(a.take_stride, ft_ranks); r += blockDim.x) {
         const int32_t p = (int32_t)(0xffffffffu - (uint32_t)s[r]);
-        selected[r] = (Index)p;
-        if (a.fill_table && r < take) ft[r] = rt[p];
+        if (r < a.take_stride) selected[r] = (Index)p;
+        if (r < ft_ranks) ft[r] = rt[p];
     }
 }
 

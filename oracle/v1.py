@@ -77,8 +77,8 @@ def route(scores, lens, takes, selected, pages, rt, ft, tail_rows, capacity, fil
             vals[:active] = np.fmax.reduce(scores[b, : 8 * active].reshape(active, 8), axis=1)
         order = top_order(vals, pages)
         selected[b, :] = order[:K]
-        if fill_table:
-            n = max(0, min(take, pages))
+        if fill_table:  # every rank < take (v1_query.cuh:44-48), within the table width
+            n = max(0, min(take, pages, ft.shape[1]))
             ft[b, :n] = rt[b, order[:n]]
 
 

@@ -167,7 +167,8 @@ def test_route_random_vs_oracle(dev, pages, bits):
     scores[g.random(scores.shape) < 0.02] = -np.inf
     lens = g.integers(1, pages * 64 + 2, B).astype(np.int32)
     K_ = min(pages, 48)
-    takes = g.integers(0, K_ + 1, B).astype(np.int32)
+    # takes past the selected width too: the fine table then takes every rank < take (v1_query.cuh:44-48)
+    takes = g.integers(0, K_ + 41, B).astype(np.int32)
     rt = g.integers(0, 10000, (B, pages)).astype(np.int32)
     tail = g.integers(0, 5, B).astype(np.int32)
     sel0 = np.full((B, K_), -7, np.int64 if bits == 64 else np.int32)
