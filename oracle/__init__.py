@@ -6,8 +6,9 @@ baseline leg of bench.py may import this package, and only to check results
 or time the host baseline: no product code path calls it.
 
 Pinning (what checks each function beyond its own text):
-  fp8 decode          every code vs torch.float8_e4m3fn (tests/test_oracle_fp8.py)
-  route               reference example known answer + brute force on small rows
+  fp8 decode          every code vs torch.float8_e4m3fn (tests/test_oracle.py)
+  route               reference example known answer + brute force on small rows;
+                      fine table over every rank < take (take > take_stride)
   topk_select         brute-force sort, tie/ -inf / ±0 special cases, L <= T rule
   fused_topk          reference example (mask, mapping, both direct_fine settings)
   transform_topk      closed form on identity / random tables
@@ -19,7 +20,9 @@ Pinning (what checks each function beyond its own text):
   query_metadata      closed form + tail-share KAT owners [0,0,2,2]
   gather              reference KAT (test_gather_slots_small.py:26-64)
   score               fp32/fp64 dequantised formula; relu/weights/scale order checked
-                      against hand-computed single-key cases
+                      against hand-computed single-key cases; the page/slot/scale
+                      addressing through per-row and shared block tables by one-hot
+                      keys with per-token scales, worked by hand and by lookup
   index build         reference KATs of _dots / _anchor (test_fused_grouping_small.py:57-86),
                       the four-partial reduction order, unit vectors, RNE e4m3 vs torch,
                       hierarchical clusters split exactly, float64 bisection where decided

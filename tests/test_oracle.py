@@ -326,6 +326,23 @@ def test_route_ties_to_lower_page_and_trivial_branch():
     assert ft[2, :6].tolist() == rt[2, :6].tolist() and ft[2, 6:].tolist() == [0, 0, 0, 0]
 
 
+def test_route_fine_table_takes_every_rank_below_take():
+    """Sorted branch with take > take_stride: selected keeps take_stride ranks,
+    the fine table every rank < take (v1_query.cuh:44-48), then the tail slots."""
+    P, K, W_ = 64, 6, 12
+    g = np.random.default_rng(3)
+    scores = np.full((1, 8 * P), -np.inf, np.float32)
+    scores[0, :8 * 32] = g.permutation(8 * 32).astype(np.float32)  # distinct page maxima
+    rt = (1000 + np.arange(P, dtype=np.int32))[None]
+    sel = np.zeros((1, K), np.int32)
+    ft = np.zeros((1, W_), np.int32)
+    O.route(scores, np.int32([2049]), np.int32([9]), sel, P, rt, ft, np.int32([2]), 500, True)
+    order = np.argsort(-scores[0, :256].reshape(32, 8).max(1), kind="stable")
+    assert sel[0].tolist() == order[:K].tolist()
+    assert ft[0, :9].tolist() == (1000 + order[:9]).tolist()
+    assert ft[0, 9:].tolist() == [500 + 2 * 68 + j for j in range(3)]
+
+
 # -------------------------------------------------------------- fused topk
 @pytest.fixture(scope="module")
 def example_after_route():
@@ -407,6 +424,62 @@ def test_score_formula_order_by_hand():
     assert np.isneginf(out[0, 1:]).all()
     signed = O.paged_logits(q8, w, native, np.int32([[0]]), np.int32([1]), 1, relu=False)
     assert signed[0, 0] == pytest.approx((0.5 * 2 - 7.0 * 3) * 0.25)
+
+
+def _onehot_pool():
+    """4 native pages whose token (page p, slot s) key is the unit vector at
+    dim (37 p + s) % 128 (FP8 1.0 = 0x38) with scale (1 + s/64) * 2^-p: every
+    token has its own dim pattern and scale, so reading a wrong token (page and
+    slot swapped, a wrong scale slot) changes the logit."""
+    native = np.zeros((4, 8448), np.uint8)
+    for p in range(4):
+        for s in range(64):
+            native[p, s * 128 + (37 * p + s) % 128] = 0x38
+            native[p, 8192 + 4 * s:8196 + 4 * s] = np.float32([(1 + s / 64) * 2.0 ** -p]).view(np.uint8)
+    return native
+
+
+def _onehot_queries():
+    """2 rows x 3 heads: q[r, h, d] = ((d + 5 h + 3 r) mod 9) - 4, exact in e4m3."""
+    q = np.array([[[((d + 5 * h + 3 * r) % 9) - 4 for d in range(128)] for h in range(3)] for r in range(2)],
+                 np.float32)
+    return W.e4m3_encode(q.reshape(-1)).reshape(2, 3, 128)
+
+
+def test_paged_logits_addressing_by_hand():
+    """sglang/srt/layers/attention/v1_deepseek/kernels.py:310-313 through
+    per-row permuted block tables: logit[r, j] = sum_h w[r,h] relu(q[r,h,d]) s
+    with (d, s) the dim and scale of token (table[r, j // 64], j % 64)."""
+    native = _onehot_pool()
+    q8 = _onehot_queries()
+    w = np.float32([[0.5, 1.5, 0.25], [2.0, -1.0, 0.75]])
+    table = np.int32([[2, 0, 3], [1, 3, 0]])
+    lens = np.int32([150, 130])
+    out = O.paged_logits(q8, w, native, table, lens, 192)
+    # worked by hand:
+    #  [0, 0]:   page 2 slot 0 -> d 74,  q0 = (-2, 3, -1) -> 1.5*3 = 4.5, s = 0.25   -> 1.125
+    #  [0, 70]:  page 0 slot 6 -> d 6,   q0 = (2, -2, 3) -> 0.5*2 + 0.25*3 = 1.75, s = 1.09375 -> 1.9140625
+    #  [0, 149]: page 3 slot 21 -> d 4,  q0 = (0, -4, 1) -> 0.25, s = 1.328125/8   -> 0.0415039...
+    #  [1, 129]: page 0 slot 1 -> d 1,   q1 = (0, -4, 1) -> 0.75, s = 1.015625     -> 0.76171875
+    #  [1, 64]:  page 3 slot 0 -> d 111, q1 = (2, -2, 3) -> 2*2 + 0.75*3 = 6.25, s = 0.125 -> 0.78125
+    #  [1, 5]:   page 1 slot 5 -> d 42,  q1 = (-4, 1, -3) -> -1*1 = -1, s = 1.078125/2 -> -0.5390625
+    assert out[0, 0] == 1.125 and out[0, 70] == 1.9140625 and out[1, 129] == 0.76171875
+    assert out[0, 149] == pytest.approx(0.25 * 1.328125 / 8, rel=1e-12)
+    assert out[1, 64] == 0.78125 and out[1, 5] == -0.5390625
+    assert np.isneginf(out[0, 150:]).all() and np.isneginf(out[1, 130:]).all()
+    # every column by lookup (no matmul): the dot with a one-hot key is one element of q
+    qf = O.e4m3_decode(q8).astype(np.float64)
+    for r in range(2):
+        for j in range(int(lens[r])):
+            p, s = int(table[r, j // 64]), j % 64
+            d, sc = (37 * p + s) % 128, (1 + s / 64) * 2.0 ** -p
+            assert out[r, j] == pytest.approx(sum(w[r, h] * max(qf[r, h, d], 0) for h in range(3)) * sc, rel=1e-12)
+    # signed rule, and one shared table (1-D) for both rows
+    signed = O.paged_logits(q8, w, native, table, lens, 192, relu=False)
+    assert signed[0, 0] == (0.5 * -2 + 1.5 * 3 + 0.25 * -1) * 0.25
+    shared = O.paged_logits(q8, w, native, table[0], lens, 192)
+    assert shared[1, 0] == pytest.approx((2.0 * max(qf[1, 0, 74], 0) - 1.0 * max(qf[1, 1, 74], 0)
+                                          + 0.75 * max(qf[1, 2, 74], 0)) * 0.25)
 
 
 # ------------------------------------------------- batched page manager
