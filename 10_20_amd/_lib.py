@@ -69,6 +69,8 @@ _SIGNATURES = {
     "v1_topk_transform": (_c_i32, [ctypes.POINTER(TopkTransformArgs), _vp]),
     "v1_score": (_c_i32, [ctypes.POINTER(ScoreArgs), _vp]),
     "v1_score_workspace": (_c_i64, [_c_i32, _c_i32]),
+    "v1_score_noalloc": (_c_i32, [ctypes.POINTER(ScoreArgs), _vp]),
+    "v1_score_noalloc_capacity": (_c_i64, []),
     "v1_gather_slots": (_c_i32, [_vp, _vp, _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32,
                                  _vp, _c_i64, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp]),
     "v1_gather_rows": (_c_i32, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i32, _vp, _c_i64, _c_i32,

@@ -20,6 +20,7 @@
 // and reused by 8 queries x 64 heads.  Rows with their own tables (decode) run one
 // query per work-group, each wave streaming whole pages straight from HBM.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -892,4 +893,65 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
     const dim3 grid((uint32_t)per_row, (uint32_t)a->rows);
     launch_hb<Rows>(hb, a->relu != 0, grid, st, p);
     return V1_LAUNCHED("score_rows");
+}
+
+// ------------------------------------------------ allocation-free variant
+// The shared-table path's scratch (per-query records, work counter, store
+// sink, exact-page bitmaps) in one static device array per GPU, for callers
+// that cannot allocate.  Every call on a GPU shares that GPU's array: calls
+// that overlap on one GPU race.  score_prep clears what must start at zero
+// (the work counter and the bitmaps) with a kernel at every call.
+constexpr int64_t kScratchBytes = 16ll << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+// Device address of this GPU's scratch: hipGetSymbolAddress once per device,
+// with that device current (the array's host-side name is not a device
+// address and is never passed to a kernel).
+int scratch_address(void* stream, void** out) {
+    int cur = 0, dev = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_status(e, "score_noalloc: hipGetDevice");
+    dev = cur;
+    if (stream != nullptr) {
+        e = hipStreamGetDevice(as_stream(stream), &dev);
+        if (e != hipSuccess) return hip_status(e, "score_noalloc: hipStreamGetDevice");
+    }
+    V1_REQUIRE(dev >= 0 && dev < 64, "score_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return hip_status(e, "score_noalloc: hipSetDevice");
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
+        if (e != hipSuccess) return hip_status(e, "score_noalloc: hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return V1_OK;
+}
+}  // namespace
+
+extern "C" int64_t v1_score_noalloc_capacity(void) { return kScratchBytes; }
+
+extern "C" int v1_score_noalloc(const v1_score_args* a, void* stream) {
+    V1_REQUIRE(a != nullptr, "score_noalloc: null args");
+    v1_score_args b = *a;
+    b.workspace = nullptr;
+    b.workspace_bytes = 0;
+    if (a->block_table_stride != 0) return v1_score(&b, stream);  // per-row tables use no scratch
+    const int64_t need = v1_score_workspace(a->rows, a->max_context_len);
+    V1_REQUIRE(need <= kScratchBytes,
+               "score_noalloc: %d rows x %d columns need %lld bytes of scratch, more than the static %lld "
+               "(call v1_score with a workspace)",
+               a->rows, a->max_context_len, (long long)need, (long long)kScratchBytes);
+    if (need > 0) {
+        const int rc = scratch_address(stream, &b.workspace);
+        if (rc != V1_OK) return rc;
+        b.workspace_bytes = kScratchBytes;
+    }
+    return v1_score(&b, stream);
 }

@@ -175,6 +175,16 @@ typedef struct {
  * no positive head dot score exactly 0, as kernels.py:310-313 gives). */
 int64_t v1_score_workspace(int32_t rows, int32_t max_context_len);
 int v1_score(const v1_score_args* a, void* stream);
+/* v1_score without a caller workspace and without any allocation: the
+ * shared-table path's scratch is a static 16 MiB device array per GPU
+ * (v1_score_noalloc_capacity() bytes), so rows * max_context_len must fit
+ * v1_score_workspace(rows, max_context_len) <= that, else V1_ERR_INVALID.
+ * a->workspace is ignored.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops).  Every call on a GPU shares that GPU's array, so calls that overlap
+ * on one GPU race; per-row tables need no scratch and do not touch it. */
+int64_t v1_score_noalloc_capacity(void);
+int v1_score_noalloc(const v1_score_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * _gather_slots: logical -> req[logical] -> K and V rows of one head into
