@@ -268,6 +268,72 @@ def config5(seed=5, rows=128, heads=64, pool_pages=32768, lo=4096, hi=131072):
                          max_ctx=int(ctx.max())))
 
 
+def config5_route(seed=5, rows=128, heads=64, pool_pages=32768, lo=4096, hi=131072, max_context=131072,
+                  topk=TOPK, num=1, den=2, sink=64, window=2048):
+    """The config5 decode batch (same contexts, native page tables, queries,
+    weights and native pool) through the V1 route path of
+    sglang/srt/layers/attention/v1_deepseek/runtime.py:417-634 for <= 512 rows:
+    center score -> fused route -> fine_table_shared -> stage_tail_shared ->
+    fine score -> mask_fine -> topk_transform_512_v2 -> output_ids -> gather,
+    with page_fraction num/den (runtime.py:25).
+
+    Each request carries a built index over its complete 1024-token buckets:
+    the bucket's tokens in a seeded member order, 16 route pages of 64 members
+    per bucket whose FP8 rows are copied into one shared fine pool (the
+    reordered table rt maps route page -> fine page through a seeded
+    permutation of the pool), and 8 FP8 centers per route page (the float32
+    mean of 8 consecutive members, power-of-two scaled).  The route covers
+    max_context / 64 pages; the fine pool holds every built page, then 68 tail
+    scratch pages per row (Config.width etc.: runtime.py:62-79)."""
+    base = config5(seed, rows, heads, pool_pages, lo, hi)
+    a = base.arrays
+    lens = a["lens"].astype(np.int32)
+    assert int(lens.max()) <= max_context and max_context % 4096 == 0
+    g = rng(seed + 500)
+    P = max_context // PAGE
+    take = min(P, max(-(-P * num // den), -(-topk // 64)))
+    width = -(-(take * 64 + 64 + 4096) // 256) * 256
+    nt = np.zeros((rows, P), np.int32)
+    nt[:, :a["table"].shape[1]] = a["table"]
+    built = np.maximum(lens.astype(np.int64) - 1, 0) // 1024 * 16
+    cap = int(built.sum())
+    fine_of = g.permutation(cap).astype(np.int32)
+    rt = np.zeros((rows, P), np.int32)
+    members = np.full((cap, 64), -1, np.int32)
+    fine = np.zeros((cap + rows * 68, PAGE_BYTES), np.uint8)
+    centers = np.zeros((max(cap // 8, 1), PAGE_BYTES), np.uint8)
+    ctab = np.zeros((rows, P // 8), np.int32)
+    nk = a["native"][:, :8192].reshape(pool_pages, PAGE, DIM)
+    ns = a["native"][:, 8192:].copy().view(np.float32).reshape(pool_pages, PAGE)
+    dec = decode_table()
+    fbase = cbase = 0
+    for r in range(rows):
+        pr = int(built[r])
+        if pr == 0:
+            continue
+        nb = pr // 16
+        order = (np.argsort(g.random((nb, 1024)), axis=1) + 1024 * np.arange(nb)[:, None]).reshape(-1)
+        ids = fine_of[fbase:fbase + pr]
+        rt[r, :pr] = ids
+        members[ids] = order.reshape(pr, 64)
+        kp, ks = nt[r, order // PAGE], order % PAGE
+        k8, sc = nk[kp, ks], ns[kp, ks]
+        fine[ids, :8192] = k8.reshape(pr, 8192)
+        fine[ids, 8192:] = sc.reshape(pr, PAGE).view(np.uint8)
+        mean = (dec[k8] * sc[:, None]).reshape(pr * 8, 8, DIM).sum(axis=1, dtype=np.float32) / np.float32(8.0)
+        c8, cs = quantize_rows(mean)
+        centers[cbase:cbase + pr // 8] = pack_pages(c8, cs)
+        ctab[r, :pr // 8] = cbase + np.arange(pr // 8)
+        fbase += pr
+        cbase += pr // 8
+    out = dict(q8=a["q8"], w=a["w"], native=a["native"], nt=nt, rt=rt, members=members, fine=fine, centers=centers,
+               center_table=ctab, lens=lens)
+    return Workload("config5_route", seed, out,
+                    dict(rows=rows, heads=heads, P=P, CAP=cap, TAKE=take, WIDTH=width, FP=width // 64, topk=topk,
+                         num=num, den=den, sink=sink, window=window, row_bytes=MLA_ROW_BYTES,
+                         latent_rows=pool_pages * PAGE, max_ctx=int(lens.max())))
+
+
 def config6(seed=6, pool_pages=32768, buckets=2048):
     """Index build: every complete 1024-token bucket of a 2M-token pool, each
     bucket's 16 pages a distinct slice of a random permutation of the pool's

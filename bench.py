@@ -17,7 +17,10 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
   3            K/V slot gather: 1024 x 2048 ids (5% padding) through per-query
                512-page windows of a 1M-token pool of 656-byte rows
   5            decode batch: 128 requests x 64 heads, contexts 4K..128K tokens with
-               their own page tables in a 2M-token pool -> Top-2048 -> gather
+               their own page tables in a 2M-token pool, through the V1 route path: center
+               score -> route (page_fraction 0.5) -> fine table -> tail staging -> fine
+               score -> mask -> Top-2048 -> raw/logical/physical map -> gather (the
+               full-scoring chain over every context key timed beside it)
   6            index build: every 1024-token bucket of a 2M-token FP8 pool (2048 buckets)
                -> member order, reordered pages and FP8 centers, one launch
   8            attention consumer: 4096 queries x 4 heads of one KV head, 2048 gathered bf16
@@ -264,43 +267,97 @@ def setup_gather(P, dev, torch, np):
 
 
 def setup_decode(P, dev, torch, np):
-    """Configuration 5: decode batch with per-request page tables."""
-    wl = P.workloads.config5()
+    """Configuration 5: decode batch through the V1 route path
+    (runtime.py:417-634 for <= 512 rows): center score -> fused route ->
+    fine_table_shared -> stage_tail_shared -> fine score -> mask_fine ->
+    topk_transform_512_v2 -> output_ids -> gather.  The full-scoring chain over
+    every context key (score -> Top-2048 -> gather) is timed beside it."""
+    wl = P.workloads.config5_route()
     a, prm = wl.arrays, wl.params
-    rows, heads, T, rb, max_ctx = prm["rows"], prm["heads"], prm["topk"], prm["row_bytes"], prm["max_ctx"]
-    q = torch.from_numpy(a["q8"]).to(dev).view(torch.float8_e4m3fn)
-    w = torch.from_numpy(a["w"]).to(dev)
-    native = torch.from_numpy(a["native"]).to(dev)
-    table = torch.from_numpy(a["table"]).to(dev)
-    lens = torch.from_numpy(a["lens"]).to(dev)
-    latent = torch.randint(0, 256, (prm["latent_rows"], rb), device=dev, dtype=torch.uint8)
-    logits = torch.empty((rows, -(-max_ctx // 4) * 4), device=dev)[:, :max_ctx]
-    slots = torch.empty((rows, T), device=dev, dtype=torch.int32)
-    raw = torch.empty_like(slots)
+    rows, heads, T, rb = prm["rows"], prm["heads"], prm["topk"], prm["row_bytes"]
+    PG, CAP, TAKE, WIDTH, FP, SINK, WIN = prm["P"], prm["CAP"], prm["TAKE"], prm["WIDTH"], prm["FP"], prm["sink"], \
+        prm["window"]
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in a.items()}
+    q = d["q8"].view(torch.float8_e4m3fn)
+    i32 = lambda *sh: torch.empty(sh, device=dev, dtype=torch.int32)
+    fl, takes, dg_lens, center_lens, tail_rows = i32(rows), i32(rows), i32(rows), i32(rows), i32(rows)
+    P.kernels.query_metadata[(rows,)](d["lens"], d["nt"], fl, takes, dg_lens, center_lens, tail_rows, PG, T,
+                                      prm["num"], prm["den"], SINK, WIN)
+    coarse = torch.empty((rows, PG * 8), device=dev)
+    sel, ft = i32(rows, TAKE), i32(rows, FP)
+    scores = torch.empty((rows, WIDTH), device=dev)
+    ident = torch.arange(FP, device=dev, dtype=torch.int32)[None].expand(rows, -1)
+    transformed, raw, out, logical = i32(rows, T), i32(rows, T), i32(rows, T), i32(rows, T)
+    # 656-byte latent rows of the 2M-token pool: byte c of row i = (131 i + 7 c) mod 256
+    row_term = ((torch.arange(prm["latent_rows"], device=dev, dtype=torch.int64) * 131) & 255).to(torch.uint8)
+    latent = row_term[:, None] + ((torch.arange(rb, device=dev, dtype=torch.int64) * 7) & 255).to(torch.uint8)[None]
     work = torch.empty((rows, T, rb), device=dev, dtype=torch.uint8)
+    fused = P.query_fused.module()
+    K = P.kernels
     stages = [
-        ("score", lambda: P.scoring.fp8_paged_mqa_logits(q, native, w, lens, table, None, max_ctx,
-                                                          clean_logits=False, out=logits)),
-        ("topk", lambda: P.topk.topk_transform_512_v2(logits, lens, table, slots, 64, None, raw)),
-        ("gather", lambda: P.native_kernels.gather_rows(latent, slots, work)),
+        ("coarse", lambda: P.scoring.fp8_paged_mqa_logits(q, d["centers"], d["w"], center_lens, d["center_table"],
+                                                           None, PG * 8, clean_logits=True, out=coarse)),
+        ("route", lambda: fused.route(coarse, d["lens"], takes, sel, PG, d["rt"], ft, tail_rows, CAP, False)),
+        ("table", lambda: K.fine_table_shared[(rows,)](d["rt"], sel, takes, d["lens"], ft, tail_rows, CAP, PG, TAKE,
+                                                       FP, 68, 1 << (FP - 1).bit_length())),
+        ("stage", lambda: K.stage_tail_shared[(rows, 68)](d["native"], None, d["nt"], d["lens"], d["fine"], None,
+                                                          tail_rows, CAP, PG, 68, SINK, WIN, ROWS=rows, GROUP=1)),
+        ("score", lambda: P.scoring.fp8_paged_mqa_logits(q, d["fine"], d["w"], dg_lens, ft, None, WIDTH,
+                                                          clean_logits=True, out=scores)),
+        ("mask", lambda: K.mask_fine[(rows, -(-WIDTH // 256))](scores, sel, d["rt"], d["members"], d["lens"], takes,
+                                                               PG, TAKE, WIDTH, WIDTH, SINK, WIN)),
+        ("topk", lambda: P.topk.topk_transform_512_v2(scores, fl, ident, transformed, 64, None, raw)),
+        ("map", lambda: K.output_ids[(rows, -(-T // 256))](raw, scores, d["members"], d["rt"], d["nt"], sel,
+                                                           d["lens"], takes, out, logical, ft, PG, PG, TAKE, WIDTH, T,
+                                                           SINK, WIN, MAP_PHYSICAL=True, DIRECT_FINE=False, FP=FP)),
+        ("gather", lambda: P.native_kernels.gather_rows(latent, out, work)),
     ]
-    L = a["lens"].astype(np.int64)
+    meta_h = [x.cpu().numpy().astype(np.int64) for x in (fl, takes, center_lens, tail_rows)]
+    F, TK_, CL, owners = meta_h[0], meta_h[1], meta_h[2], meta_h[3]
+    n = a["lens"].astype(np.int64)
+    built = np.maximum(n - 1, 0) // 1024 * 16
+    sink = np.minimum(n, SINK)
+    tail = np.maximum(sink, np.minimum(np.maximum(n - 1, 0) // 1024 * 1024, np.maximum(sink, n - WIN)))
+    staged_pages = np.where(owners == np.arange(rows), np.maximum(1, -(-(sink + n - tail) // 64)), 0)
     work_units = {
-        # decode scoring is bound by the K pages it streams: 132 B per (row, key) + Q, w and the logit
-        "score": ((132.0 * L.sum() + rows * heads * 132.0 + 4.0 * L.sum()) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
-        "topk": ((4.0 * L.sum() + 8.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
-        "gather": (lambda: _gather_gb(torch, slots, rb, latent.shape[0]), "GB/s", PEAK_HBM_GBS, "hbm"),
+        # HBM-bound stages: algorithmic bytes from the per-row lengths
+        "coarse": ((132.0 * CL.sum() + rows * heads * 132.0 + 4.0 * rows * PG * 8) / 1e9, "GB/s", PEAK_HBM_GBS,
+                   "hbm"),
+        "route": ((32.0 * built.sum() + 4.0 * rows * TAKE) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "table": ((8.0 * rows * FP) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "stage": ((2.0 * 8448 * staged_pages.sum()) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "score": ((132.0 * F.sum() + rows * heads * 132.0 + 4.0 * rows * WIDTH) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "mask": ((4.0 * (TK_ * 64).sum() + 4.0 * rows * WIDTH) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "topk": ((4.0 * F.sum() + 8.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "map": ((28.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "gather": (lambda: _gather_gb(torch, out, rb, latent.shape[0]), "GB/s", PEAK_HBM_GBS, "hbm"),
     }
+
+    # the full-scoring chain over every context key, timed beside the route path
+    max_ctx = prm["max_ctx"]
+    tab5 = d["nt"][:, : -(-max_ctx // 64)].contiguous()
+    full_logits = torch.empty((rows, -(-max_ctx // 4) * 4), device=dev)[:, :max_ctx]
+    f_slots, f_raw = i32(rows, T), i32(rows, T)
+
+    def full_chain():
+        P.scoring.fp8_paged_mqa_logits(q, d["native"], d["w"], d["lens"], tab5, None, max_ctx, clean_logits=False,
+                                       out=full_logits)
+        P.topk.topk_transform_512_v2(full_logits, d["lens"], tab5, f_slots, 64, None, f_raw)
+        P.native_kernels.gather_rows(latent, f_slots, work)
 
     def cpu(budget):
         from oracle import cpu_baseline
-        qps, n, threads = cpu_baseline.decode_queries_per_second(a["q8"], a["w"], a["native"], a["table"],
-                                                                 a["lens"], T, budget)
-        return qps, threads, f"{n} of {rows} requests (score+top2048+slot map; gather rows synthetic)"
+        qps, nq, threads = cpu_baseline.decode_route_queries_per_second(a, prm, budget)
+        return qps, threads, f"{nq} of {rows} requests (V1 route path: center score, route, fine score, mask, " \
+                             f"top2048, slot map; gather rows left out)"
 
-    meta = {"workload": "decode batch: 128 requests x 64 heads FP8, contexts 4K-128K tokens with per-request "
-                        "page tables in a 2M-token pool, Top-2048, 656-byte row gather",
-            "global_batch": rows, "seq_len": max_ctx, "parallelism": "single GPU"}
+    meta = {"workload": "decode batch: 128 requests x 64 heads FP8, contexts 4K-128K tokens with per-request page "
+                        "tables in a 2M-token pool, V1 route path (page_fraction 0.5, fine widths up to 67K), "
+                        "Top-2048, 656-byte row gather",
+            "global_batch": rows, "seq_len": WIDTH, "parallelism": "single GPU",
+            "_extra": [("full_scoring_chain", full_chain,
+                        (lambda: (132.0 * n.sum() + 4.0 * 2 * n.sum() + rows * T * (8.0 + rb * 2)) / 1e9, "GB/s",
+                         PEAK_HBM_GBS, "hbm"))]}
     return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 5)"
 
 

@@ -137,6 +137,45 @@ def decode_queries_per_second(q8, w, native, table, lens, topk=2048, budget_s=10
     return done / (time.perf_counter() - t0), done, threads
 
 
+def decode_route_queries_per_second(a, prm, budget_s=10.0, min_rows=4):
+    """The decode batch's V1 route path per request in the reference's torch
+    terms (example_v1_query_single_head.py:38-70 with 64 heads and the
+    scoring expression of test_and_bench.py:37): center scores, page max of
+    8, top-take pages, candidate keys (their members, sink, tail), masked fine
+    scores, Top-2048, slot map (the row gather is left out of this sample)."""
+    threads = torch.get_num_threads()
+    rows, P, topk, sink_cap, window = prm["rows"], prm["P"], prm["topk"], prm["sink"], prm["window"]
+    num, den = prm["num"], prm["den"]
+    members = torch.from_numpy(a["members"].astype(np.int64))
+    order = np.random.default_rng(0).permutation(rows)
+    done, t0 = 0, time.perf_counter()
+    while done < rows and (done < min_rows or time.perf_counter() - t0 < budget_s):
+        r = int(order[done])
+        n = int(a["lens"][r])
+        pages = max(n - 1, 0) // 1024 * 16
+        take = min(pages, max(-(-pages * num // den), -(-topk // 64)))
+        q = torch.from_numpy(a["q8"][r]).view(torch.float8_e4m3fn).float()
+        w = torch.from_numpy(a["w"][r])
+        cen, cs = _dequant_pages(a["centers"], a["center_table"][r, : pages // 8])
+        coarse = (torch.relu(q @ cen.T) * w[:, None]).sum(0) * cs
+        chosen_pages = coarse.view(pages, 8).amax(1).topk(take).indices
+        rt = torch.from_numpy(a["rt"][r].astype(np.int64))
+        chosen = members[rt[chosen_pages]].reshape(-1)
+        sink = min(n, sink_cap)
+        tail = max(sink, min((n - 1) // 1024 * 1024, max(sink, n - window)))
+        cand = torch.cat((chosen, torch.arange(sink), torch.arange(tail, n)))
+        keys, ks = _dequant_pages(a["native"], a["nt"][r, : -(-n // 64)])
+        valid = torch.ones(cand.shape[0], dtype=torch.bool)
+        valid[: take * 64] = (chosen >= sink) & (chosen < tail)
+        scores = ((torch.relu(q @ keys[cand].T) * w[:, None]).sum(0) * ks[cand]).masked_fill(~valid, float("-inf"))
+        raw = scores.topk(min(topk, scores.shape[0])).indices
+        lg = cand[raw]
+        phys = torch.from_numpy(a["nt"][r].astype(np.int64))[lg // 64] * 64 + lg % 64
+        assert phys.shape[0] == raw.shape[0]
+        done += 1
+    return done / (time.perf_counter() - t0), done, threads
+
+
 class _RowsOf:
     """tmp[i] = payload[inv[i]] without materialising every entry's page."""
 

@@ -181,3 +181,122 @@ def test_config5_decode_batch(dev):
     assert np.array_equal(raw_h[pick], e_raw) and np.array_equal(slots_h[pick], e_slots)
     assert np.array_equal(H(out[torch.from_numpy(pick).to(dev)]), O.gather_rows(latent, e_slots))
     assert (np.diff(raw_h, axis=1) > 0).all() and (raw_h < a["lens"][:, None]).all()
+
+
+def _latent_rows(ids, row_bytes):
+    """Closed-form 656-byte latent rows (byte c of row i = (131 i + 7 c) mod 256)."""
+    ids = np.asarray(ids, np.int64)
+    return ((ids[..., None] * 131 + np.arange(row_bytes) * 7) & 255).astype(np.uint8)
+
+
+@pytest.fixture(scope="module")
+def config5_route():
+    return W.config5_route()
+
+
+def test_config5_route_chain(dev, config5_route):
+    """The decode batch as the reference runs it for <= 512 rows
+    (sglang/srt/layers/attention/v1_deepseek/runtime.py:417-634, page_fraction
+    0.5): center score -> fused route -> fine_table_shared -> stage_tail_shared
+    -> fine score -> mask_fine -> topk_transform_512_v2 -> output_ids -> gather,
+    128 requests of 4K..128K tokens over the 2M-token pool.  Integer hand-offs
+    are compared on every row, scores, staging, mask and gather on the first,
+    last, longest and shortest rows and a seeded sample; fine widths reach
+    ~67 K columns (segmented Top-K)."""
+    wl = config5_route
+    a, prm = wl.arrays, wl.params
+    rows, P, CAP, TAKE, WIDTH, FP = prm["rows"], prm["P"], prm["CAP"], prm["TAKE"], prm["WIDTH"], prm["FP"]
+    TOP, SINK, WIN = prm["topk"], prm["sink"], prm["window"]
+    d = {k: T(v, dev) for k, v in a.items() if k not in ("fine",)}
+    fine_d = T(a["fine"], dev)
+    q = d["q8"].view(torch.float8_e4m3fn)
+    i32 = lambda *s: torch.empty(s, device=dev, dtype=torch.int32)
+
+    # per-row lengths and owners (kernels.py:568-591)
+    fl, takes, dg_lens, center_lens, tail_rows = i32(rows), i32(rows), i32(rows), i32(rows), i32(rows)
+    K.query_metadata[(rows,)](d["lens"], d["nt"], fl, takes, dg_lens, center_lens, tail_rows, P, TOP, prm["num"],
+                              prm["den"], SINK, WIN)
+    meta = O.query_metadata(a["lens"], a["nt"], TOP, prm["num"], prm["den"], SINK, WIN)
+    for got, exp in zip((fl, takes, dg_lens, center_lens, tail_rows), meta):
+        assert np.array_equal(H(got), exp)
+    fl_h, takes_h, tail_h = meta[0], meta[1], meta[4]
+    assert fl_h.max() > 32768  # segmented Top-K rows are part of the batch
+
+    g = np.random.default_rng(55)
+    pick = _sample_rows(rows, g, extra=(int(np.argmax(a["lens"])), int(np.argmin(a["lens"]))))
+    pick_d = torch.from_numpy(pick).to(dev)
+
+    # center score over each row's center table (8 centers per built page)
+    coarse = SC.fp8_paged_mqa_logits(q, d["centers"], d["w"], center_lens, d["center_table"], None, P * 8,
+                                     clean_logits=True)
+    coarse_h = H(coarse)
+    ref = O.paged_logits(a["q8"][pick], a["w"][pick], a["centers"], a["center_table"][pick], meta[3][pick], P * 8)
+    bound = O.paged_logits(a["q8"][pick], a["w"][pick], a["centers"], a["center_table"][pick], meta[3][pick], P * 8,
+                           magnitude=True)
+    assert_scores_close(coarse_h[pick].astype(np.float64), ref, bound)
+
+    # fused route (no table fill, runtime.py:445-448), then fine_table_shared
+    sel, ft = i32(rows, TAKE), i32(rows, FP)
+    QF.module().route(coarse, d["lens"], takes, sel, P, d["rt"], ft, tail_rows, CAP, False)
+    e_sel = np.zeros((rows, TAKE), np.int32)
+    O.route(coarse_h, a["lens"], takes_h, e_sel, P, a["rt"], np.zeros((rows, FP), np.int32), tail_h, CAP, False)
+    sel_h = H(sel)
+    assert np.array_equal(sel_h, e_sel)
+    K.fine_table_shared[(rows,)](d["rt"], sel, takes, d["lens"], ft, tail_rows, CAP, P, TAKE, FP, 68,
+                                 1 << (FP - 1).bit_length())
+    ft_h = H(ft)
+    assert np.array_equal(ft_h, O.fine_table(a["rt"], e_sel, takes_h, FP, CAP, 68, tail_rows=tail_h))
+
+    # shared tail staging into each owner's 68 scratch pages
+    K.stage_tail_shared[(rows, 68)](d["native"], None, d["nt"], d["lens"], fine_d, None, tail_rows, CAP, P, 68, SINK,
+                                    WIN, ROWS=rows, GROUP=1)
+    fine_h = H(fine_d)
+    for r in pick:
+        if tail_h[r] != r:
+            continue
+        exp = np.zeros((68, 8448), np.uint8)
+        O.stage_tail(a["native"], a["nt"][r:r + 1], a["lens"][r:r + 1], exp, 0, 68, SINK, WIN)
+        assert np.array_equal(fine_h[CAP + r * 68:CAP + (r + 1) * 68], exp), f"staged tail of row {r}"
+
+    # fine score over each row's fine table, then the sink/tail mask
+    scores = SC.fp8_paged_mqa_logits(q, fine_d, d["w"], dg_lens, ft, None, WIDTH, clean_logits=True)
+    pre = H(scores[pick_d])
+    ref = O.paged_logits(a["q8"][pick], a["w"][pick], fine_h, ft_h[pick], meta[2][pick], WIDTH)
+    bound = O.paged_logits(a["q8"][pick], a["w"][pick], fine_h, ft_h[pick], meta[2][pick], WIDTH, magnitude=True)
+    assert_scores_close(pre.astype(np.float64), ref, bound)
+    K.mask_fine[(rows, -(-WIDTH // 256))](scores, sel, d["rt"], d["members"], d["lens"], takes, P, TAKE,
+                                          scores.stride(0), WIDTH, SINK, WIN)
+    post = H(scores)
+    O.mask_fine(pre, sel_h[pick], a["rt"][pick], a["members"], a["lens"][pick], takes_h[pick], WIDTH, SINK, WIN)
+    assert np.array_equal(post[pick], pre)
+
+    # Top-2048 over each row's fine candidates, then the raw -> logical -> physical map
+    ident = torch.arange(FP, device=dev, dtype=torch.int32)[None].expand(rows, -1)
+    transformed, raw = i32(rows, TOP), i32(rows, TOP)
+    TK.topk_transform_512_v2(scores, fl, ident, transformed, 64, None, raw)
+    e_tr, e_raw = O.transform_topk(post, fl_h, np.broadcast_to(np.arange(FP, dtype=np.int32), (rows, FP)), TOP, 6)
+    raw_h = H(raw)
+    assert np.array_equal(raw_h, e_raw) and np.array_equal(H(transformed), e_tr)
+    out, logical = i32(rows, TOP), i32(rows, TOP)
+    K.output_ids[(rows, -(-TOP // 256))](raw, scores, d["members"], d["rt"], d["nt"], sel, d["lens"], takes, out,
+                                         logical, ft, P, P, TAKE, scores.stride(0), TOP, SINK, WIN, MAP_PHYSICAL=True,
+                                         DIRECT_FINE=False, FP=FP)
+    e_out, e_lg = O.output_ids(e_raw, post, a["members"], a["rt"], a["nt"], sel_h, a["lens"], takes_h,
+                               scores.stride(0), TOP, SINK, WIN, True, False, ft_h)
+    out_h = H(out)
+    assert np.array_equal(out_h, e_out) and np.array_equal(H(logical), e_lg)
+    # every selected token lies in its request's context, once
+    for r in range(rows):
+        lg = e_lg[r][e_lg[r] >= 0]
+        assert lg.max() < a["lens"][r] and np.unique(lg).size == lg.size
+
+    # gather of 656-byte latent rows through the physical slots
+    rb = prm["row_bytes"]
+    row_term = ((torch.arange(prm["latent_rows"], device=dev, dtype=torch.int64) * 131) & 255).to(torch.uint8)
+    col_term = ((torch.arange(rb, device=dev, dtype=torch.int64) * 7) & 255).to(torch.uint8)
+    latent = row_term[:, None] + col_term[None]  # uint8 addition wraps mod 256
+    work = torch.empty((rows, TOP, rb), device=dev, dtype=torch.uint8)
+    NK.gather_rows(latent, out, work)
+    got = H(work[pick_d])
+    exp = np.where((e_out[pick] >= 0)[..., None], _latent_rows(np.maximum(e_out[pick], 0), rb), 0)
+    assert np.array_equal(got, exp)
