@@ -694,6 +694,35 @@ def test_topk_adversarial_rows(dev, kind, cols):
     assert np.array_equal(H(raw), e_raw) and np.array_equal(H(out), e_out)
 
 
+@pytest.mark.parametrize("cols", [2100, 9000, 32768])
+def test_topk_large_batch_vs_oracle(dev, cols):
+    """1100 rows (more than four per CU) of varying lengths with every
+    adversarial row kind mixed in (their pivot misses take the re-aimed pivot
+    or the exact passes), rows of at most T candidates and a padded row
+    stride; every row compared with the oracle."""
+    g = np.random.default_rng(cols + 7)
+    B = 1100
+    stride = -(-cols // 4) * 4 + 4
+    scores = g.standard_normal((B, stride)).astype(np.float32)
+    kinds = ["plateau", "ascending", "descending", "neg_inf_heavy", "two_values", "tiny_spread", "signed_zero",
+             "nan_sprinkled", "nan_heavy"]
+    for i, kind in enumerate(kinds):
+        for j in range(4):
+            scores[37 * i + j, :cols] = _adversarial_rows(kind, g, cols)
+    lens = g.integers(2049, cols + 1, B).astype(np.int32)
+    lens[[5, 600]] = [2048, 100]
+    lens[[6, 601]] = cols
+    table = np.arange(-(-cols // 64), dtype=np.int32)[None].repeat(B, 0)
+    out = torch.empty((B, 2048), device=dev, dtype=torch.int32)
+    raw = torch.empty_like(out)
+    TK.topk_transform_512_v2(T(scores, dev)[:, :cols], T(lens, dev), T(table, dev), out, 64, None, raw)
+    e_out, e_raw = O.transform_topk(scores[:, :cols], lens, table, 2048, 6)
+    raw_h, out_h = H(raw), H(out)
+    bad = np.flatnonzero((raw_h != e_raw).any(axis=1))
+    assert bad.size == 0, f"rows {bad[:10].tolist()} differ"
+    assert np.array_equal(out_h, e_out)
+
+
 # ------------------------------------------------- unfused C4 x4 expansion
 @pytest.mark.parametrize("rows,topk,stride,block,offset", [
     (64, 2048, 4 * 2048 + 64, 16384, 0),   # runtime.py:638-641 shape (BLOCK = next power of two)
