@@ -300,3 +300,90 @@ def test_config5_route_chain(dev, config5_route):
     got = H(work[pick_d])
     exp = np.where((e_out[pick] >= 0)[..., None], _latent_rows(np.maximum(e_out[pick], 0), rb), 0)
     assert np.array_equal(got, exp)
+
+
+def _top_fp64(scores, lens, topk):
+    """Top-`topk` of each row of fp64 scores over its first lens[r] columns:
+    value descending, ties toward the lower index, returned ascending."""
+    out = np.full((scores.shape[0], topk), -1, np.int64)
+    for b in range(scores.shape[0]):
+        L = int(lens[b])
+        order = np.lexsort((np.arange(L), -scores[b, :L]))[:topk]
+        out[b, :min(L, topk)] = np.sort(order)
+    return out
+
+
+def _disagreement(got, exp, ref, bound):
+    """(count of selected indices that differ, largest fp64 score inversion
+    between a differing pair in units of 2^-16 * magnitude) over all rows;
+    asserts each inversion is within the two scores' tolerances (a near-tie)."""
+    count, worst = 0, 0.0
+    for b in range(got.shape[0]):
+        g, e = set(got[b][got[b] >= 0].tolist()), set(exp[b][exp[b] >= 0].tolist())
+        only_got, only_exp = sorted(g - e), sorted(e - g)
+        assert len(only_got) == len(only_exp)
+        count += len(only_got)
+        for x in only_exp:
+            for y in only_got:
+                gap = ref[b, x] - ref[b, y]
+                tol = 1e-2 * (abs(ref[b, x]) + abs(ref[b, y])) + 2.0 ** -16 * (bound[b, x] + bound[b, y])
+                assert gap <= tol, (b, x, y, gap, tol)
+                worst = max(worst, gap / (2.0 ** -16 * max(bound[b, x], bound[b, y])))
+    return count, worst
+
+
+def test_index_agreement_with_fp64_reference_topk(dev):
+    """End to end: the Top-2048 the GPU chain selects from its FP8-MFMA logits
+    against a Top-2048 over the fp64 dequantised reference scores
+    (sglang/srt/layers/attention/v1_deepseek/kernels.py:310-313), as the
+    reference example checks its Top-K against topk on reference scores
+    (example_v1_query_single_head.py:55-70).  Indices can differ only where
+    two scores are within fp32 rounding of each other across the selection
+    boundary: every differing pair is checked to be such a near-tie, and the
+    counts are printed."""
+    report = []
+    # prefill chunk (4096 x 64 heads x 32K keys): sampled rows
+    wl = W.config4()
+    a, prm = wl.arrays, wl.params
+    rows, ctx, TOP = prm["rows"], prm["ctx"], prm["topk"]
+    table = T(a["table"], dev)
+    logits = SC.fp8_paged_mqa_logits(T(a["q8"], dev).view(torch.float8_e4m3fn), T(a["native"], dev), T(a["w"], dev),
+                                     T(a["lens"], dev), table[None].expand(rows, -1), None, ctx, clean_logits=True)
+    slots = torch.empty((rows, TOP), device=dev, dtype=torch.int32)
+    raw = torch.empty_like(slots)
+    TK.topk_transform_512_v2(logits, T(a["lens"], dev), table[None].expand(rows, -1).contiguous(), slots, 64, None, raw)
+    pick = _sample_rows(rows, np.random.default_rng(40))
+    full = np.broadcast_to(a["table"], (len(pick), a["table"].shape[0]))
+    ref = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], full, a["lens"][pick], ctx)
+    bound = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], full, a["lens"][pick], ctx, magnitude=True)
+    diff4, gap4 = _disagreement(H(raw)[pick], _top_fp64(ref, a["lens"][pick], TOP), ref, bound)
+    report.append(f"prefill 4096x32K: {diff4} of {len(pick) * TOP} selected indices differ ({len(pick)} rows), "
+                  f"largest inversion {gap4:.3g}")
+    # reference example chain (1024 queries x 2688 candidates, masked): every row
+    wl = W.config1()
+    a, prm = wl.arrays, wl.params
+    B, P, CAP, TAKE, WIDTH = prm["B"], prm["P"], prm["CAP"], prm["TAKE"], prm["WIDTH"]
+    q, w, fl = T(a["q8"], dev).view(torch.float8_e4m3fn), T(a["w"], dev), a["fine_lens"]
+    coarse = SC.fp8_paged_mqa_logits(q, T(a["centers"], dev), w, T(np.full(B, 512, np.int32), dev),
+                                     T(a["center_table"], dev)[None].expand(B, -1), None, P * 8, clean_logits=True)
+    sel = torch.empty((B, TAKE), device=dev, dtype=torch.int32)
+    ft = torch.empty((B, prm["FT_COLS"]), device=dev, dtype=torch.int32)
+    QF.module().route(coarse, T(a["lens"], dev), T(a["takes"], dev), sel, P, T(a["rt"], dev), ft,
+                      T(a["tail_rows"], dev), CAP, True)
+    fine = a["fine"].copy()
+    O.stage_tail(a["native"], a["nt"], a["lens"], fine, CAP, 68, prm["SINK"], prm["WINDOW"], tail_rows=a["tail_rows"],
+                 rows=B)
+    logits1 = SC.fp8_paged_mqa_logits(q, T(fine, dev), w, T(fl, dev), ft, None, WIDTH, clean_logits=True)
+    physical = torch.empty((B, TOP), device=dev, dtype=torch.int32)
+    logical, raw1 = torch.empty_like(physical), torch.empty_like(physical)
+    QF.module().topk(logits1, T(fl, dev), T(a["members"], dev), T(a["rt"], dev), T(a["nt"], dev), sel,
+                     T(a["lens"], dev), T(a["takes"], dev), physical, logical, raw1, prm["WINDOW"], True,
+                     torch.empty((B, 0), device=dev, dtype=torch.int32), True, True, ft, False)
+    ref1 = O.paged_logits(a["q8"], a["w"], fine, H(ft), fl, WIDTH)
+    ref1[np.isneginf(H(logits1))] = -np.inf  # the sink/tail mask the kernel applied in place
+    bound1 = O.paged_logits(a["q8"], a["w"], fine, H(ft), fl, WIDTH, magnitude=True)
+    exp1 = _top_fp64(ref1, fl, TOP)
+    diff1, gap1 = _disagreement(H(raw1), exp1, ref1, bound1)
+    report.append(f"reference example 1024x2688: {diff1} of {int((exp1 >= 0).sum())} selected indices differ, "
+                  f"largest inversion {gap1:.3g}")
+    print("; ".join(report))
