@@ -51,7 +51,7 @@ PEAK_FP8_TFLOPS = 5000.0
 # plain copy), kept with the kernel trace of the same workload.
 TRAFFIC = {
     4: (ROOT / "profiles" / "prefill_chunk_4096x32k.md",
-        {"score": ("score_prep", "score_shared"), "topk": ("transform_rows",), "gather": ("gather_rows16",)}),
+        {"score": ("score_prep", "score_shared", "score_exact"), "topk": ("transform_rows",), "gather": ("gather_rows16",)}),
     6: (ROOT / "profiles" / "index_build_2048x1024.md", {"build": ("build_buckets_kernel",)}),
     2: (ROOT / "profiles" / "page_management_4096req.md",
         {"insert": ("pb_init", "pb_hash", "pb_classify", "pb_slow_live", "pb_slow", "pb_allocate", "pb_table",
@@ -86,6 +86,17 @@ def measured_traffic(config, stage):
             continue
     vals = [per_kernel.get(k) for k in stages[stage]]
     return None if any(v is None for v in vals) else sum(vals)
+
+
+def cpu_model():
+    """The host processor's model name, as the kernel reports it."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def parse():
@@ -726,7 +737,7 @@ def main():
     if args.cpu_budget > 0:
         qps_cpu, threads, sample = cpu_fn(args.cpu_budget)
         cpu = {"value": round(qps_cpu, 3), "unit": rate_unit, "cores": threads, "kind": "port",
-               "sample": f"{sample}, torch CPU, {os.cpu_count()} host cpus visible"}
+               "sample": f"{sample}, torch CPU, {os.cpu_count()} host cpus visible", "cpu": cpu_model()}
 
     qps = rows * args.steps / (t1 - t0)
     line = {
