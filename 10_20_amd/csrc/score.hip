@@ -62,7 +62,6 @@ struct ScoreParams {
     int32_t groups;         // shared-table kernel: 8-query row groups
     int32_t items;          // shared-table kernel: groups x levels
     uint32_t* work;         // shared-table kernel: next work item (zeroed by score_prep)
-    float* sink;            // shared-table kernel: 64 floats that masked-out logit stores write
     int32_t bulk;           // shared-table kernel: levels of full-size ranges (chunks [L*F, (L+1)*F))
     int32_t lvl_start[16];  // shared-table kernel: chunk range of each later level's items
     int32_t lvl_chunks[16];
@@ -272,11 +271,16 @@ __device__ __forceinline__ int key_swizzle(int k) { return (k ^ (k >> 3)) & 7; }
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-// Raw buffer descriptor over one native page (stride 0, 32-bit dwords).
+// Word 3 of a raw buffer descriptor (stride 0, 32-bit dwords).  Accesses at
+// byte offsets at or past the descriptor's length are range-checked by the
+// hardware: loads return zeros and stores are dropped.
+constexpr int32_t kRawDword = 0x00020000;
+
+// Raw buffer descriptor over one native page.
 __device__ __forceinline__ i32x4 page_rsrc(const uint8_t* kv, int32_t page) {
     const uint64_t base = reinterpret_cast<uint64_t>(kv + (int64_t)max(page, 0) * V1_PAGE_BYTES);
     return i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)(base >> 32) & 0xffff, page >= 0 ? V1_PAGE_BYTES : 0,
-                 0x00020000};
+                 kRawDword};
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -347,6 +351,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     const int32_t c_begin = level < p.bulk ? level * kFull : p.lvl_start[level - p.bulk];
     const int32_t nchunk = level < p.bulk ? kFull : p.lvl_chunks[level - p.bulk];
     const int32_t page_begin = c_begin * kChunkPages;
+    const int32_t grows = (int32_t)min<int64_t>(kQueriesPerGroup, (int64_t)p.rows - row0);  // rows of the group
 
     // The independent loads of the prologue are all issued before the first
     // wait: query lengths (lane q mod 8: query row0 + q), the range's page
@@ -510,29 +515,39 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
             }
         }
     };
-    // Every step issues exactly kQueriesPerWave logit stores: lanes with
-    // nothing to write (no page, a row past the end, a column past the
-    // context without clean_logits) store to the sink.  The count of vector
-    // memory operations per step is then fixed, which the page wait relies on.
+    // Every step issues exactly kQueriesPerWave logit stores, each through a
+    // buffer descriptor over the columns of the page that the query writes:
+    // lanes with nothing to write (no page, a row past the end, a column past
+    // max_context_len, or past the context without clean_logits) lie past the
+    // descriptor's length, so the hardware's range check drops their stores.
+    // The count of vector memory operations per step is then fixed, which
+    // the page wait relies on.
     // Keys whose fast ReLU value lies within the query's exact-path threshold
     // of zero only mark their page here (a bit per query and page in LDS, set
     // in a rarely taken scalar branch with no vector memory operation); the
     // item's end hands the marks to score_exact.
     auto store = [&](int32_t pg, bool live, const float (&part)[kQueriesPerWave][4], float scale) {
+        const int32_t col = (page_begin + pg) * 64;  // this page's first column
 #pragma unroll
         for (int q = 0; q < kQueriesPerWave; ++q) {
             const float v = reduce_scatter4(part[q]);
-            const int64_t row = row0 + wv * kQueriesPerWave + q;
-            const int32_t j = (page_begin + pg) * 64 + l;
-            const bool in = live & (row < p.rows) & (j < p.max_context_len) & ((j < ctx[q]) | (p.clean != 0));
-            float* dst = in ? p.logits + row * p.logits_stride + j : p.sink + l;
-            *dst = j < ctx[q] ? v * scale : -__builtin_huge_valf();
+            const int32_t qr = wv * kQueriesPerWave + q;  // row within the group
+            // columns [col, col + 64) of the query: logits below its context,
+            // -inf from there to max_context_len with clean_logits; the
+            // descriptor covers the columns to write, lanes past it are dropped
+            const int32_t valid = ctx[q] - col;
+            const int32_t end = (p.clean ? p.max_context_len : ctx[q]) - col;
+            const int32_t lim = (live && qr < grows && end > 0) ? (end < 64 ? end : 64) : 0;
+            const auto rs = __builtin_amdgcn_make_buffer_rsrc(p.logits + (row0 + qr) * p.logits_stride + col, 0,
+                                                              lim * 4, kRawDword);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l < valid ? v * scale : -__builtin_huge_valf()), rs,
+                                                  l * 4, 0, 0);
             if (RELU) {
                 // (ballots of the bare compares stay scalar masks; the
                 // uniform conditions join on the scalar side)
                 const uint64_t near = __builtin_amdgcn_ballot_w64(fabsf(v) <= exact_thr[q]) &
-                                      __builtin_amdgcn_ballot_w64(j < ctx[q]);
-                if (near != 0ull && live && row < p.rows) {
+                                      __builtin_amdgcn_ballot_w64(l < valid);
+                if (near != 0ull && live && qr < grows) {
                     // (the empty asm keeps this block's address arithmetic
                     // from being hoisted out of the loop into live registers)
                     int32_t bit = (page_begin & 31) + pg;
@@ -620,8 +635,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     fill_rest(npages);
     // Marked pages go to the per-row page bitmap that score_exact reads (an
     // OR per word that has a mark; the words are cleared for the next item).
-    // (The bitmaps sit 256 bytes past the sink, and their row length follows
-    // from max_context_len: no more kernel arguments stay live in the loop.)
+    // (The bitmaps' row length follows from max_context_len.)
     int lane = l;
     asm volatile("" : "+v"(lane));  // keeps the lane arithmetic below inside the loop
     if (RELU && lane < kQueriesPerWave * kMarkWords) {
@@ -629,8 +643,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         const uint32_t bits = marks[(wv * kQueriesPerWave + q) * kMarkWords + k];
         if (bits != 0u) {
             const int32_t words = (((p.max_context_len + 63) >> 6) + 31) >> 5;
-            uint32_t* pages = reinterpret_cast<uint32_t*>(p.sink + 64);
-            atomicOr(pages + (row0 + wv * kQueriesPerWave + q) * words + (page_begin >> 5) + k, bits);
+            atomicOr(p.exact_pages + (row0 + wv * kQueriesPerWave + q) * words + (page_begin >> 5) + k, bits);
             marks[(wv * kQueriesPerWave + q) * kMarkWords + k] = 0u;
         }
     }
@@ -811,16 +824,13 @@ void launch_hb(int hb, bool relu, dim3 g, hipStream_t st, const ScoreParams& p) 
 
 using namespace v1;
 
-// per-query records, the work counter (256 bytes), the store sink (256 bytes)
-// Shared-table layout: per-query records, the work counter (256 bytes), the
-// store sink (256 bytes), then (ReLU rule) the per-row bitmaps of pages that
-// score_exact recomputes.
+// Shared-table workspace: per-query records, the work counter (256 bytes),
+// then (ReLU rule) the per-row bitmaps of pages that score_exact recomputes.
 static int32_t exact_words(int32_t max_context_len) { return (int32_t)cdiv(cdiv(max_context_len, 64), 32); }
-static_assert(kPieceRowBytes % 16 == 0, "the bitmaps follow the sink at a fixed offset");
 
 extern "C" int64_t v1_score_workspace(int32_t rows, int32_t max_context_len) {
     if (rows <= 0 || max_context_len < 0) return 0;
-    return (int64_t)rows * kPieceRowBytes + 512 + (int64_t)rows * exact_words(max_context_len) * 4;
+    return (int64_t)rows * kPieceRowBytes + 256 + (int64_t)rows * exact_words(max_context_len) * 4;
 }
 
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
@@ -869,8 +879,7 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         uint8_t* ws = static_cast<uint8_t*>(a->workspace);
         p.pieces = ws;
         p.work = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes);
-        p.sink = reinterpret_cast<float*>(ws + (int64_t)a->rows * kPieceRowBytes + 256);
-        p.exact_pages = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes + 512);
+        p.exact_pages = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes + 256);
         p.exact_words = a->relu ? exact_words(a->max_context_len) : 0;
         const dim3 row_waves((uint32_t)cdiv(a->rows, 4));
         hipLaunchKernelGGL(score_prep, row_waves, dim3(256), 0, st, a->q, a->weights, a->rows, a->heads, a->relu, ws,
@@ -896,8 +905,8 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
 }
 
 // ------------------------------------------------ allocation-free variant
-// The shared-table path's scratch (per-query records, work counter, store
-// sink, exact-page bitmaps) in one static device array per GPU, for callers
+// The shared-table path's scratch (per-query records, work counter,
+// exact-page bitmaps) in one static device array per GPU, for callers
 // that cannot allocate.  Every call on a GPU shares that GPU's array: calls
 // that overlap on one GPU race.  score_prep clears what must start at zero
 // (the work counter and the bitmaps) with a kernel at every call.
