@@ -107,3 +107,85 @@ def test_index_build_and_slot_attention_replay_in_a_hip_graph():
         torch.cuda.synchronize()
         for a, b in zip(got, (*out, att)):
             assert torch.equal(a, b)
+
+
+def test_query_chain_replays_in_a_hip_graph():
+    """Query.compute's fused chain (sglang/srt/layers/attention/v1_deepseek/
+    runtime.py:417-678) captured once: coarse score -> route with the fine-table
+    fill -> shared tail staging -> fine score -> fused Top-2048 with the mask and
+    physical map -> slot gather.  Replayed with new queries, a new context
+    length for the request (pages, sink and tail move), new per-row budgets and
+    a permuted reordered table (as experiments/fine_pool_shared_20261021/
+    test_route_shared.py:43-48 replays route), each replay equal bit for bit to
+    the chain run eagerly."""
+    QF = importlib.import_module("10_20_amd.query_fused")
+    K = importlib.import_module("10_20_amd.kernels")
+    wl = W.config1(rows=640)  # the fused Top-K takes batches above 512 rows (v1_query.cuh:206)
+    a, prm = wl.arrays, wl.params
+    B, P, CAP, TAKE, WIDTH, TOP = prm["B"], prm["P"], prm["CAP"], prm["TAKE"], prm["WIDTH"], prm["TOPK"]
+    SINK, WINDOW = prm["SINK"], prm["WINDOW"]
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+    q = t(a["q8"])
+    w = t(a["w"])
+    centers, native, members, nt = t(a["centers"]), t(a["native"]), t(a["members"]), t(a["nt"])
+    rt, lens, takes, tail_rows = t(a["rt"]), t(a["lens"]), t(a["takes"]), t(a["tail_rows"])
+    fine_lens, fine = t(a["fine_lens"]), t(a["fine"])
+    center_table = t(a["center_table"])[None].expand(B, -1)
+    center_lens = torch.full((B,), 512, device=DEV, dtype=torch.int32)
+    latent = t(a["latent"])
+    coarse = torch.empty((B, P * 8), device=DEV)
+    sel = torch.empty((B, TAKE), device=DEV, dtype=torch.int32)
+    ft = torch.empty((B, prm["FT_COLS"]), device=DEV, dtype=torch.int32)
+    logits = torch.empty((B, WIDTH), device=DEV)
+    physical = torch.empty((B, TOP), device=DEV, dtype=torch.int32)
+    logical, raw = torch.empty_like(physical), torch.empty_like(physical)
+    expanded = torch.empty((B, 4 * TOP + 64), device=DEV, dtype=torch.int32)
+    work = torch.empty((B, TOP, W.MLA_ROW_BYTES), device=DEV, dtype=torch.uint8)
+    outs = (coarse, sel, ft, fine, logits, physical, logical, raw, expanded, work)
+
+    def chain():
+        qv = q.view(torch.float8_e4m3fn)
+        SC.fp8_paged_mqa_logits(qv, centers, w, center_lens, center_table, None, P * 8, clean_logits=True, out=coarse)
+        QF.module().route(coarse, lens, takes, sel, P, rt, ft, tail_rows, CAP, True)
+        K.stage_tail_shared[(-(-B // 32), 68)](native, None, nt, lens, fine, None, tail_rows, CAP, P, 68, SINK, WINDOW,
+                                               ROWS=B, GROUP=32)
+        SC.fp8_paged_mqa_logits(qv, fine, w, fine_lens, ft, None, WIDTH, clean_logits=True, out=logits)
+        QF.module().topk(logits, fine_lens, members, rt, nt, sel, lens, takes, physical, logical, raw, WINDOW, True,
+                         expanded, True, True, ft, False)
+        NK.gather_rows(latent, physical, work)
+
+    def inputs(seed, n, budget, flip):
+        h = np.random.default_rng(seed)
+        q8, qs = W.quantize_rows(h.standard_normal((B, 128)).astype(np.float32))
+        q.copy_(torch.from_numpy(q8.reshape(B, 1, 128)))
+        w.copy_(torch.from_numpy(qs[:, None].astype(np.float32)))
+        lens.fill_(n)
+        takes.copy_(torch.from_numpy(np.minimum(budget, h.integers(8, TAKE + 1, B)).astype(np.int32)))
+        # candidates below the fine width, as query_lengths gives them
+        pages = (n - 1) // 1024 * 16
+        sink = min(SINK, n)
+        tail = max(sink, min((n - 1) // 1024 * 1024, max(sink, n - WINDOW)))
+        count = np.minimum(takes.cpu().numpy(), pages) * 64 + sink + n - tail
+        fine_lens.copy_(torch.from_numpy(np.minimum(count, WIDTH).astype(np.int32)))
+        if flip:
+            rt[:, :64] = rt[:, :64].flip(1)
+
+    inputs(0, 4097, TAKE, False)
+    chain()  # sizes the workspaces
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        chain()
+    for seed, n, budget, flip in ((1, 4097, TAKE, False), (2, 3073, 24, True), (3, 2100, TAKE, False),
+                                  (4, 4097, 16, True)):
+        inputs(seed, n, budget, flip)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [o.clone() for o in outs]
+        chain()
+        torch.cuda.synchronize()
+        for name, x, y in zip(("coarse", "sel", "ft", "fine", "logits", "physical", "logical", "raw", "expanded",
+                               "work"), got, outs):
+            assert torch.equal(x.view(torch.uint8) if x.dtype == torch.float32 else x,
+                               y.view(torch.uint8) if y.dtype == torch.float32 else y), (seed, name)
+        assert int((raw >= 0).sum()) > 0 and int((physical >= 0).sum()) > 0
