@@ -59,6 +59,24 @@ class ScoreArgs(ctypes.Structure):
     ]
 
 
+class CoarseArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("weights", _vp), ("centers", _vp), ("center_blocks", _c_i64), ("table", _vp),
+        ("table_stride", _c_i64), ("lens", _vp), ("scores", _vp), ("rows", _c_i32), ("heads", _c_i32),
+        ("maxp", _c_i32), ("relu", _c_i32), ("workspace", _vp), ("workspace_bytes", _c_i64),
+    ]
+
+
+class FineArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("weights", _vp), ("fine_pages", _vp), ("fine_blocks", _c_i64), ("native_pages", _vp),
+        ("native_blocks", _c_i64), ("members", _vp), ("rt", _vp), ("nt", _vp), ("selected", _vp),
+        ("selected_bits", _c_i32), ("lens", _vp), ("takes", _vp), ("scores", _vp), ("rows", _c_i32),
+        ("heads", _c_i32), ("maxp", _c_i32), ("np", _c_i32), ("take_stride", _c_i32), ("width", _c_i32),
+        ("sink", _c_i32), ("window", _c_i32), ("relu", _c_i32),
+    ]
+
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     "v1_last_error": (ctypes.c_char_p, []),
@@ -68,6 +86,10 @@ _SIGNATURES = {
     "v1_topk_workspace": (_c_i64, [_c_i32, _c_i32, _c_i32]),
     "v1_topk_transform": (_c_i32, [ctypes.POINTER(TopkTransformArgs), _vp]),
     "v1_score": (_c_i32, [ctypes.POINTER(ScoreArgs), _vp]),
+    "v1_reduce_centers": (_c_i32, [_vp, _c_i64, _vp, _vp, _c_i32, _c_i32, _vp]),
+    "v1_coarse_workspace": (_c_i64, [_c_i32, _c_i32, _c_i64]),
+    "v1_coarse": (_c_i32, [ctypes.POINTER(CoarseArgs), _vp]),
+    "v1_fine": (_c_i32, [ctypes.POINTER(FineArgs), _vp]),
     "v1_score_workspace": (_c_i64, [_c_i32, _c_i32]),
     "v1_score_noalloc": (_c_i32, [ctypes.POINTER(ScoreArgs), _vp]),
     "v1_score_noalloc_capacity": (_c_i64, []),

@@ -788,6 +788,141 @@ __global__ __launch_bounds__(256) void score_exact(ScoreParams p) {
     }
 }
 
+// -------------------------------------------- scoring without DeepGEMM
+// The reference's Triton fallbacks for hosts without DeepGEMM or with the
+// query optimisations off (runtime.py:450-466, 565-590).
+
+// sglang/srt/layers/attention/v1_deepseek/kernels.py:475-486: page p of a row
+// scores the max of its 8 center logits for p < max(n-1, 0) / 1024 * 16, else
+// -inf.  One thread per (row, page).
+__global__ __launch_bounds__(256) void reduce_centers_kernel(const float* logits, int64_t stride, const int32_t* lens,
+                                                             float* scores, int32_t maxp) {
+    const int64_t row = blockIdx.y;
+    const int32_t pg = (int32_t)blockIdx.x * 256 + threadIdx.x;
+    if (pg >= maxp) return;
+    const int32_t pages = max(lens[row] - 1, 0) / 1024 * 16;
+    float v = -__builtin_huge_valf();
+    if (pg < pages) {
+        const float* src = logits + row * stride + (int64_t)pg * 8;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) v = fmaxf(v, src[g]);
+    }
+    scores[row * maxp + pg] = v;
+}
+
+// Center counts of the coarse scoring: 8 per built page, at most maxp pages.
+__global__ __launch_bounds__(256) void center_lens_kernel(const int32_t* lens, int32_t* out, int32_t rows,
+                                                          int32_t maxp) {
+    const int32_t r = (int32_t)blockIdx.x * 256 + threadIdx.x;
+    if (r < rows) out[r] = min(max(lens[r] - 1, 0) / 1024 * 16, maxp) * 8;
+}
+
+// kernels.py:248-320: the fine candidates of a row scored straight from the
+// two pools.  Candidate i < take * 64 is slot i % 64 of fine page
+// rt[selected[i / 64]], kept when its logical position members[page][slot]
+// lies in [sink, tail) and below n; the next sink + n - tail candidates are
+// the sink and tail tokens read from native pages through nt.  One wave per
+// 64 candidates: the 16-key MFMA fragments of a fine block come from one page;
+// a tail block's keys are located one by one.  Pages or ranks outside their
+// tables, and candidates past count, score -inf.
+struct FineExtra {
+    const uint8_t* native;
+    int64_t native_blocks;
+    const int32_t* members;   // [fine pages, 64]
+    const int32_t* rt;        // [rows, maxp]
+    const int32_t* nt;        // [rows, np]
+    const void* selected;     // [rows, take_stride], int32 or int64
+    int32_t selected_bits;
+    const int32_t* takes;
+    int32_t maxp, np, take_stride, sink, window;
+};
+
+template <int HB, bool RELU>
+__global__ __launch_bounds__(kThreads) void fine_scores(ScoreParams p, FineExtra f) {
+    const int l = __lane_id(), wv = threadIdx.x / kWave;
+    const int64_t row = blockIdx.y;
+    const int32_t width = p.max_context_len;
+    const int32_t block = (int32_t)blockIdx.x * 4 + wv;
+    if (block * 64 >= width) return;
+    const int32_t n = p.ctx[row], take = max(f.takes[row], 0);
+    const int32_t sink = min(n, f.sink);
+    const int32_t tail = max(sink, min(max(n - 1, 0) / 1024 * 1024, max(sink, n - f.window)));
+    const int64_t count = (int64_t)take * 64 + sink + n - tail;
+    const int32_t i = block * 64 + l;  // this lane's candidate
+    float* out = p.logits + row * p.logits_stride;
+    const float ninf = -__builtin_huge_valf();
+    if ((int64_t)block * 64 >= count) {
+        if (i < width) out[i] = ninf;
+        return;
+    }
+    v8i b[4];
+    float scale = 0.f;
+    bool good;
+    if (block < take) {
+        int64_t rank = -1;
+        if (block < f.take_stride)
+            rank = f.selected_bits == 64 ? static_cast<const int64_t*>(f.selected)[row * f.take_stride + block]
+                                         : static_cast<const int32_t*>(f.selected)[row * f.take_stride + block];
+        const int32_t page = (rank >= 0 && rank < f.maxp) ? f.rt[row * f.maxp + rank] : -1;
+        const bool ok = page >= 0 && page < p.kv_blocks;
+        const uint8_t* base = p.kv + (int64_t)(ok ? page : 0) * V1_PAGE_BYTES;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            b[kb] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+            if (ok) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(base + (kb * 16 + (l & 15)) * 128 + 32 * (l >> 4));
+                const u32x4 x = src[0], y = src[1];
+                b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+            }
+        }
+        int32_t logical = -1;
+        if (ok) {
+            scale = reinterpret_cast<const float*>(base + 8192)[l];
+            logical = f.members[(int64_t)page * 64 + l];
+        }
+        good = ok && logical >= sink && logical < tail && logical < n;
+    } else {
+        // candidate c of the sink/tail part: its native page and slot, or false
+        auto locate = [&](int32_t c, int32_t& page, int32_t& logical) __attribute__((always_inline)) {
+            if ((int64_t)c >= count) return false;
+            const int32_t off = c - take * 64;
+            logical = off < sink ? off : tail + off - sink;
+            if (logical / 64 >= f.np) return false;
+            page = f.nt[row * f.np + logical / 64];
+            return page >= 0 && page < f.native_blocks;
+        };
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            int32_t page = 0, logical = 0;
+            b[kb] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+            if (locate(block * 64 + kb * 16 + (l & 15), page, logical)) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(f.native + (int64_t)page * V1_PAGE_BYTES +
+                                                                  (logical % 64) * 128 + 32 * (l >> 4));
+                const u32x4 x = src[0], y = src[1];
+                b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+            }
+        }
+        int32_t page = 0, logical = 0;
+        good = locate(i, page, logical) && logical < n;
+        if (good) scale = reinterpret_cast<const float*>(f.native + (int64_t)page * V1_PAGE_BYTES + 8192)[logical % 64];
+    }
+    v8i a[HB];
+    float w[HB][4];
+    load_q<HB>(p, row, a);
+    load_w<HB>(p, row, w);
+    float part[4];
+    page_partials<HB, RELU>(a, b, w, part);
+    const float v = reduce_scatter4(part) * scale;  // every lane takes part in the fold
+    if (i < width) out[i] = good ? v : ninf;
+}
+
+struct Fine {
+    template <int HB, bool RELU>
+    static void launch(dim3 g, hipStream_t st, const ScoreParams& p, const FineExtra& f) {
+        hipLaunchKernelGGL((fine_scores<HB, RELU>), g, dim3(kThreads), 0, st, p, f);
+    }
+};
+
 struct Shared {
     template <int HB, bool RELU>
     static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
@@ -801,21 +936,21 @@ struct Rows {
     }
 };
 
-template <typename K, int HB>
-void launch_relu(bool relu, dim3 g, hipStream_t st, const ScoreParams& p) {
+template <typename K, int HB, typename... X>
+void launch_relu(bool relu, dim3 g, hipStream_t st, const ScoreParams& p, const X&... x) {
     if (relu)
-        K::template launch<HB, true>(g, st, p);
+        K::template launch<HB, true>(g, st, p, x...);
     else
-        K::template launch<HB, false>(g, st, p);
+        K::template launch<HB, false>(g, st, p, x...);
 }
 
-template <typename K>
-void launch_hb(int hb, bool relu, dim3 g, hipStream_t st, const ScoreParams& p) {
+template <typename K, typename... X>
+void launch_hb(int hb, bool relu, dim3 g, hipStream_t st, const ScoreParams& p, const X&... x) {
     switch (hb) {
-        case 1: launch_relu<K, 1>(relu, g, st, p); break;
-        case 2: launch_relu<K, 2>(relu, g, st, p); break;
-        case 3: launch_relu<K, 3>(relu, g, st, p); break;
-        default: launch_relu<K, 4>(relu, g, st, p); break;
+        case 1: launch_relu<K, 1>(relu, g, st, p, x...); break;
+        case 2: launch_relu<K, 2>(relu, g, st, p, x...); break;
+        case 3: launch_relu<K, 3>(relu, g, st, p, x...); break;
+        default: launch_relu<K, 4>(relu, g, st, p, x...); break;
     }
 }
 
@@ -902,6 +1037,89 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
     const dim3 grid((uint32_t)per_row, (uint32_t)a->rows);
     launch_hb<Rows>(hb, a->relu != 0, grid, st, p);
     return V1_LAUNCHED("score_rows");
+}
+
+// ---------------------------------------------- scoring without DeepGEMM
+extern "C" int v1_reduce_centers(const float* logits, int64_t logits_stride, const int32_t* lens, float* scores,
+                                 int32_t rows, int32_t maxp, void* stream) {
+    V1_REQUIRE(rows >= 0 && maxp >= 0, "reduce_centers: negative shape");
+    V1_REQUIRE(logits_stride >= 8ll * maxp, "reduce_centers: logits row stride below 8 * maxp");
+    if (rows == 0 || maxp == 0) return V1_OK;
+    hipLaunchKernelGGL(reduce_centers_kernel, dim3((uint32_t)cdiv(maxp, 256), (uint32_t)rows), dim3(256), 0,
+                       as_stream(stream), logits, logits_stride, lens, scores, maxp);
+    return V1_LAUNCHED("reduce_centers");
+}
+
+static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+extern "C" int64_t v1_coarse_workspace(int32_t rows, int32_t maxp, int64_t table_stride) {
+    if (rows <= 0 || maxp <= 0) return 0;
+    return align256(4ll * rows) + align256(4ll * rows * 8 * maxp) +
+           (table_stride == 0 ? v1_score_workspace(rows, 8 * maxp) : 0);
+}
+
+extern "C" int v1_coarse(const v1_coarse_args* a, void* stream) {
+    V1_REQUIRE(a != nullptr, "coarse: null args");
+    V1_REQUIRE(a->rows >= 0 && a->maxp >= 0 && a->maxp % 8 == 0, "coarse: maxp must be a non-negative multiple of 8");
+    V1_REQUIRE(a->heads >= 1 && a->heads <= 64, "coarse: heads must be in [1, 64]");
+    V1_REQUIRE(a->table_stride >= 0 && (a->table_stride == 0 || a->table_stride >= a->maxp / 8),
+               "coarse: center table row stride below maxp / 8");
+    if (a->rows == 0 || a->maxp == 0) return V1_OK;
+    const int64_t need = v1_coarse_workspace(a->rows, a->maxp, a->table_stride);
+    V1_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= need, "coarse: workspace of %lld bytes required",
+               (long long)need);
+    V1_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 255) == 0, "coarse: workspace must be 256-byte aligned");
+    uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+    int32_t* center_lens = reinterpret_cast<int32_t*>(ws);
+    float* logits = reinterpret_cast<float*>(ws + align256(4ll * a->rows));
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(center_lens_kernel, dim3((uint32_t)cdiv(a->rows, 256)), dim3(256), 0, st, a->lens, center_lens,
+                       a->rows, a->maxp);
+    int rc = V1_LAUNCHED("coarse: center lengths");
+    if (rc != V1_OK) return rc;
+    // center logits of the built pages (columns past them -inf), then the max per page
+    v1_score_args sa{};
+    sa.q = a->q;
+    sa.kv_pages = a->centers;
+    sa.kv_blocks = a->center_blocks;
+    sa.weights = a->weights;
+    sa.context_lens = center_lens;
+    sa.block_table = a->table;
+    sa.block_table_stride = a->table_stride;
+    sa.max_blocks = a->maxp / 8;
+    sa.logits = logits;
+    sa.logits_stride = 8ll * a->maxp;
+    sa.max_context_len = 8 * a->maxp;
+    sa.rows = a->rows;
+    sa.heads = a->heads;
+    sa.relu = a->relu;
+    sa.clean_logits = 1;
+    sa.workspace = ws + align256(4ll * a->rows) + align256(4ll * a->rows * 8 * a->maxp);
+    sa.workspace_bytes = a->workspace_bytes - (align256(4ll * a->rows) + align256(4ll * a->rows * 8 * a->maxp));
+    rc = v1_score(&sa, stream);
+    if (rc != V1_OK) return rc;
+    return v1_reduce_centers(logits, 8ll * a->maxp, a->lens, a->scores, a->rows, a->maxp, stream);
+}
+
+extern "C" int v1_fine(const v1_fine_args* a, void* stream) {
+    V1_REQUIRE(a != nullptr, "fine: null args");
+    V1_REQUIRE(a->heads >= 1 && a->heads <= 64, "fine: heads must be in [1, 64]");
+    V1_REQUIRE(a->rows >= 0 && a->width >= 0 && a->maxp >= 0 && a->np >= 0 && a->take_stride >= 0,
+               "fine: negative shape");
+    V1_REQUIRE(a->selected_bits == 32 || a->selected_bits == 64, "fine: selected must be int32 or int64");
+    V1_REQUIRE(a->fine_blocks > 0 && a->native_blocks > 0, "fine: empty pool");
+    V1_REQUIRE((reinterpret_cast<uintptr_t>(a->q) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->fine_pages) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(a->native_pages) & 15) == 0,
+               "fine: q and the pools must be 16-byte aligned");
+    V1_REQUIRE(a->sink >= 0 && a->window >= 0, "fine: negative sink or window");
+    if (a->rows == 0 || a->width == 0) return V1_OK;
+    ScoreParams p{a->q, a->fine_pages, a->fine_blocks, a->weights, a->lens, nullptr, 0, 0, a->scores, a->width,
+                  a->width, a->rows, a->heads, a->relu, 1, nullptr};
+    FineExtra f{a->native_pages, a->native_blocks, a->members, a->rt, a->nt, a->selected, a->selected_bits, a->takes,
+                a->maxp, a->np, a->take_stride, a->sink, a->window};
+    const dim3 grid((uint32_t)cdiv(cdiv(a->width, 64), 4), (uint32_t)a->rows);
+    launch_hb<Fine>((a->heads + 15) / 16, a->relu != 0, grid, as_stream(stream), p, f);
+    return V1_LAUNCHED("fine");
 }
 
 // ------------------------------------------------ allocation-free variant

@@ -7,10 +7,14 @@ and argument order (the reference itself swaps Triton kernels for objects with
 ignored.  Tensors passed as fp8 / fp32 views of one byte pool are used by
 their data pointer, exactly like the Triton kernels address them.
 """
+import ctypes
+
 import torch
 
 from . import _lib
+from ._workspace import workspace
 
+PAGE_BYTES = 8448
 _TRITON_OPTIONS = {"num_warps", "num_stages", "debug", "enable_fp_fusion", "num_ctas"}
 
 
@@ -209,6 +213,67 @@ def _expand_logical(grid, LOGICAL, OUT, TOPK, STRIDE, BLOCK):
               _stream(OUT))
 
 
+# --------------------------------------------- scoring without DeepGEMM
+def _pool(view, scales, name):
+    """Byte pointer and page count of a pool passed as its FP8 view and its
+    fp32 view (the same storage, kernels.py:205-207)."""
+    if view.data_ptr() != scales.data_ptr():
+        raise ValueError(f"{name}: the FP8 and fp32 views must be the same pool")
+    if not view.is_contiguous() or (view.numel() * view.element_size()) % PAGE_BYTES:
+        raise ValueError(f"{name}: the pool must be contiguous whole 8448-byte pages")
+    return _lib.ptr(view), view.numel() * view.element_size() // PAGE_BYTES
+
+
+def _reduce_centers(grid, LOGITS, LENS, SCORES, MAXP, STRIDE):
+    """kernels.py:475-486: SCORES[r, p] = max of LOGITS[r, 8p..8p+7] for pages
+    below max(n-1, 0) // 1024 * 16, else -inf."""
+    _lib.require_gpu(LOGITS, LENS, SCORES)
+    if LOGITS.dtype != torch.float32 or SCORES.dtype != torch.float32 or LENS.dtype != torch.int32:
+        raise ValueError("reduce_centers: LOGITS / SCORES float32, LENS int32")
+    _lib.call("v1_reduce_centers", _lib.ptr(LOGITS), int(STRIDE), _lib.ptr(LENS), _lib.ptr(SCORES), grid[0],
+              int(MAXP), _stream(SCORES))
+
+
+def _coarse(grid, Q, W, C, CS, TABLE, LENS, SCORES, MAXP, H, RELU):
+    """kernels.py:182-221 (called at runtime.py:453-466): page scores as the
+    max of their 8 center logits, through the FP8 scoring kernel."""
+    _lib.require_gpu(Q, W, C, LENS, SCORES, TABLE)
+    rows = grid[0]
+    centers, blocks = _pool(C, CS, "coarse")
+    if TABLE.dtype != torch.int32 or TABLE.dim() != 2 or TABLE.stride(1) != 1:
+        raise ValueError("coarse: TABLE must be an int32 [rows, MAXP // 8] table")
+    if Q.element_size() != 1 or not Q.is_contiguous() or Q.numel() != rows * int(H) * 128:
+        raise ValueError("coarse: Q must be a contiguous FP8 [rows, H, 128] tensor")
+    need = _lib.lib().v1_coarse_workspace(rows, int(MAXP), TABLE.stride(0))
+    ws, ws_bytes = workspace(Q.device, need, "coarse")
+    a = _lib.CoarseArgs(_lib.ptr(Q), _lib.ptr(W), centers, blocks, _lib.ptr(TABLE), TABLE.stride(0), _lib.ptr(LENS),
+                        _lib.ptr(SCORES), rows, int(H), int(MAXP), int(bool(RELU)), ws, ws_bytes)
+    _lib.check(_lib.lib().v1_coarse(ctypes.byref(a), _stream(SCORES)), "coarse")
+
+
+def _fine(grid, Q, W, K, KS, NATIVE, NS, MEMBERS, RT, NT, SELECTED, LENS, TAKES, SCORES, MAXP, NP, TAKE, WIDTH, SINK,
+          WINDOW, H, RELU):
+    """kernels.py:248-320 (called at runtime.py:565-590): fine candidates
+    scored straight from the fine and native pools."""
+    _lib.require_gpu(Q, W, K, NATIVE, MEMBERS, RT, NT, SELECTED, LENS, TAKES, SCORES)
+    rows = grid[0]
+    fine, fine_blocks = _pool(K, KS, "fine")
+    native, native_blocks = _pool(NATIVE, NS, "fine")
+    if MEMBERS.dtype != torch.int32 or not MEMBERS.is_contiguous() or MEMBERS.numel() % 64:
+        raise ValueError("fine: MEMBERS must be a contiguous int32 [pages, 64] tensor")
+    fine_blocks = min(fine_blocks, MEMBERS.numel() // 64)  # pages with a member row
+    if Q.element_size() != 1 or not Q.is_contiguous() or Q.numel() != rows * int(H) * 128:
+        raise ValueError("fine: Q must be a contiguous FP8 [rows, H, 128] tensor")
+    a = _lib.FineArgs(_lib.ptr(Q), _lib.ptr(W), fine, fine_blocks, native, native_blocks, _lib.ptr(MEMBERS),
+                      _lib.ptr(RT), _lib.ptr(NT), _lib.ptr(SELECTED), _sel_bits(SELECTED), _lib.ptr(LENS),
+                      _lib.ptr(TAKES), _lib.ptr(SCORES), rows, int(H), int(MAXP), int(NP), int(TAKE), int(WIDTH),
+                      int(SINK), int(WINDOW), int(bool(RELU)))
+    _lib.check(_lib.lib().v1_fine(ctypes.byref(a), _stream(SCORES)), "fine")
+
+
+reduce_centers = _Kernel("reduce_centers", _reduce_centers)
+coarse = _Kernel("coarse", _coarse)
+fine = _Kernel("fine", _fine)
 mask_fine = _Kernel("mask_fine", _mask_fine)
 output_ids = _Kernel("output_ids", _output_ids)
 expand_logical = _Kernel("expand_logical", _expand_logical)

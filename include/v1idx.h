@@ -187,6 +187,76 @@ int64_t v1_score_noalloc_capacity(void);
 int v1_score_noalloc(const v1_score_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Scoring without DeepGEMM: the reference's Triton fallbacks, used when
+ * DeepGEMM is absent or the query optimisations are off
+ * (sglang/srt/layers/attention/v1_deepseek/runtime.py:450-466, 565-590).
+ *
+ * reduce_centers (kernels.py:475-486): scores[r, p] = max of
+ * logits[r, 8p .. 8p+7] for p < max(lens[r]-1, 0) / 1024 * 16, else -inf;
+ * scores is [rows, maxp].
+ * ---------------------------------------------------------------------- */
+int v1_reduce_centers(const float* logits, int64_t logits_stride, const int32_t* lens, float* scores,
+                      int32_t rows, int32_t maxp, void* stream);
+
+/* coarse (kernels.py:182-221): center page table[r, b] holds the 64 centers
+ * of pages 8b..8b+7; a page scores the max of its 8 centers'
+ * sum_h w relu(q . c) s_c for pages below max(lens[r]-1, 0) / 1024 * 16 (at
+ * most maxp), else -inf.  Runs as center logits (v1_score over the row's
+ * centers) reduced by v1_reduce_centers, in the caller's workspace. */
+typedef struct {
+    const uint8_t* q;             /* [rows, heads, 128] e4m3fn */
+    const float* weights;         /* [rows, heads] */
+    const uint8_t* centers;       /* center pages [center_blocks, 8448] */
+    int64_t center_blocks;
+    const int32_t* table;         /* [rows, maxp / 8] center pages, row stride table_stride (0: shared) */
+    int64_t table_stride;
+    const int32_t* lens;          /* [rows] tokens */
+    float* scores;                /* [rows, maxp] */
+    int32_t rows;
+    int32_t heads;
+    int32_t maxp;                 /* multiple of 8 */
+    int32_t relu;
+    void* workspace;              /* >= v1_coarse_workspace(rows, maxp, table_stride) bytes, 256-byte aligned */
+    int64_t workspace_bytes;
+} v1_coarse_args;
+int64_t v1_coarse_workspace(int32_t rows, int32_t maxp, int64_t table_stride);
+int v1_coarse(const v1_coarse_args* a, void* stream);
+
+/* fine (kernels.py:248-320): scores[r, i] for i < width.  i < take * 64 is
+ * slot i % 64 of fine page rt[r, selected[r, i / 64]], kept when its logical
+ * position members[page][slot] lies in [sink, tail) and below lens[r]; the
+ * next sink + n - tail candidates are the sink and tail tokens read from
+ * native pages nt[r, logical / 64]; -inf elsewhere (also for ranks, pages or
+ * logical pages outside their tables).  sink = min(n, sink_cap), tail as the
+ * reference's query_lengths. */
+typedef struct {
+    const uint8_t* q;             /* [rows, heads, 128] e4m3fn */
+    const float* weights;         /* [rows, heads] */
+    const uint8_t* fine_pages;    /* fine pool [fine_blocks, 8448] */
+    int64_t fine_blocks;
+    const uint8_t* native_pages;  /* native pool [native_blocks, 8448] */
+    int64_t native_blocks;
+    const int32_t* members;       /* [fine_blocks, 64] logical positions */
+    const int32_t* rt;            /* [rows, maxp] reordered table */
+    const int32_t* nt;            /* [rows, np] native table */
+    const void* selected;         /* [rows, take_stride] ranks, int32 or int64 */
+    int32_t selected_bits;
+    const int32_t* lens;          /* [rows] tokens */
+    const int32_t* takes;         /* [rows] */
+    float* scores;                /* [rows, width] */
+    int32_t rows;
+    int32_t heads;
+    int32_t maxp;
+    int32_t np;
+    int32_t take_stride;
+    int32_t width;
+    int32_t sink;
+    int32_t window;
+    int32_t relu;
+} v1_fine_args;
+int v1_fine(const v1_fine_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
  * _gather_slots: logical -> req[logical] -> K and V rows of one head into
  * contiguous [rows, top, 128] outputs; ids < 0 give zero rows.
  * Replaces sglang/srt/layers/attention/v1_native/kernels.py:62-77 (_gather_slots)

@@ -564,6 +564,77 @@ def paged_logits(q8, w, native, block_table, lens, max_len, relu=True, clean=Tru
     return out
 
 
+# --------------------------------------------- scoring without DeepGEMM
+# The reference's Triton fallbacks when DeepGEMM is absent or the query
+# optimisations are off (runtime.py:450-466, 565-590).
+def reduce_centers(logits, lens, maxp):
+    """sglang/srt/layers/attention/v1_deepseek/kernels.py:475-486: page p of a
+    row scores the max of its 8 center logits (columns 8p..8p+7) for p below
+    pages(n) = max(n-1, 0) // 1024 * 16, else -inf; [rows, maxp] fp32."""
+    rows = logits.shape[0]
+    out = np.full((rows, maxp), NEG_INF, dtype=np.float32)
+    for r in range(rows):
+        pages = min(tdiv(max(int(lens[r]) - 1, 0), 1024) * 16, maxp)
+        if pages > 0:
+            out[r, :pages] = np.fmax.reduce(np.asarray(logits[r, :pages * 8], dtype=np.float32).reshape(pages, 8),
+                                            axis=1)
+    return out
+
+
+def coarse(q8, w, centers, table, lens, maxp, relu=True):
+    """kernels.py:182-221: center page table[r, b] holds the 64 centers of
+    pages 8b..8b+7 (8 each); a page scores the max of its centers'
+    sum_h w relu(q . c) s_c, for pages below pages(n), else -inf.  Restated
+    as the center logits of each row's pages(n) * 8 centers followed by
+    reduce_centers."""
+    pages = np.array([min(tdiv(max(int(n) - 1, 0), 1024) * 16, maxp) for n in lens], dtype=np.int64)
+    logits = paged_logits(q8, w, centers, np.asarray(table), pages * 8, maxp * 8, relu=relu)
+    return reduce_centers(logits, lens, maxp)
+
+
+def fine(q8, w, fine_pool, native, members, rt, nt, selected, lens, takes, width, sink_cap, window, relu=True,
+         magnitude=False):
+    """kernels.py:248-320: candidate i of a row is slot i % 64 of fine page
+    rt[selected[i // 64]] for i < take * 64 (kept when its logical position
+    members[page, slot] lies in [sink, tail) and below n), then the sink and
+    tail tokens read straight from the native pool (logical i' for
+    i' = i - take * 64 < sink, else tail + i' - sink, kept below count);
+    score = sum_h w relu(q . k) s_k in fp64, -inf where not kept.
+    magnitude=True gives sum_h |w| sum_d |q k| s_k at the kept candidates."""
+    rows = q8.shape[0]
+    qf = e4m3_decode(q8).astype(np.float64)
+    pools = (fine_pool, native)
+    keys = [p[:, :8192].reshape(-1, 64, 128) for p in pools]
+    scales = [p[:, 8192:].copy().view(np.float32).reshape(-1, 64) for p in pools]
+    out = np.full((rows, width), -np.inf, dtype=np.float64)
+    for r in range(rows):
+        n, take = int(lens[r]), int(takes[r])
+        sink, tail = _bounds(n, window, sink_cap)
+        count = take * 64 + sink + n - tail
+        for i in range(min(width, max(count, 0))):
+            if i < take * 64:
+                src, page, slot = 0, int(rt[r, int(selected[r, i // 64])]), i % 64
+                logical = int(members[page, slot])
+                keep = sink <= logical < tail and logical < n
+            else:
+                off = i - take * 64
+                logical = off if off < sink else tail + off - sink
+                src, page, slot = 1, int(nt[r, logical // 64]), logical % 64
+                keep = logical < n
+            if not keep:
+                continue
+            k = e4m3_decode(keys[src][page, slot]).astype(np.float64)
+            s = float(scales[src][page, slot])
+            if magnitude:
+                out[r, i] = float((np.abs(w[r].astype(np.float64)) * (np.abs(qf[r]) @ np.abs(k))).sum()) * s
+                continue
+            dots = qf[r] @ k
+            if relu:
+                dots = np.maximum(dots, 0.0)
+            out[r, i] = float((w[r].astype(np.float64) * dots).sum()) * s
+    return out
+
+
 # ------------------------------------------------------------ index build
 # The producer of the pages the query path reads: per 1024-token bucket
 # (16 native pages), unit vectors, a balanced cosine bisection into groups of

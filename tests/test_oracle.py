@@ -653,3 +653,80 @@ def test_expand_logical_kat_and_fused_equality(example_after_route):
     out = np.full(res["expanded"].shape, 7, np.int32)
     O.expand_logical(res["logical"], out)
     assert np.array_equal(out, res["expanded"])
+
+
+# ------------------------------------------- scoring without DeepGEMM
+def test_reduce_centers_by_hand():
+    """kernels.py:475-486: page p of a row = max of center logits 8p..8p+7 for
+    p < max(n-1, 0) // 1024 * 16 (capped at maxp), -inf elsewhere."""
+    logits = np.full((3, 160), -5.0, np.float32)
+    logits[0, :128] = np.arange(128, dtype=np.float32)  # page p: max 8p + 7
+    logits[1, :128] = -np.arange(128, dtype=np.float32)  # page p: max -8p
+    logits[1, 9] = -np.inf
+    got = O.reduce_centers(logits, np.array([2049, 1025, 1024]), 20)
+    # row 0: 32 pages capped at maxp 20; logits past column 127 are -5
+    exp0 = np.array([8 * p + 7 if p < 16 else -5 for p in range(20)], np.float32)
+    assert np.array_equal(got[0], exp0)
+    # row 1: 16 pages; page 1's center 9 is -inf, the max is still -8
+    exp1 = np.array([-8.0 * p if p < 16 else -np.inf for p in range(20)], np.float32)
+    assert np.array_equal(got[1], exp1)
+    # row 2: n = 1024 gives no built page
+    assert np.all(np.isneginf(got[2]))
+
+
+def test_coarse_by_brute_force():
+    """kernels.py:182-221 by explicit loops: center page table[r, b] holds the
+    centers of pages 8b..8b+7, page p = max over its 8 centers g of
+    sum_h w_h relu(q_h . c) s_c, -inf from pages(n) on."""
+    g = np.random.default_rng(77)
+    c8, cs = W.quantize_rows(g.standard_normal((3 * 64, 128)).astype(np.float32))
+    centers = W.pack_pages(c8, cs)  # 3 center pages
+    q8, _ = W.quantize_rows(g.standard_normal((2 * 3, 128)).astype(np.float32))
+    q8 = q8.reshape(2, 3, 128)
+    w = g.random((2, 3)).astype(np.float32)
+    table = np.array([[2, 0], [1, 2]], np.int32)  # maxp = 16: two center pages per row
+    lens = np.array([1025, 4000])  # 16 pages for both (capped at maxp)
+    got = O.coarse(q8, w, centers, table, lens, 16)
+    qf = O.e4m3_decode(q8).astype(np.float64)
+    for r in range(2):
+        for p in range(16):
+            page = table[r, p // 8]
+            best = -np.inf
+            for c in range(8):
+                slot = (p % 8) * 8 + c
+                k = O.e4m3_decode(c8[page * 64 + slot]).astype(np.float64)
+                v = sum(float(w[r, h]) * max(float(qf[r, h] @ k), 0.0) for h in range(3)) * float(cs[page * 64 + slot])
+                best = max(best, v)
+            assert np.isclose(got[r, p], best, rtol=1e-6, atol=0), (r, p)
+    # a request of one bucket (n = 1025) has 16 pages; n = 1024 has none
+    assert np.all(np.isneginf(O.coarse(q8, w, centers, table, np.array([1024, 1]), 16)))
+
+
+def test_fine_equals_staged_table_scoring_with_mask():
+    """kernels.py:248-320 against the optimised path built from pinned pieces:
+    fine_table + stage_tail (scratch pages per row) + paged_logits over the
+    fine table + mask_fine (kernels.py:379-441, 444-472) give the same scores,
+    including rows whose take is 0, rows shorter than the built pages and
+    candidates past count."""
+    wl = W.config1(rows=6)
+    a, prm = wl.arrays, wl.params
+    B, CAP, TAKE, WIDTH, SINK, WINDOW = prm["B"], prm["CAP"], prm["TAKE"], prm["WIDTH"], prm["SINK"], prm["WINDOW"]
+    g = np.random.default_rng(8)
+    lens = np.array([4097, 4097, 3073, 2100, 1500, 4097], np.int32)
+    takes = np.array([40, 0, 17, 24, 3, 40], np.int32)
+    selected = np.stack([g.permutation(64)[:TAKE] for _ in range(B)]).astype(np.int32)
+    scratch = 68
+    fine = np.zeros((CAP + B * scratch, a["fine"].shape[1]), np.uint8)
+    fine[:CAP] = a["fine"][:CAP]
+    ft = O.fine_table(a["rt"], selected, takes, TAKE + scratch, CAP, scratch)
+    O.stage_tail(a["native"], a["nt"], lens, fine, CAP, scratch, SINK, WINDOW)
+    count = np.array([t * 64 + O._bounds(int(n), WINDOW, SINK)[0] + int(n) - O._bounds(int(n), WINDOW, SINK)[1]
+                      for n, t in zip(lens, takes)])
+    staged = O.paged_logits(a["q8"], a["w"], fine, ft, np.minimum(count, WIDTH), WIDTH)
+    O.mask_fine(staged, selected, a["rt"], a["members"], lens, takes, WIDTH, SINK, WINDOW)
+    got = O.fine(a["q8"], a["w"], fine, a["native"], a["members"], a["rt"], a["nt"], selected, lens, takes, WIDTH,
+                 SINK, WINDOW)
+    assert np.array_equal(np.isneginf(got), np.isneginf(staged))
+    fin = np.isfinite(staged)
+    assert fin.sum() > 5000
+    assert np.allclose(got[fin], staged[fin], rtol=1e-12, atol=0)
