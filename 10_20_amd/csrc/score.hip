@@ -32,6 +32,10 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
+// Word 3 of a raw buffer descriptor (stride 0, 32-bit dwords).  Accesses at
+// byte offsets at or past the descriptor's length are range-checked by the
+// hardware: loads return zeros and stores are dropped.
+constexpr int32_t kRawDword = 0x00020000;
 constexpr int kChunkPages = 16;                      // pages per work-group
 constexpr int kQueriesPerWave = 2;
 constexpr int kQueriesPerGroup = 4 * kQueriesPerWave;
@@ -106,44 +110,59 @@ static_assert(kRecWeights % 16 == 0 && kRecBound % 16 == 0 && kPieceRowBytes % 1
 // about 2^-H of the keys on the exact path.
 constexpr float kExactFrac = 1.0f / 4096.0f;
 
+// Reductions over a wave: a DPP butterfly within each row of 16 lanes, then
+// the four row results read out and combined; the result is wave-uniform.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, false));
+}
+
+template <typename Op>
+__device__ __forceinline__ float wave_all(float v, Op op) {
+    v = op(v, dpp_mov<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = op(v, dpp_mov<0x4e>(v));   // quad_perm [2,3,0,1]
+    v = op(v, dpp_mov<0x141>(v));  // row_half_mirror: the other quad of the half row
+    v = op(v, dpp_mov<0x140>(v));  // row_mirror: the other half row
+    auto row = [&](int lane) __attribute__((always_inline)) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+    };
+    return op(op(row(0), row(16)), op(row(32), row(48)));
+}
+
 // One wave per query row: q' = sum_h w_h q_h split into its pieces, and the
 // record described above.
 __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float* w, int32_t rows, int32_t heads,
                                                   int32_t relu, uint8_t* out, uint32_t* work, uint32_t* exact_pages,
                                                   int32_t exact_words) {
-    const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int l = __lane_id();
     if (blockIdx.x == 0 && threadIdx.x == 0) *work = 0u;  // the work counter of score_shared
     if (row >= rows) return;
     for (int k = l; k < exact_words; k += kWave) exact_pages[row * exact_words + k] = 0u;
-    // lane l owns dims 2l, 2l+1
+    // lane l owns dims 2l, 2l+1; every head's two bytes come in one round
+    // trip of buffer loads over the query row (heads past `heads` read as
+    // zeros), lane h holds head h's weight, and the sums run in head order.
+    // v_cvt_pk_f32_fp8 decodes OCP e4m3fn exactly (NaN codes to NaN).
     float a0 = 0.f, a1 = 0.f, bound = 0.f;
-    for (int h0 = 0; h0 < heads; h0 += 16) {
-        // 16 heads' loads in flight (indices clamped, weights of missing heads zeroed)
-        float wh[16];
-        uint32_t b[16];
+    const float wl = w[row * heads + min(l, heads - 1)];
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(q + row * heads * 128), 0, heads * 128,
+                                                      kRawDword);
+    uint32_t b[64];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int h = min(h0 + j, heads - 1);
-            const float v = w[row * heads + h];
-            wh[j] = (h0 + j < heads) ? v : 0.f;
-            b[j] = *reinterpret_cast<const uint16_t*>(q + (row * heads + h) * 128 + 2 * l);
-        }
+    for (int j = 0; j < 64; ++j) b[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, 2 * l, j * 128, 0);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float x0 = e4m3_value(b[j] & 0xff), x1 = e4m3_value(b[j] >> 8);
-            a0 = fmaf(wh[j], x0, a0);
-            a1 = fmaf(wh[j], x1, a1);
-            bound = fmaf(fabsf(wh[j]), fabsf(x0) + fabsf(x1), bound);
-        }
+    for (int j = 0; j < 64; ++j) {
+        const float wh = j < heads ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j))
+                                   : 0.f;
+        const auto x = __builtin_amdgcn_cvt_pk_f32_fp8((int)b[j], false);
+        a0 = fmaf(wh, x[0], a0);
+        a1 = fmaf(wh, x[1], a1);
+        bound = fmaf(fabsf(wh), fabsf(x[0]) + fabsf(x[1]), bound);
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) bound += __shfl_xor(bound, off, kWave);
+    bound = wave_all(bound, [](float x, float y) { return x + y; });
     uint8_t* dst = out + row * kPieceRowBytes;
     for (int pc = 0; pc < kPieces; ++pc) {
-        float m = fmaxf(fabsf(a0), fabsf(a1));
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+        const float m = wave_all(fmaxf(fabsf(a0), fabsf(a1)), [](float x, float y) { return fmaxf(x, y); });
         // scale: smallest power of two >= m / 448 (1 when the residual is zero)
         float sc = 1.f;
         if (m > 0.f) {
@@ -271,10 +290,6 @@ __device__ __forceinline__ int key_swizzle(int k) { return (k ^ (k >> 3)) & 7; }
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-// Word 3 of a raw buffer descriptor (stride 0, 32-bit dwords).  Accesses at
-// byte offsets at or past the descriptor's length are range-checked by the
-// hardware: loads return zeros and stores are dropped.
-constexpr int32_t kRawDword = 0x00020000;
 
 // Raw buffer descriptor over one native page.
 __device__ __forceinline__ i32x4 page_rsrc(const uint8_t* kv, int32_t page) {
