@@ -27,7 +27,11 @@ _gather_slots = _Kernel("_gather_slots", _gather_launch)
 
 
 class GatherWorkspace:
-    """Backend-owned bounded scratch, reused across requests/heads/layers."""
+    """The gathered K and V of up to `rows` decode queries x 2048 slots, held
+    by the attention backend and reused by every call (sglang/srt/layers/
+    attention/v1_native/kernels.py:80-111 is the interface): the buffers are
+    made on first use, `gather` fills the first len(ids) rows and returns them,
+    and a batch larger than `rows` is an error."""
 
     def __init__(self, rows, device, dtype):
         self.rows, self.device, self.dtype = rows, device, dtype

@@ -85,6 +85,20 @@ KATS = {
     },
 }
 
+
+def example_permutations():
+    """The example's two page permutations: the first two draws of a CPU
+    torch.Generator seeded 19 (native table over P pages, then the reordered
+    pool over CAP pages), stored as data so the tests need no RNG replay."""
+    import torch
+    gen = torch.Generator().manual_seed(KATS["route_example"]["seed"])
+    native = torch.randperm(KATS["route_example"]["P"], generator=gen).tolist()
+    reorder = torch.randperm(KATS["route_example"]["CAP"], generator=gen).tolist()
+    return native, reorder
+
+
+KATS["route_example"]["native_pages"], KATS["route_example"]["reorder_pages"] = example_permutations()
+
 if __name__ == "__main__":
     out = Path(__file__).with_name("reference_kats.json")
     out.write_text(json.dumps(KATS, indent=1) + "\n")

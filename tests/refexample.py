@@ -1,18 +1,21 @@
-"""Inputs of the reference's single-head query example, rebuilt with torch on
-the CPU (torch.Generator seeded 19, as in
-sglang/srt/layers/attention/v1_deepseek/example_v1_query_single_head.py:11-54):
-unique non-negative dot products, one K head, members reversed inside each
-1K bucket, 64 built pages of a 128-page reordered pool.
+"""Inputs of the reference's single-head query example
+(sglang/srt/layers/attention/v1_deepseek/example_v1_query_single_head.py:11-54),
+built on the CPU from the fixture's page permutations: unique non-negative dot
+products, one K head, members reversed inside each 1K bucket, 64 built pages of
+a 128-page reordered pool.
 """
+import json
+from pathlib import Path
+
 import torch
 
 B, P, CAP, TAKE, N, TOP, WINDOW, SINK = 1024, 128, 128, 40, 4097, 2048, 64, 64
+_EXAMPLE = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())["route_example"]
 
 
 def route_inputs(rows=B):
-    gen = torch.Generator().manual_seed(19)
-    native_pages = torch.randperm(P, generator=gen).to(torch.int32)
-    reorder_pages = torch.randperm(CAP, generator=gen).to(torch.int32)
+    native_pages = torch.tensor(_EXAMPLE["native_pages"], dtype=torch.int32)
+    reorder_pages = torch.tensor(_EXAMPLE["reorder_pages"], dtype=torch.int32)
     nt = native_pages[None].expand(rows, -1).contiguous()
     rt = reorder_pages[None].expand(rows, -1).contiguous()
     k = torch.zeros((N, 128))
