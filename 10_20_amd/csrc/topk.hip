@@ -240,11 +240,19 @@ __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_
         Radix rx;
         rx.start(smax, smin, 1);
         const int lo = rx.shift > kDigitBits ? rx.shift - kDigitBits : 0;
+        // (the empty asm keeps the bin addresses from being computed once
+        // before the caller's attempt loop and held, spilled, across the stream)
+        uint32_t k[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            k[e] = sk[e];
+            asm volatile("" : "+v"(k[e]));
+        }
         clear_hist(sm);
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            if (sk[e] > kNegInfKey) atomicAdd(&sm.hist[(sk[e] >> lo) & (kHist - 1u)], 1u);
+            if (k[e] > kNegInfKey) atomicAdd(&sm.hist[(k[e] >> lo) & (kHist - 1u)], 1u);
         __syncthreads();
         const uint32_t want = (uint32_t)min((float)scnt, (float)scnt * (float)T * target / (float)n + 16.f);
         uint32_t bin, above;
@@ -265,8 +273,8 @@ __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_
             __syncthreads();
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                if (sk[e] > kNegInfKey && ((sk[e] >> lo) & (kHist - 1u)) == bin && (sk[e] & rx.pmask) == rx.prefix)
-                    atomicAdd(&sm.hist[(sk[e] >> lo2) & ((1u << (lo - lo2)) - 1u)], 1u);
+                if (k[e] > kNegInfKey && ((k[e] >> lo) & (kHist - 1u)) == bin && (k[e] & rx.pmask) == rx.prefix)
+                    atomicAdd(&sm.hist[(k[e] >> lo2) & ((1u << (lo - lo2)) - 1u)], 1u);
             __syncthreads();
             uint32_t bin2, above2;
             find_bin(want - above, sm, bin2, above2);
