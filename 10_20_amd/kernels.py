@@ -224,12 +224,23 @@ def _pool(view, scales, name):
     return _lib.ptr(view), view.numel() * view.element_size() // PAGE_BYTES
 
 
+def _holds(t, dtype, count, name):
+    """t is a contiguous `dtype` tensor of at least `count` elements (the
+    kernels address these buffers by row strides of their own)."""
+    if t.dtype != dtype or not t.is_contiguous() or t.numel() < count:
+        raise ValueError(f"{name} must be a contiguous {dtype} tensor of at least {count} elements")
+
+
 def _reduce_centers(grid, LOGITS, LENS, SCORES, MAXP, STRIDE):
     """kernels.py:475-486: SCORES[r, p] = max of LOGITS[r, 8p..8p+7] for pages
     below max(n-1, 0) // 1024 * 16, else -inf."""
     _lib.require_gpu(LOGITS, LENS, SCORES)
-    if LOGITS.dtype != torch.float32 or SCORES.dtype != torch.float32 or LENS.dtype != torch.int32:
-        raise ValueError("reduce_centers: LOGITS / SCORES float32, LENS int32")
+    rows, maxp = grid[0], int(MAXP)
+    if LOGITS.dtype != torch.float32 or LOGITS.stride(-1) != 1 or (rows > 0 and LOGITS.numel() < (rows - 1) * int(STRIDE)
+                                                                    + 8 * maxp):
+        raise ValueError("reduce_centers: LOGITS must be float32 rows of STRIDE elements holding 8 * MAXP logits")
+    _holds(LENS, torch.int32, rows, "reduce_centers: LENS")
+    _holds(SCORES, torch.float32, rows * maxp, "reduce_centers: SCORES")
     _lib.call("v1_reduce_centers", _lib.ptr(LOGITS), int(STRIDE), _lib.ptr(LENS), _lib.ptr(SCORES), grid[0],
               int(MAXP), _stream(SCORES))
 
@@ -244,6 +255,11 @@ def _coarse(grid, Q, W, C, CS, TABLE, LENS, SCORES, MAXP, H, RELU):
         raise ValueError("coarse: TABLE must be an int32 [rows, MAXP // 8] table")
     if Q.element_size() != 1 or not Q.is_contiguous() or Q.numel() != rows * int(H) * 128:
         raise ValueError("coarse: Q must be a contiguous FP8 [rows, H, 128] tensor")
+    if TABLE.shape[0] < rows or TABLE.shape[1] < int(MAXP) // 8:
+        raise ValueError("coarse: TABLE must hold MAXP // 8 center pages per row")
+    _holds(W, torch.float32, rows * int(H), "coarse: W")
+    _holds(LENS, torch.int32, rows, "coarse: LENS")
+    _holds(SCORES, torch.float32, rows * int(MAXP), "coarse: SCORES")
     need = _lib.lib().v1_coarse_workspace(rows, int(MAXP), TABLE.stride(0))
     ws, ws_bytes = workspace(Q.device, need, "coarse")
     a = _lib.CoarseArgs(_lib.ptr(Q), _lib.ptr(W), centers, blocks, _lib.ptr(TABLE), TABLE.stride(0), _lib.ptr(LENS),
@@ -264,6 +280,13 @@ def _fine(grid, Q, W, K, KS, NATIVE, NS, MEMBERS, RT, NT, SELECTED, LENS, TAKES,
     fine_blocks = min(fine_blocks, MEMBERS.numel() // 64)  # pages with a member row
     if Q.element_size() != 1 or not Q.is_contiguous() or Q.numel() != rows * int(H) * 128:
         raise ValueError("fine: Q must be a contiguous FP8 [rows, H, 128] tensor")
+    _holds(W, torch.float32, rows * int(H), "fine: W")
+    _holds(RT, torch.int32, rows * int(MAXP), "fine: RT")
+    _holds(NT, torch.int32, rows * int(NP), "fine: NT")
+    _holds(SELECTED, SELECTED.dtype, rows * int(TAKE), "fine: SELECTED")
+    _holds(LENS, torch.int32, rows, "fine: LENS")
+    _holds(TAKES, torch.int32, rows, "fine: TAKES")
+    _holds(SCORES, torch.float32, rows * int(WIDTH), "fine: SCORES")
     a = _lib.FineArgs(_lib.ptr(Q), _lib.ptr(W), fine, fine_blocks, native, native_blocks, _lib.ptr(MEMBERS),
                       _lib.ptr(RT), _lib.ptr(NT), _lib.ptr(SELECTED), _sel_bits(SELECTED), _lib.ptr(LENS),
                       _lib.ptr(TAKES), _lib.ptr(SCORES), rows, int(H), int(MAXP), int(NP), int(TAKE), int(WIDTH),
