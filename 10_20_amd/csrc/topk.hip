@@ -11,8 +11,8 @@
 // Design: one 512-thread work-group selects over up to 32768 positions with
 // under 40 KiB of LDS, so four work-groups (rows) share a CU and the HBM
 // streams of some rows overlap the LDS selection of others.
-//  1. 2048 keys sampled in 256 runs of 8 (a few percent of the row's cache
-//     lines) give a pivot that about 1.3*T of the row's keys exceed.
+//  1. 2048 keys sampled in 64 runs of 32 (one 128-byte line each: 8 KB of a
+//     row's lines) give a pivot that about 1.2*T of the row's keys exceed.
 //  2. One streaming pass, wave-independent (no barriers), sends every score at
 //     or above the pivot to an LDS candidate buffer (a float compare per score,
 //     ballot-counted slots per wave).
@@ -44,12 +44,12 @@ constexpr int kDigitBits = 11;          // radix digit width
 constexpr int kHist = 1 << kDigitBits;  // histogram bins, 4 per thread
 constexpr int kCandMax = 3584;
 constexpr int kCandPerThread = kCandMax / kBlock;  // 7
-constexpr int kSampleRuns = 256;                   // pivot sample: runs of 8 keys
+constexpr int kSampleRuns = 64;                    // pivot sample: runs of 32 keys (128 bytes)
 constexpr uint32_t kNegInfKey = 0x007fffffu;
 constexpr uint32_t kPosInfKey = 0xff800000u;  // key of +inf; keys above it are positive NaNs
 constexpr uint32_t kNegInfBits = 0xff800000u;  // float bits of -inf
 static_assert(kHist == 4 * kBlock && kWords % kBlock == 0 && kCandMax % kBlock == 0, "work split");
-static_assert(kSampleRuns * 8 == 4 * kBlock, "two threads per sample run");
+static_assert(kSampleRuns * 32 == 4 * kBlock, "eight threads per sample run");
 
 struct SelSmem {
     uint32_t hist[kHist];      // radix histograms; bitmap word prefixes
@@ -228,7 +228,7 @@ struct Ranker {
     }
 };
 
-// Pivot from the sampled keys sk (threads 2r, 2r+1 hold run r of 8 keys;
+// Pivot from the sampled keys sk (threads 8r..8r+7 hold run r of 32 keys;
 // block statistics smax / smin / scnt) such that about target * T of the n
 // keys are expected at or above it.  Ends with a barrier.
 __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_t smin, uint32_t scnt, int32_t n,
@@ -421,9 +421,11 @@ template <class Src, class Emit>
 __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emit& emit) {
     const int t = threadIdx.x, w = t / kWave, lane = __lane_id();
     const int32_t n = src.n;
-    // 1. pivot from 2048 sampled keys: threads 2r, 2r+1 read run r of 8 keys
+    // 1. pivot from 2048 sampled keys: threads 8r..8r+7 read run r of 32 keys,
+    //    one 128-byte line of the row (a line-sized run costs no more fetch
+    //    than a shorter one, and the stream re-reads the row anyway)
     uint32_t sk[4];
-    src.load4((int32_t)((((int64_t)(t >> 1) * n / kSampleRuns) & ~7ll) + 4 * (t & 1)), sk);
+    src.load4((int32_t)((((int64_t)(t >> 3) * n / kSampleRuns) & ~31ll) + 4 * (t & 7)), sk);
     uint32_t smax = 0, smin = 0xffffffffu, scnt = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) key_stats(sk[e], smax, smin, scnt);
