@@ -45,9 +45,14 @@ constexpr int kHist = 1 << kDigitBits;  // histogram bins, 4 per thread
 constexpr int kCandMax = 3584;
 constexpr int kCandPerThread = kCandMax / kBlock;  // 7
 constexpr int kSampleRuns = 64;                    // pivot sample: runs of 32 keys (128 bytes)
+constexpr int kTableBits = 6;                      // page size (log2) from which a row's table fits kBlock ints
 constexpr uint32_t kNegInfKey = 0x007fffffu;
 constexpr uint32_t kPosInfKey = 0xff800000u;  // key of +inf; keys above it are positive NaNs
 constexpr uint32_t kNegInfBits = 0xff800000u;  // float bits of -inf
+// Word 3 of a raw buffer descriptor (stride 0, 32-bit dwords): loads at byte
+// offsets at or past the descriptor's length return zeros.
+constexpr int32_t kRawDword = 0x00020000;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 static_assert(kHist == 4 * kBlock && kWords % kBlock == 0 && kCandMax % kBlock == 0, "work split");
 static_assert(kSampleRuns * 32 == 4 * kBlock, "eight threads per sample run");
 
@@ -60,7 +65,7 @@ struct SelSmem {
     uint32_t red[4 * kWaves];
     uint32_t bc[4];
     uint32_t ncand;
-    int32_t maskpage[kSpan / 64];  // V1 mask: page per selected rank, -1 when unmasked
+    int32_t maskpage[kSpan / 64];  // V1 mask: page per selected rank, -1 when unmasked; or a row's page table
 };
 static_assert(sizeof(SelSmem) <= 40 * 1024, "four work-groups per CU");
 
@@ -68,26 +73,29 @@ __device__ __forceinline__ uint32_t readlane(uint32_t v, int lane) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
 }
 
-__device__ __forceinline__ uint32_t block_incl_scan(uint32_t v, SelSmem& sm) {
-    const int w = threadIdx.x / kWave;
-    const uint32_t x = wave_inclusive_sum(v);
-    if (__lane_id() == kWave - 1) sm.red[w] = x;
-    __syncthreads();
-    uint32_t base = 0;
-#pragma unroll
-    for (int k = 0; k < kWaves; ++k) base += k < w ? sm.red[k] : 0u;
-    __syncthreads();
-    return base + x;
+// Wave-wide max (kOp 0), min (1) or sum (2) on DPP lane moves: row_shr
+// 1/2/4/8 inside each 16-lane row, then row_bcast 15 / 31 across rows, which
+// leaves the result in lane 63.
+template <int kOp>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v) {
+    constexpr int kId = kOp == 1 ? -1 : 0;
+    auto f = [](uint32_t a, uint32_t b) { return kOp == 0 ? max(a, b) : kOp == 1 ? min(a, b) : a + b; };
+    v = f(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
+    v = f(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
+    v = f(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x114, 0xf, 0xf, false));  // row_shr:4
+    v = f(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x118, 0xf, 0xf, false));  // row_shr:8
+    v = f(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v = f(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, kWave - 1);
 }
 
-// Block-wide max / min / count; every thread gets the result.
+// Block-wide max / min / count; every thread gets the result.  sm.red is read
+// after the one barrier: the caller passes another barrier before sm.red is
+// written again.
 __device__ __forceinline__ void block_stats(uint32_t& mx, uint32_t& mn, uint32_t& n, SelSmem& sm) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, kWave));
-        mn = min(mn, (uint32_t)__shfl_xor((int)mn, off, kWave));
-        n += (uint32_t)__shfl_xor((int)n, off, kWave);
-    }
+    mx = wave_reduce<0>(mx);
+    mn = wave_reduce<1>(mn);
+    n = wave_reduce<2>(n);
     const int w = threadIdx.x / kWave;
     if (__lane_id() == 0) {
         sm.red[w] = mx;
@@ -104,7 +112,10 @@ __device__ __forceinline__ void block_stats(uint32_t& mx, uint32_t& mn, uint32_t
         mn = min(mn, sm.red[kWaves + k]);
         n += sm.red[2 * kWaves + k];
     }
-    __syncthreads();
+    // (uniform: kept in scalar registers)
+    mx = __builtin_amdgcn_readfirstlane(mx);
+    mn = __builtin_amdgcn_readfirstlane(mn);
+    n = __builtin_amdgcn_readfirstlane(n);
 }
 
 __device__ __forceinline__ void key_stats(uint32_t k, uint32_t& mx, uint32_t& mn, uint32_t& n) {
@@ -115,34 +126,46 @@ __device__ __forceinline__ void key_stats(uint32_t k, uint32_t& mx, uint32_t& mn
 }
 
 // Descending scan of hist[0..kHist): the bin holding the `rank`-th largest
-// counted key, and the count above it.  Ends with a barrier.
-__device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& bin, uint32_t& above) {
-    const int t = threadIdx.x;
-    uint32_t h[4];
-    uint32_t local = 0;
+// counted key (1 <= rank <= the count), the count above it and the bin's own
+// count.  Wave 0 scans alone: lane l sums the 32 bins below kHist - 32 l
+// (eight 16-byte reads), a lane prefix finds the owning lane, and its 32 bins,
+// one per lane, a second prefix finds the bin.  Every bin read is zeroed, so
+// the histogram is clear for the next pass without a clearing step.  Call
+// after the barrier that completes the histogram; ends with a barrier.
+__device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& bin, uint32_t& above,
+                                         uint32_t& inbin) {
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        uint4* h4 = reinterpret_cast<uint4*>(sm.hist + kHist - 32 * (lane + 1));
+        uint32_t local = 0;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {  // thread t owns bins kHist-1-4t .. kHist-4-4t
-        h[b] = sm.hist[kHist - 1 - (4 * t + b)];
-        local += h[b];
-    }
-    const uint32_t incl = block_incl_scan(local, sm);
-    const uint32_t excl = incl - local;
-    if (excl < rank && rank <= incl) {
-        uint32_t acc = excl;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            if (acc + h[b] >= rank) {
-                sm.bc[0] = kHist - 1 - (4 * t + b);
-                sm.bc[1] = acc;
-                break;
-            }
-            acc += h[b];
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = h4[i];
+            local += v.x + v.y + v.z + v.w;
         }
+        const uint32_t incl = wave_inclusive_sum(local);
+        const uint64_t own = __builtin_amdgcn_ballot_w64(incl >= rank);
+        if (own != 0) {
+            const int L = (int)__builtin_ctzll(own);
+            const uint32_t excl = readlane(incl - local, L);
+            const uint32_t top = (uint32_t)(kHist - 1 - 32 * L);
+            const uint32_t c = lane < 32 ? sm.hist[top - lane] : 0u;
+            const uint32_t ci = wave_inclusive_sum(c);
+            const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < 32 && excl + ci >= rank);
+            if (lane == (int)__builtin_ctzll(hit)) {
+                sm.bc[0] = top - lane;
+                sm.bc[1] = excl + ci - c;
+                sm.bc[2] = c;
+            }
+        }
+        // (after the reads above: one wave's LDS accesses complete in order)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h4[i] = make_uint4(0u, 0u, 0u, 0u);
     }
     __syncthreads();
-    bin = sm.bc[0];
-    above = sm.bc[1];
-    __syncthreads();
+    bin = __builtin_amdgcn_readfirstlane(sm.bc[0]);
+    above = __builtin_amdgcn_readfirstlane(sm.bc[1]);
+    inbin = __builtin_amdgcn_readfirstlane(sm.bc[2]);
 }
 
 __device__ __forceinline__ void clear_hist(SelSmem& sm) {
@@ -168,10 +191,10 @@ struct Radix {
     __device__ __forceinline__ uint32_t digit(uint32_t k) const {
         return (k >> (shift - bits())) & ((1u << bits()) - 1u);
     }
-    // after the histogram of this pass is in sm.hist
+    // after the histogram of this pass is in sm.hist (and a barrier)
     __device__ __forceinline__ void finish(SelSmem& sm) {
-        uint32_t bin, above;
-        find_bin(remaining, sm, bin, above);
+        uint32_t bin, above, inbin;
+        find_bin(remaining, sm, bin, above, inbin);
         const int b = bits();
         shift -= b;
         remaining -= above;
@@ -248,18 +271,15 @@ __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_
             k[e] = sk[e];
             asm volatile("" : "+v"(k[e]));
         }
-        clear_hist(sm);
-        __syncthreads();
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             if (k[e] > kNegInfKey) atomicAdd(&sm.hist[(k[e] >> lo) & (kHist - 1u)], 1u);
         __syncthreads();
         const uint32_t want = (uint32_t)min((float)scnt, (float)scnt * (float)T * target / (float)n + 16.f);
-        uint32_t bin, above;
-        find_bin(want, sm, bin, above);
+        uint32_t bin, above, inbin;
+        find_bin(want, sm, bin, above, inbin);
         // Expected candidates with the pivot at the bin's lower edge (every
         // sample of the bin passes) or just above the bin (none passes).
-        const uint32_t inbin = sm.hist[bin];
         const uint64_t est_lo = (uint64_t)(above + inbin) * n / scnt, est_hi = (uint64_t)above * n / scnt;
         if (est_lo <= (uint64_t)kCandMax * 7 / 8 || lo == 0) {
             pivot = rx.prefix | (bin << lo);
@@ -268,22 +288,76 @@ __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_
         } else {
             // refine inside the bin on the next digit
             const int lo2 = lo > kDigitBits ? lo - kDigitBits : 0;
-            __syncthreads();
-            clear_hist(sm);
-            __syncthreads();
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (k[e] > kNegInfKey && ((k[e] >> lo) & (kHist - 1u)) == bin && (k[e] & rx.pmask) == rx.prefix)
                     atomicAdd(&sm.hist[(k[e] >> lo2) & ((1u << (lo - lo2)) - 1u)], 1u);
             __syncthreads();
-            uint32_t bin2, above2;
-            find_bin(want - above, sm, bin2, above2);
+            uint32_t bin2, above2, inbin2;
+            find_bin(want - above, sm, bin2, above2, inbin2);
             pivot = rx.prefix | (bin << lo) | (bin2 << lo2);
         }
         pivot = max(pivot, kNegInfKey + 1);
     }
-    __syncthreads();
     return pivot;
+}
+
+// The candidate test and LDS append for one wave's kBatch loads of 4 entries
+// (load u at step s0 + u * kWaves, lane's entries p..p+3).
+template <class Src, int kBatch>
+__device__ __forceinline__ void take_candidates(const uint32_t (&v)[kBatch][4], int32_t s0, uint32_t pivot,
+                                                bool float_test, float fpivot, SelSmem& sm) {
+    const int lane = __lane_id();
+    // slots are allocated per pair of batches (keeps the lane masks in
+    // scalar registers)
+#pragma unroll
+    for (int h = 0; h < kBatch; h += 2) {
+        bool c[2][4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            bool nan = false;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x = __uint_as_float(v[h + u][e]);
+                c[u][e] = Src::kFloats ? x >= fpivot : v[h + u][e] >= pivot;
+                nan |= x != x;
+            }
+            if (Src::kFloats && (!float_test || __builtin_amdgcn_ballot_w64(nan) != 0)) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) c[u][e] = score_key(__uint_as_float(v[h + u][e])) >= pivot;
+            }
+        }
+        uint64_t m[2][4];
+        uint32_t pre[2][4], total = 0;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                m[u][e] = __builtin_amdgcn_ballot_w64(c[u][e]);
+                pre[u][e] = total;
+                total += (uint32_t)__builtin_popcountll(m[u][e]);
+            }
+        if (total == 0) continue;
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&sm.ncand, total);
+        base = readlane(base, 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int32_t p = (s0 + (h + u) * kWaves) * 256 + 4 * lane;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (c[u][e]) {
+                    const uint32_t at = base + pre[u][e] +
+                        __builtin_amdgcn_mbcnt_hi((uint32_t)(m[u][e] >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)m[u][e], 0u));
+                    if (at < (uint32_t)kCandMax) {
+                        sm.cand_key[at] = v[h + u][e];
+                        sm.cand_pos[at] = (uint16_t)(p + e);
+                    }
+                }
+            }
+        }
+    }
 }
 
 // Step 2: every entry at or above the pivot goes to the LDS candidate buffer
@@ -292,68 +366,63 @@ __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_
 // agree on every non-NaN score, with -0 == +0) and stored as raw bits, which
 // the selection turns into keys; a wave batch holding a NaN, or a pivot in
 // the NaN key range, takes the exact key test.  Slots come from one LDS
-// allocation per wave and pair of batches (ballot counts, mbcnt ranks).  Each
-// wave keeps kBatch 1 KB loads in flight.
+// allocation per wave and pair of batches (ballot counts, mbcnt ranks).
+// Sources with a buffer descriptor (Src::kBuffer) are double-buffered: a
+// wave issues its next kBatch 1 KB loads before it tests the current ones,
+// so the load latency runs under the test; others load, then test.
 template <class Src>
-__device__ void stream_candidates(const Src& src, uint32_t pivot, SelSmem& sm) {
-    const int w = threadIdx.x / kWave, lane = __lane_id();
-    const int32_t steps = (src.n + 255) / 256;
+__device__ __forceinline__ void stream_candidates(const Src& src, uint32_t pivot, SelSmem& sm) {
+    // (the wave index as a scalar: the loop below branches per wave)
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = __lane_id();
+    const int32_t n = src.n;
+    const int32_t steps = (n + 255) / 256;
     constexpr int kBatch = 4;
+    constexpr int32_t kStride = kWaves * kBatch;  // steps per wave iteration
     const bool float_test = Src::kFloats && pivot <= kPosInfKey;
     const float fpivot = key_score(pivot);
-    for (int32_t s0 = w; s0 < steps; s0 += kWaves * kBatch) {
-        uint32_t v[kBatch][4];
+    if constexpr (Src::kBuffer) {
+        const auto rs = src.rsrc();
+        uint32_t a[kBatch][4], b[kBatch][4];
+        auto issue = [&](uint32_t (&x)[kBatch][4], int32_t s0) {
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) src.load_raw4((s0 + u * kWaves) * 256 + 4 * lane, v[u]);
-        // slots are allocated per pair of batches (keeps the lane masks in
-        // scalar registers)
-#pragma unroll
-        for (int h = 0; h < kBatch; h += 2) {
-            bool c[2][4];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                bool nan = false;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float x = __uint_as_float(v[h + u][e]);
-                    c[u][e] = Src::kFloats ? x >= fpivot : v[h + u][e] >= pivot;
-                    nan |= x != x;
-                }
-                if (Src::kFloats && (!float_test || __builtin_amdgcn_ballot_w64(nan) != 0)) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) c[u][e] = score_key(__uint_as_float(v[h + u][e])) >= pivot;
-                }
+            for (int u = 0; u < kBatch; ++u) {
+                const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * ((s0 + u * kWaves) * 256 + 4 * lane),
+                                                                      0, 0);
+                x[u][0] = r[0];
+                x[u][1] = r[1];
+                x[u][2] = r[2];
+                x[u][3] = r[3];
             }
-            uint64_t m[2][4];
-            uint32_t pre[2][4], total = 0;
+        };
+        // entries past n read as zeros: the wave holding the row's end sets them to -inf
+        auto take = [&](uint32_t (&x)[kBatch][4], int32_t s0) {
+            if ((s0 + (kBatch - 1) * kWaves + 1) * 256 > n) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < kBatch; ++u)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    m[u][e] = __builtin_amdgcn_ballot_w64(c[u][e]);
-                    pre[u][e] = total;
-                    total += (uint32_t)__builtin_popcountll(m[u][e]);
-                }
-            if (total == 0) continue;
-            uint32_t base = 0;
-            if (lane == 0) base = atomicAdd(&sm.ncand, total);
-            base = readlane(base, 0);
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int32_t p = (s0 + (h + u) * kWaves) * 256 + 4 * lane;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (c[u][e]) {
-                        const uint32_t at = base + pre[u][e] +
-                            __builtin_amdgcn_mbcnt_hi((uint32_t)(m[u][e] >> 32),
-                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m[u][e], 0u));
-                        if (at < (uint32_t)kCandMax) {
-                            sm.cand_key[at] = v[h + u][e];
-                            sm.cand_pos[at] = (uint16_t)(p + e);
-                        }
-                    }
-                }
+                    for (int e = 0; e < 4; ++e)
+                        if ((s0 + u * kWaves) * 256 + 4 * lane + e >= n) x[u][e] = kNegInfBits;
             }
+            take_candidates<Src, kBatch>(x, s0, pivot, float_test, fpivot, sm);
+        };
+        int32_t s0 = w;
+        if (s0 < steps) issue(a, s0);
+        while (s0 < steps) {
+            const int32_t s1 = s0 + kStride;
+            if (s1 < steps) issue(b, s1);
+            take(a, s0);
+            if (s1 >= steps) break;
+            const int32_t s2 = s1 + kStride;
+            if (s2 < steps) issue(a, s2);
+            take(b, s1);
+            s0 = s2;
+        }
+    } else {
+        for (int32_t s0 = w; s0 < steps; s0 += kStride) {
+            uint32_t v[kBatch][4];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) src.load_raw4((s0 + u * kWaves) * 256 + 4 * lane, v[u]);
+            take_candidates<Src, kBatch>(v, s0, pivot, float_test, fpivot, sm);
         }
     }
 }
@@ -378,8 +447,6 @@ __device__ void select_candidates(uint32_t ncand, uint32_t T, SelSmem& sm, const
         Radix rx;
         rx.start(cmax, cmin, T);
         while (rx.shift > 0) {
-            clear_hist(sm);
-            __syncthreads();
 #pragma unroll
             for (int i = 0; i < kCandPerThread; ++i)
                 if (rx.counts(ck[i], true)) atomicAdd(&sm.hist[rx.digit(ck[i])], 1u);
@@ -418,31 +485,50 @@ __device__ void select_candidates(uint32_t ncand, uint32_t T, SelSmem& sm, const
 // (p % 4 == 0), key 0 past n; src.load_raw4 the raw entries (float bits, -inf
 // past n, when Src::kFloats; else keys).  Ends with a barrier.
 template <class Src, class Emit>
+__device__ void select_exact(const Src& src, uint32_t T, SelSmem& sm, const Emit& emit);
+
+// Step 1's sample: thread t reads keys p..p+3 of run t / 8 of 32 keys, one
+// 128-byte line of the row (a line-sized run costs no more fetch than a
+// shorter one, and the stream re-reads the row anyway); 2048 keys in all.
+__device__ __forceinline__ int32_t sample_pos(int32_t n) {
+    const int t = threadIdx.x;
+    return (int32_t)((((int64_t)(t >> 3) * n / kSampleRuns) & ~31ll) + 4 * (t & 7));
+}
+
+template <class Src, class Emit>
+__device__ void select_sampled(const Src& src, const uint32_t (&sk)[4], uint32_t T, SelSmem& sm, const Emit& emit);
+
+template <class Src, class Emit>
 __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emit& emit) {
-    const int t = threadIdx.x, w = t / kWave, lane = __lane_id();
-    const int32_t n = src.n;
-    // 1. pivot from 2048 sampled keys: threads 8r..8r+7 read run r of 32 keys,
-    //    one 128-byte line of the row (a line-sized run costs no more fetch
-    //    than a shorter one, and the stream re-reads the row anyway)
     uint32_t sk[4];
-    src.load4((int32_t)((((int64_t)(t >> 3) * n / kSampleRuns) & ~31ll) + 4 * (t & 7)), sk);
+    src.load4(sample_pos(src.n), sk);
+    select_sampled(src, sk, T, sm, emit);
+}
+
+// select_stream with the pivot sample (the keys at sample_pos) given.
+template <class Src, class Emit>
+__device__ void select_sampled(const Src& src, const uint32_t (&sk)[4], uint32_t T, SelSmem& sm, const Emit& emit) {
+    const int t = threadIdx.x;
+    const int32_t n = src.n;
+    // LDS state of a selection: the histogram and the rank bitmaps start
+    // clear (the first barrier below orders these stores before any use)
+    clear_hist(sm);
+    Ranker::clear(sm);
+    if (t == 0) sm.ncand = 0;
+    // 1. pivot from the sample
     uint32_t smax = 0, smin = 0xffffffffu, scnt = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) key_stats(sk[e], smax, smin, scnt);
-    if (t == 0) sm.ncand = 0;
     block_stats(smax, smin, scnt, sm);
     // Pivot attempts: the first aims at 1.2 T candidates; after a miss the
     // target is corrected by the observed candidate count and the row is
     // streamed once more; a second miss takes the exact passes below.
-    const int32_t steps = (n + 255) / 256;
     float target = 1.2f;
     for (int attempt = 0; attempt < 2; ++attempt) {
         const uint32_t pivot = choose_pivot(sk, smax, smin, scnt, n, T, target, sm);
         stream_candidates(src, pivot, sm);
         __syncthreads();
-        const uint32_t ncand = sm.ncand;
-        Ranker::clear(sm);
-        __syncthreads();
+        const uint32_t ncand = __builtin_amdgcn_readfirstlane(sm.ncand);
         if (ncand >= T && ncand <= (uint32_t)kCandMax) {
             select_candidates<Src>(ncand, T, sm, emit);
             return;
@@ -450,11 +536,21 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emi
         if (scnt == 0 || smax == smin) break;
         target *= ncand < T ? fmaxf(1.25f, 1.15f * (float)T / fmaxf((float)ncand, 1.f))
                             : fminf(0.8f, 0.9f * (float)kCandMax / (float)ncand);
+        __syncthreads();  // every thread has read sm.ncand
         if (t == 0) sm.ncand = 0;
         __syncthreads();
     }
-    // fallback: the same steps on the whole row, streamed again (first for
-    // the row's key statistics)
+    select_exact(src, T, sm, emit);
+}
+
+// The exact steps on the whole row (the fallback after two pivot misses):
+// the row's key statistics, radix passes over the row, marks and emit, each
+// streaming the row again.  Ends with a barrier.
+template <class Src, class Emit>
+__device__ void select_exact(const Src& src, uint32_t T, SelSmem& sm, const Emit& emit) {
+    const int w = threadIdx.x / kWave, lane = __lane_id();
+    const int32_t n = src.n;
+    const int32_t steps = (n + 255) / 256;
     uint32_t rmax = 0, rmin = 0xffffffffu, rcnt = 0;
     for (int32_t s = w; s < steps; s += kWaves) {
         uint32_t k[4];
@@ -539,9 +635,14 @@ __device__ void select_stream(const Src& src, uint32_t T, SelSmem& sm, const Emi
 // Columns [lo, lo + n) of one fp32 score row.
 struct RowSrc {
     static constexpr bool kFloats = true;
+    static constexpr bool kBuffer = true;
     const float* row;  // already offset by lo
     int32_t n;
     bool vec;
+    // raw buffer descriptor of the n entries (loads at or past n return zeros)
+    __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc() const {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), 0, n * 4, kRawDword);
+    }
     // raw float bits of positions p..p+3, -inf past n
     __device__ __forceinline__ void load_raw4(int32_t p, uint32_t (&v)[4]) const {
         if (vec && p + 3 < n) {
@@ -733,6 +834,7 @@ __device__ __forceinline__ void transform_emit_batch(const int32_t* __restrict__
 // pages (sm.maskpage) whose member lies outside [sink, tail) read as -inf.
 struct V1Src {
     static constexpr bool kFloats = true;
+    static constexpr bool kBuffer = false;
     RowSrc base;
     const int32_t* members;
     const int32_t* maskpage;  // LDS, indexed by (position - segment start) / 64
@@ -849,14 +951,35 @@ __global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
     }
     const float* rp = p.scores + row * p.score_stride;
     const RowSrc src{rp, L, (reinterpret_cast<uintptr_t>(rp) & 15) == 0};
-    select_stream(src, (uint32_t)T, sm, [&](const auto& at, const auto& pos, const auto&) {
+    const int32_t* table = p.page_table + row * p.page_table_stride;
+    int32_t* out = p.page_indices + row * p.topk;
+    int32_t* raws = p.raw_indices ? p.raw_indices + row * p.topk : nullptr;
+    // Pages of at least 64 positions: the row's page table (at most
+    // kSpan / 64 = kBlock entries) is staged in LDS (the mask-page array,
+    // unused by plain rows), its loads issued with the pivot sample's.
+    const int bits = p.page_bits;
+    const bool staged = bits >= kTableBits;
+    const int32_t entries = staged ? min(p.page_table_cols, kSpan >> bits) : 0;
+    const int32_t entry = (int32_t)threadIdx.x < entries ? table[threadIdx.x] : 0;
+    uint32_t sk[4];
+    src.load4(sample_pos(L), sk);
+    if (staged) sm.maskpage[threadIdx.x] = entry;  // read after select_sampled's first barrier
+    select_sampled(src, sk, (uint32_t)T, sm, [&](const auto& at, const auto& pos, const auto&) {
         constexpr int N = sizeof(at) / sizeof(at[0]);
         int32_t raw[N];
 #pragma unroll
         for (int i = 0; i < N; ++i) raw[i] = (int32_t)pos[i];
-        transform_emit_batch<N>(p.page_table + row * p.page_table_stride, p.page_table_cols, p.page_bits,
-                                p.page_indices + row * p.topk, p.raw_indices ? p.raw_indices + row * p.topk : nullptr,
-                                at, raw);
+        if (staged) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if (at[i] < 0) continue;
+                const int32_t e = raw[i] >> bits;
+                out[at[i]] = e < entries ? (sm.maskpage[e] << bits) | (raw[i] & ((1 << bits) - 1)) : -1;
+                if (raws) raws[at[i]] = raw[i];
+            }
+        } else {
+            transform_emit_batch<N>(table, p.page_table_cols, bits, out, raws, at, raw);
+        }
     });
 }
 
@@ -966,6 +1089,7 @@ __global__ __launch_bounds__(kBlock, 8) void transform_segments(TransformParams 
 // The concatenated segment candidates of a row: position q = s*T + k.
 struct CandSrc {
     static constexpr bool kFloats = false;
+    static constexpr bool kBuffer = false;
     const uint32_t* keys;  // workspace keys of this row
     const int32_t* count;  // per segment
     int32_t T;

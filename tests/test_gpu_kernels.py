@@ -723,6 +723,36 @@ def test_topk_large_batch_vs_oracle(dev, cols):
     assert np.array_equal(out_h, e_out)
 
 
+@pytest.mark.parametrize("page_size", [16, 64, 128, 1024])
+@pytest.mark.parametrize("short_table", [False, True])
+def test_topk_transform_page_sizes(dev, page_size, short_table):
+    """Page sizes either side of 64 tokens (the register-resident rows take
+    tables of at most 512 entries, smaller pages stream), a page table that
+    covers only part of each row (positions past it map to -1), rows of every
+    length class, more rows than CUs, and no raw output on half the calls."""
+    g = np.random.default_rng(page_size + short_table)
+    B, cols = 700, 32768
+    scores = np.round(g.standard_normal((B, cols)) * 30).astype(np.float32)
+    lens = g.integers(1, cols + 1, B).astype(np.int32)
+    lens[:4] = [cols, 2048, 2049, 1]
+    entries = -(-cols // page_size)
+    if short_table:
+        entries = entries * 3 // 4
+    table = g.integers(0, 1 << 18, (B, entries)).astype(np.int32)
+    bits = page_size.bit_length() - 1
+    full = np.zeros((B, -(-cols // page_size)), np.int32)
+    full[:, :entries] = table
+    e_out, e_raw = O.transform_topk(scores, lens, full, 2048, bits)
+    e_out[(e_raw >> bits) >= entries] = -1  # no table entry: unmapped
+    out = torch.empty((B, 2048), device=dev, dtype=torch.int32)
+    raw = torch.empty_like(out)
+    TK.topk_transform_512_v2(T(scores, dev), T(lens, dev), T(table, dev), out, page_size, None, raw)
+    assert np.array_equal(H(raw), e_raw) and np.array_equal(H(out), e_out)
+    out2 = torch.empty_like(out)
+    TK.topk_transform_512_v2(T(scores, dev), T(lens, dev), T(table, dev), out2, page_size, None, None)
+    assert np.array_equal(H(out2), e_out)
+
+
 # ------------------------------------------------- unfused C4 x4 expansion
 @pytest.mark.parametrize("rows,topk,stride,block,offset", [
     (64, 2048, 4 * 2048 + 64, 16384, 0),   # runtime.py:638-641 shape (BLOCK = next power of two)
