@@ -30,6 +30,7 @@
 // Rows longer than 32768 columns are cut into 32768-column segments whose
 // Top-T land in a workspace; a merge work-group selects from their union.
 #include <algorithm>
+#include <cstddef>
 
 #include "common.h"
 
@@ -56,9 +57,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 static_assert(kHist == 4 * kBlock && kWords % kBlock == 0 && kCandMax % kBlock == 0, "work split");
 static_assert(kSampleRuns * 32 == 4 * kBlock, "eight threads per sample run");
 
-struct SelSmem {
+struct SelSmem {  // (arrays at 16-byte offsets: read as 16-byte words)
     uint32_t hist[kHist];      // radix histograms; bitmap word prefixes
-    uint32_t cand_key[kCandMax];
+    uint32_t cand_key[kCandMax];  // (after the ranks of a transform row: its selected positions in slot order)
     uint16_t cand_pos[kCandMax];
     uint32_t gt_bits[kWords];  // positions with key > tau
     uint32_t eq_bits[kWords];  // positions with key == tau
@@ -68,6 +69,8 @@ struct SelSmem {
     int32_t maskpage[kSpan / 64];  // V1 mask: page per selected rank, -1 when unmasked; or a row's page table
 };
 static_assert(sizeof(SelSmem) <= 40 * 1024, "four work-groups per CU");
+static_assert(offsetof(SelSmem, gt_bits) % 16 == 0 && offsetof(SelSmem, eq_bits) % 16 == 0, "16-byte words");
+static_assert(offsetof(SelSmem, cand_key) % 8 == 0 && kCandMax * 4 >= 2 * 2048, "T <= 2048 staged positions");
 
 __device__ __forceinline__ uint32_t readlane(uint32_t v, int lane) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
@@ -161,6 +164,7 @@ __device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& b
         // (after the reads above: one wave's LDS accesses complete in order)
 #pragma unroll
         for (int i = 0; i < 8; ++i) h4[i] = make_uint4(0u, 0u, 0u, 0u);
+        if (threadIdx.x == 0) sm.bc[3] = 0;  // append counter of small_bin_select
     }
     __syncthreads();
     bin = __builtin_amdgcn_readfirstlane(sm.bc[0]);
@@ -191,8 +195,9 @@ struct Radix {
     __device__ __forceinline__ uint32_t digit(uint32_t k) const {
         return (k >> (shift - bits())) & ((1u << bits()) - 1u);
     }
-    // after the histogram of this pass is in sm.hist (and a barrier)
-    __device__ __forceinline__ void finish(SelSmem& sm) {
+    // after the histogram of this pass is in sm.hist (and a barrier); returns
+    // the count of the bin now fixed in the prefix
+    __device__ __forceinline__ uint32_t finish(SelSmem& sm) {
         uint32_t bin, above, inbin;
         find_bin(remaining, sm, bin, above, inbin);
         const int b = bits();
@@ -200,6 +205,7 @@ struct Radix {
         remaining -= above;
         prefix |= bin << shift;
         pmask |= ((1u << b) - 1u) << shift;
+        return inbin;
     }
 };
 
@@ -223,19 +229,34 @@ struct Ranker {
     __device__ __forceinline__ static void scan(SelSmem& sm) {
         if (threadIdx.x < kWave) {
             const int lane = threadIdx.x;
+            // (16-byte LDS accesses: words 16 lane .. 16 lane + 15)
+            const uint4* g4 = reinterpret_cast<const uint4*>(sm.gt_bits + 16 * lane);
+            const uint4* e4 = reinterpret_cast<const uint4*>(sm.eq_bits + 16 * lane);
             uint32_t c[16];
             uint32_t local = 0;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int wd = 16 * lane + i;
-                c[i] = (uint32_t)__popc(sm.gt_bits[wd]) | ((uint32_t)__popc(sm.eq_bits[wd]) << 16);
-                local += c[i];
+            for (int q = 0; q < 4; ++q) {
+                const uint4 g = g4[q], e = e4[q];
+                c[4 * q + 0] = (uint32_t)__popc(g.x) | ((uint32_t)__popc(e.x) << 16);
+                c[4 * q + 1] = (uint32_t)__popc(g.y) | ((uint32_t)__popc(e.y) << 16);
+                c[4 * q + 2] = (uint32_t)__popc(g.z) | ((uint32_t)__popc(e.z) << 16);
+                c[4 * q + 3] = (uint32_t)__popc(g.w) | ((uint32_t)__popc(e.w) << 16);
+                local += c[4 * q] + c[4 * q + 1] + c[4 * q + 2] + c[4 * q + 3];
             }
             uint32_t run = wave_inclusive_sum(local) - local;
+            uint4* h4 = reinterpret_cast<uint4*>(sm.hist + 16 * lane);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                sm.hist[16 * lane + i] = run;
-                run += c[i];
+            for (int q = 0; q < 4; ++q) {
+                uint4 o;
+                o.x = run;
+                run += c[4 * q];
+                o.y = run;
+                run += c[4 * q + 1];
+                o.z = run;
+                run += c[4 * q + 2];
+                o.w = run;
+                run += c[4 * q + 3];
+                h4[q] = o;
             }
         }
         __syncthreads();
@@ -303,28 +324,40 @@ __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_
 }
 
 // The candidate test and LDS append for one wave's kBatch loads of 4 entries
-// (load u at step s0 + u * kWaves, lane's entries p..p+3).
+// (load u at step s0 + u * kWaves, lane's entries p..p+3).  With a pivot
+// above +0 (int_test) the key test is one signed compare of the raw bits
+// against the pivot's float bits: negative scores and -NaNs are negative as
+// int32, +0 / -0 lie below the pivot, and +inf / +NaNs order above every
+// finite score, as their keys do.
 template <class Src, int kBatch>
 __device__ __forceinline__ void take_candidates(const uint32_t (&v)[kBatch][4], int32_t s0, uint32_t pivot,
-                                                bool float_test, float fpivot, SelSmem& sm) {
+                                                bool float_test, float fpivot, bool int_test, SelSmem& sm) {
     const int lane = __lane_id();
     // slots are allocated per pair of batches (keeps the lane masks in
     // scalar registers)
 #pragma unroll
     for (int h = 0; h < kBatch; h += 2) {
         bool c[2][4];
+        if (Src::kFloats && int_test) {
+            const int32_t ipivot = (int32_t)__float_as_uint(fpivot);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            bool nan = false;
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float x = __uint_as_float(v[h + u][e]);
-                c[u][e] = Src::kFloats ? x >= fpivot : v[h + u][e] >= pivot;
-                nan |= x != x;
-            }
-            if (Src::kFloats && (!float_test || __builtin_amdgcn_ballot_w64(nan) != 0)) {
+                for (int e = 0; e < 4; ++e) c[u][e] = (int32_t)v[h + u][e] >= ipivot;
+        } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) c[u][e] = score_key(__uint_as_float(v[h + u][e])) >= pivot;
+            for (int u = 0; u < 2; ++u) {
+                bool nan = false;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x = __uint_as_float(v[h + u][e]);
+                    c[u][e] = Src::kFloats ? x >= fpivot : v[h + u][e] >= pivot;
+                    nan |= x != x;
+                }
+                if (Src::kFloats && (!float_test || __builtin_amdgcn_ballot_w64(nan) != 0)) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) c[u][e] = score_key(__uint_as_float(v[h + u][e])) >= pivot;
+                }
             }
         }
         uint64_t m[2][4];
@@ -341,19 +374,21 @@ __device__ __forceinline__ void take_candidates(const uint32_t (&v)[kBatch][4], 
         uint32_t base = 0;
         if (lane == 0) base = atomicAdd(&sm.ncand, total);
         base = readlane(base, 0);
+        // A pair that would pass kCandMax writes nothing: ncand then ends
+        // above kCandMax, and the attempt's buffer is not used.
+        if (base + total > (uint32_t)kCandMax) continue;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int32_t p = (s0 + (h + u) * kWaves) * 256 + 4 * lane;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (c[u][e]) {
-                    const uint32_t at = base + pre[u][e] +
-                        __builtin_amdgcn_mbcnt_hi((uint32_t)(m[u][e] >> 32),
-                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)m[u][e], 0u));
-                    if (at < (uint32_t)kCandMax) {
-                        sm.cand_key[at] = v[h + u][e];
-                        sm.cand_pos[at] = (uint16_t)(p + e);
-                    }
+                    // slot base + pre + (lanes below with the entry): scalar
+                    // row pointers plus one shifted add per array
+                    const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m[u][e] >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m[u][e], 0u));
+                    (sm.cand_key + base + pre[u][e])[below] = v[h + u][e];
+                    (sm.cand_pos + base + pre[u][e])[below] = (uint16_t)(p + e);
                 }
             }
         }
@@ -367,9 +402,8 @@ __device__ __forceinline__ void take_candidates(const uint32_t (&v)[kBatch][4], 
 // the selection turns into keys; a wave batch holding a NaN, or a pivot in
 // the NaN key range, takes the exact key test.  Slots come from one LDS
 // allocation per wave and pair of batches (ballot counts, mbcnt ranks).
-// Sources with a buffer descriptor (Src::kBuffer) are double-buffered: a
-// wave issues its next kBatch 1 KB loads before it tests the current ones,
-// so the load latency runs under the test; others load, then test.
+// Sources with a buffer descriptor (Src::kBuffer) keep a ring of loads in
+// flight per wave while they test; others load kBatch, then test.
 template <class Src>
 __device__ __forceinline__ void stream_candidates(const Src& src, uint32_t pivot, SelSmem& sm) {
     // (the wave index as a scalar: the loop below branches per wave)
@@ -379,52 +413,97 @@ __device__ __forceinline__ void stream_candidates(const Src& src, uint32_t pivot
     constexpr int kBatch = 4;
     constexpr int32_t kStride = kWaves * kBatch;  // steps per wave iteration
     const bool float_test = Src::kFloats && pivot <= kPosInfKey;
+    const bool int_test = Src::kFloats && pivot > 0x80000000u;  // pivot score above +0
     const float fpivot = key_score(pivot);
     if constexpr (Src::kBuffer) {
+        // A ring of kRing 1 KB loads per wave over the wave's (at most
+        // kMaxLoads) loads, fully unrolled: the loads of a pair of slots are
+        // waited for, tested, and the slots reloaded kRing loads ahead, so up
+        // to kRing - 2 loads stay in flight while a pair is tested.  Every
+        // load is issued (past the row's end the buffer descriptor returns
+        // zeros without a memory access), which keeps the wait counts exact.
+        constexpr int kRing = 8;
+        constexpr int kMaxLoads = kSpan / (256 * kWaves);  // 16: n <= kSpan
         const auto rs = src.rsrc();
-        uint32_t a[kBatch][4], b[kBatch][4];
-        auto issue = [&](uint32_t (&x)[kBatch][4], int32_t s0) {
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * ((s0 + u * kWaves) * 256 + 4 * lane),
-                                                                      0, 0);
-                x[u][0] = r[0];
-                x[u][1] = r[1];
-                x[u][2] = r[2];
-                x[u][3] = r[3];
-            }
+        const int32_t nload = (steps - w + kWaves - 1) / kWaves;  // this wave's loads: steps w + i * kWaves
+        uint32_t r[kRing][4];
+        auto issue = [&](uint32_t (&x)[4], int i) {
+            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * ((w + i * kWaves) * 256 + 4 * lane), 0, 0);
+            x[0] = q[0];
+            x[1] = q[1];
+            x[2] = q[2];
+            x[3] = q[3];
         };
-        // entries past n read as zeros: the wave holding the row's end sets them to -inf
-        auto take = [&](uint32_t (&x)[kBatch][4], int32_t s0) {
-            if ((s0 + (kBatch - 1) * kWaves + 1) * 256 > n) {
+        // (in slot order: the scheduler would otherwise reorder the loads,
+        // and the first wait would then cover the whole ring)
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u)
+        for (int j = 0; j < kRing; ++j) {
+            issue(r[j], j);
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if ((s0 + u * kWaves) * 256 + 4 * lane + e >= n) x[u][e] = kNegInfBits;
+        for (int i = 0; i < kMaxLoads; i += 2) {
+            uint32_t(&x)[2][4] = *reinterpret_cast<uint32_t(*)[2][4]>(&r[i % kRing]);
+            if (i < nload) {
+                const int32_t s0 = w + i * kWaves;
+                // entries past n read as zeros: the pair holding the row's end sets them to -inf
+                if ((s0 + kWaves + 1) * 256 > n) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if ((s0 + u * kWaves) * 256 + 4 * lane + e >= n) x[u][e] = kNegInfBits;
+                }
+                take_candidates<Src, 2>(x, s0, pivot, float_test, fpivot, int_test, sm);
             }
-            take_candidates<Src, kBatch>(x, s0, pivot, float_test, fpivot, sm);
-        };
-        int32_t s0 = w;
-        if (s0 < steps) issue(a, s0);
-        while (s0 < steps) {
-            const int32_t s1 = s0 + kStride;
-            if (s1 < steps) issue(b, s1);
-            take(a, s0);
-            if (s1 >= steps) break;
-            const int32_t s2 = s1 + kStride;
-            if (s2 < steps) issue(a, s2);
-            take(b, s1);
-            s0 = s2;
+            if (i + kRing < kMaxLoads) {
+                issue(x[0], i + kRing);
+                issue(x[1], i + 1 + kRing);
+            }
         }
     } else {
         for (int32_t s0 = w; s0 < steps; s0 += kStride) {
             uint32_t v[kBatch][4];
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) src.load_raw4((s0 + u * kWaves) * 256 + 4 * lane, v[u]);
-            take_candidates<Src, kBatch>(v, s0, pivot, float_test, fpivot, sm);
+            take_candidates<Src, kBatch>(v, s0, pivot, float_test, fpivot, int_test, sm);
         }
     }
+}
+
+// The radix select's end when the bin just fixed in rx's prefix holds at most
+// one wave of keys: they are appended to sm.hist[0..inbin) (the histogram is
+// clear between passes), and wave 0 ranks them against each other, which
+// resolves every remaining bit at once.  tau is the rx.remaining-th largest
+// key of the bin and r the number of keys equal to tau that are taken (the
+// radix select's final prefix and remaining).  The list is cleared again.
+template <int kN>
+__device__ __forceinline__ void small_bin_select(const uint32_t (&ck)[kN], const Radix& rx, uint32_t inbin,
+                                                 SelSmem& sm, uint32_t& tau, uint32_t& r) {
+#pragma unroll
+    for (int i = 0; i < kN; ++i)
+        if (rx.counts(ck[i], true)) sm.hist[atomicAdd(&sm.bc[3], 1u)] = ck[i];
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        const uint32_t k = lane < (int)inbin ? sm.hist[lane] : 0u;
+        uint32_t gt = 0, eq = 0;
+        for (uint32_t j = 0; j < inbin; ++j) {
+            const uint32_t kj = readlane(k, (int)j);
+            gt += kj > k ? 1u : 0u;
+            eq += kj == k ? 1u : 0u;
+        }
+        const uint64_t hit =
+            __builtin_amdgcn_ballot_w64(lane < (int)inbin && gt < rx.remaining && rx.remaining <= gt + eq);
+        if (lane == (int)__builtin_ctzll(hit)) {
+            sm.bc[0] = k;
+            sm.bc[1] = rx.remaining - gt;
+        }
+        if (lane < (int)inbin) sm.hist[lane] = 0;  // after the read above (in-order LDS)
+    }
+    __syncthreads();
+    tau = __builtin_amdgcn_readfirstlane(sm.bc[0]);
+    r = __builtin_amdgcn_readfirstlane(sm.bc[1]);
 }
 
 // Steps 3 and 4 over ncand (T <= ncand <= kCandMax) buffered candidates.
@@ -446,15 +525,23 @@ __device__ void select_candidates(uint32_t ncand, uint32_t T, SelSmem& sm, const
     if (cmax != cmin) {
         Radix rx;
         rx.start(cmax, cmin, T);
+        bool done = false;
         while (rx.shift > 0) {
 #pragma unroll
             for (int i = 0; i < kCandPerThread; ++i)
                 if (rx.counts(ck[i], true)) atomicAdd(&sm.hist[rx.digit(ck[i])], 1u);
             __syncthreads();
-            rx.finish(sm);
+            const uint32_t inbin = rx.finish(sm);
+            if (rx.shift > 0 && inbin <= (uint32_t)kWave) {
+                small_bin_select(ck, rx, inbin, sm, tau, r);
+                done = true;
+                break;
+            }
         }
-        tau = rx.prefix;
-        r = rx.remaining;
+        if (!done) {
+            tau = rx.prefix;
+            r = rx.remaining;
+        }
     }
     // 4. position ranks
 #pragma unroll
@@ -970,17 +1057,42 @@ __global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
 #pragma unroll
         for (int i = 0; i < N; ++i) raw[i] = (int32_t)pos[i];
         if (staged) {
+            // slot -> position into LDS (the candidate-key array: read only
+            // before the ranks); written out in slot order below
+            uint16_t* stage = reinterpret_cast<uint16_t*>(sm.cand_key);
 #pragma unroll
-            for (int i = 0; i < N; ++i) {
-                if (at[i] < 0) continue;
-                const int32_t e = raw[i] >> bits;
-                out[at[i]] = e < entries ? (sm.maskpage[e] << bits) | (raw[i] & ((1 << bits) - 1)) : -1;
-                if (raws) raws[at[i]] = raw[i];
-            }
+            for (int i = 0; i < N; ++i)
+                if (at[i] >= 0) stage[at[i]] = (uint16_t)raw[i];
         } else {
             transform_emit_batch<N>(table, p.page_table_cols, bits, out, raws, at, raw);
         }
     });
+    if (!staged) return;
+    // (the selection ends with a barrier: every slot is staged) slots in
+    // order, four per thread and 16-byte stores where the rows allow them
+    const uint16_t* stage = reinterpret_cast<const uint16_t*>(sm.cand_key);
+    const int32_t lo_mask = (1 << bits) - 1;
+    auto map = [&](int32_t raw) {
+        const int32_t e = raw >> bits;
+        return e < entries ? (sm.maskpage[e] << bits) | (raw & lo_mask) : -1;
+    };
+    const bool vec = T % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(raws) & 15) == 0;
+    if (vec) {
+        for (int32_t q = threadIdx.x; q < T / 4; q += kBlock) {
+            const uint2 w2 = *reinterpret_cast<const uint2*>(stage + 4 * q);
+            const int32_t r0 = (int32_t)(w2.x & 0xffffu), r1 = (int32_t)(w2.x >> 16);
+            const int32_t r2 = (int32_t)(w2.y & 0xffffu), r3 = (int32_t)(w2.y >> 16);
+            *reinterpret_cast<int4*>(out + 4 * q) = make_int4(map(r0), map(r1), map(r2), map(r3));
+            if (raws) *reinterpret_cast<int4*>(raws + 4 * q) = make_int4(r0, r1, r2, r3);
+        }
+    } else {
+        for (int32_t tx = threadIdx.x; tx < T; tx += kBlock) {
+            const int32_t raw = stage[tx];
+            out[tx] = map(raw);
+            if (raws) raws[tx] = raw;
+        }
+    }
 }
 
 // ------------------------------------------------------- segmented rows
