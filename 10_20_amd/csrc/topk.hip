@@ -480,18 +480,37 @@ __device__ __forceinline__ void stream_candidates(const Src& src, uint32_t pivot
 template <int kN>
 __device__ __forceinline__ void small_bin_select(const uint32_t (&ck)[kN], const Radix& rx, uint32_t inbin,
                                                  SelSmem& sm, uint32_t& tau, uint32_t& r) {
+    // one LDS allocation per wave (ballot counts, mbcnt ranks)
+    const int lane = __lane_id();
+    uint64_t bal[kN];
+    uint32_t pre[kN], total = 0;
 #pragma unroll
-    for (int i = 0; i < kN; ++i)
-        if (rx.counts(ck[i], true)) sm.hist[atomicAdd(&sm.bc[3], 1u)] = ck[i];
+    for (int i = 0; i < kN; ++i) {
+        bal[i] = __builtin_amdgcn_ballot_w64(rx.counts(ck[i], true));
+        pre[i] = total;
+        total += (uint32_t)__builtin_popcountll(bal[i]);
+    }
+    if (total > 0) {
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&sm.bc[3], total);
+        base = readlane(base, 0);
+#pragma unroll
+        for (int i = 0; i < kN; ++i)
+            if (rx.counts(ck[i], true))
+                sm.hist[base + pre[i] +
+                        __builtin_amdgcn_mbcnt_hi((uint32_t)(bal[i] >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bal[i], 0u))] = ck[i];
+    }
     __syncthreads();
     if (threadIdx.x < kWave) {
-        const int lane = threadIdx.x;
+        // every lane reads the list as 16-byte words (bins past it are zero,
+        // below every real key)
         const uint32_t k = lane < (int)inbin ? sm.hist[lane] : 0u;
         uint32_t gt = 0, eq = 0;
-        for (uint32_t j = 0; j < inbin; ++j) {
-            const uint32_t kj = readlane(k, (int)j);
-            gt += kj > k ? 1u : 0u;
-            eq += kj == k ? 1u : 0u;
+        for (uint32_t j = 0; j < inbin; j += 4) {
+            const uint4 q = *reinterpret_cast<const uint4*>(sm.hist + j);
+            gt += (q.x > k ? 1u : 0u) + (q.y > k ? 1u : 0u) + (q.z > k ? 1u : 0u) + (q.w > k ? 1u : 0u);
+            eq += (q.x == k ? 1u : 0u) + (q.y == k ? 1u : 0u) + (q.z == k ? 1u : 0u) + (q.w == k ? 1u : 0u);
         }
         const uint64_t hit =
             __builtin_amdgcn_ballot_w64(lane < (int)inbin && gt < rx.remaining && rx.remaining <= gt + eq);
@@ -499,7 +518,7 @@ __device__ __forceinline__ void small_bin_select(const uint32_t (&ck)[kN], const
             sm.bc[0] = k;
             sm.bc[1] = rx.remaining - gt;
         }
-        if (lane < (int)inbin) sm.hist[lane] = 0;  // after the read above (in-order LDS)
+        if (lane < (int)inbin) sm.hist[lane] = 0;  // after the reads above (in-order LDS)
     }
     __syncthreads();
     tau = __builtin_amdgcn_readfirstlane(sm.bc[0]);
