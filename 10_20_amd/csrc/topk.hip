@@ -301,10 +301,12 @@ __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_
         find_bin(want, sm, bin, above, inbin);
         // Expected candidates with the pivot at the bin's lower edge (every
         // sample of the bin passes) or just above the bin (none passes).
-        const uint64_t est_lo = (uint64_t)(above + inbin) * n / scnt, est_hi = (uint64_t)above * n / scnt;
-        if (est_lo <= (uint64_t)kCandMax * 7 / 8 || lo == 0) {
+        // (floor(a * n / scnt) <= K  <=>  a * n < (K + 1) * scnt, and
+        // floor(a * n / scnt) >= K  <=>  a * n >= K * scnt: no divisions)
+        const uint64_t lo_n = (uint64_t)(above + inbin) * (uint64_t)n, hi_n = (uint64_t)above * (uint64_t)n;
+        if (lo_n < ((uint64_t)kCandMax * 7 / 8 + 1) * scnt || lo == 0) {
             pivot = rx.prefix | (bin << lo);
-        } else if (est_hi >= (uint64_t)T * 9 / 8 && bin + 1 < (uint32_t)kHist) {
+        } else if (hi_n >= ((uint64_t)T * 9 / 8) * scnt && bin + 1 < (uint32_t)kHist) {
             pivot = rx.prefix | ((bin + 1) << lo);
         } else {
             // refine inside the bin on the next digit
