@@ -753,6 +753,25 @@ def test_topk_transform_page_sizes(dev, page_size, short_table):
     assert np.array_equal(H(out2), e_out)
 
 
+@pytest.mark.parametrize("topk", [1, 37, 2047, 2048])
+def test_topk_transform_odd_topk_single_pass(dev, topk):
+    """Rows within one work-group's span with T not a multiple of 4: the
+    slot-order output then takes the element-wise stores (output rows are
+    not 16-byte aligned), with ties, -inf and rows shorter than T."""
+    g = np.random.default_rng(topk)
+    B, cols = 300, 20000
+    scores = np.round(g.standard_normal((B, cols)) * 8).astype(np.float32)
+    scores[g.random((B, cols)) < 0.01] = -np.inf
+    lens = g.integers(1, cols + 1, B).astype(np.int32)
+    lens[:3] = [cols, topk, max(1, topk - 1)]
+    table = g.integers(0, 1 << 20, (B, -(-cols // 64))).astype(np.int32)
+    out = torch.empty((B, topk), device=dev, dtype=torch.int32)
+    raw = torch.empty_like(out)
+    TK.topk_transform_512_v2(T(scores, dev), T(lens, dev), T(table, dev), out, 64, None, raw)
+    e_out, e_raw = O.transform_topk(scores, lens, table, topk, 6)
+    assert np.array_equal(H(raw), e_raw) and np.array_equal(H(out), e_out)
+
+
 # ------------------------------------------------- unfused C4 x4 expansion
 @pytest.mark.parametrize("rows,topk,stride,block,offset", [
     (64, 2048, 4 * 2048 + 64, 16384, 0),   # runtime.py:638-641 shape (BLOCK = next power of two)
