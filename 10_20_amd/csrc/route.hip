@@ -36,10 +36,74 @@ struct U64Less {
     __device__ bool operator()(uint64_t a, uint64_t b) const { return a < b; }
 };
 
+// The same network over n composites held in registers: thread t holds
+// elements t*E .. t*E+E-1 (threads at or past n / E hold none and only join
+// the barriers).  Pairs (e, e ^ j) inside a thread swap registers, pairs
+// inside a wave meet through lane shuffles, and pairs across waves through
+// LDS, two buffers used in turn with one barrier per such step: of the 66
+// steps of a 2048-key network, 6 cross waves.
+__device__ __forceinline__ uint64_t keep(uint64_t a, uint64_t b, bool keep_max) {
+    return keep_max ? (a > b ? a : b) : (a > b ? b : a);
+}
+
+template <int E, int J>
+__device__ __forceinline__ void step_in_thread(uint64_t (&v)[E], int e0, int k, bool last) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        if ((i & J) == 0) {
+            const bool desc = last || (((e0 + i) & k) == 0);
+            const uint64_t a = v[i], b = v[i + J];
+            v[i] = keep(a, b, desc);
+            v[i + J] = keep(a, b, !desc);
+        }
+    }
+}
+
+template <int E>
+__device__ void bitonic_desc_regs(uint64_t (&v)[E], int n, uint64_t* buf0, uint64_t* buf1) {
+    const int e0 = (int)threadIdx.x * E;
+    const bool live = e0 < n;
+    int flip = 0;
+    for (int k = 2; k <= n; k <<= 1) {
+        const bool last = k == n;
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            if (j < E) {
+                if (j == 1) step_in_thread<E, 1>(v, e0, k, last);
+                if (E > 2 && j == 2) step_in_thread<E, (E > 2 ? 2 : 1)>(v, e0, k, last);
+                if (E > 4 && j == 4) step_in_thread<E, (E > 4 ? 4 : 1)>(v, e0, k, last);
+            } else if (j / E < kWave) {
+                const int d = j / E;
+#pragma unroll
+                for (int i = 0; i < E; ++i) {
+                    const int e = e0 + i;
+                    const uint64_t a = v[i];
+                    const uint32_t blo = (uint32_t)__shfl_xor((int)(uint32_t)a, d, kWave);
+                    const uint32_t bhi = (uint32_t)__shfl_xor((int)(uint32_t)(a >> 32), d, kWave);
+                    const uint64_t b = ((uint64_t)bhi << 32) | blo;
+                    v[i] = keep(a, b, ((e & j) == 0) == (last || (e & k) == 0));
+                }
+            } else {
+                uint64_t* w = flip ? buf1 : buf0;
+                flip ^= 1;
+                if (live)
+#pragma unroll
+                    for (int i = 0; i < E; ++i) w[e0 + i] = v[i];
+                __syncthreads();
+                if (live)
+#pragma unroll
+                    for (int i = 0; i < E; ++i) {
+                        const int e = e0 + i;
+                        v[i] = keep(v[i], w[e ^ j], ((e & j) == 0) == (last || (e & k) == 0));
+                    }
+            }
+        }
+    }
+}
+
 // sglang/kernels/jit/csrc/deepseek_v4/v1_query.cuh:7-49
-template <typename Index>
+template <typename Index, int E>
 __global__ __launch_bounds__(512) void route_kernel(v1_route_args a, int n_sort) {
-    __shared__ uint64_t s[kMaxSort];
+    __shared__ uint64_t s0[512 * E], s1[512 * E];  // (E = n_sort / 512: 8 KB of LDS per 512 keys)
     const int64_t row = blockIdx.x;
     const int32_t active = max(a.lens[row] - 1, 0) / 1024 * 16;
     const int32_t take = a.takes[row];
@@ -57,8 +121,12 @@ __global__ __launch_bounds__(512) void route_kernel(v1_route_args a, int n_sort)
         return;
     }
     const float* sc = a.scores + row * a.score_stride;
-    for (int p = threadIdx.x; p < n_sort; p += blockDim.x) {
-        uint64_t v = 0;  // padding slots sort last
+    const int e0 = (int)threadIdx.x * E;
+    uint64_t v[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const int p = e0 + i;
+        v[i] = 0;  // padding slots sort last
         if (p < a.pages) {
             float best = -__builtin_huge_valf();
             if (p < active) {
@@ -66,17 +134,17 @@ __global__ __launch_bounds__(512) void route_kernel(v1_route_args a, int n_sort)
                 const float4 y = reinterpret_cast<const float4*>(sc + 8 * p)[1];
                 best = fmaxf(fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w)), fmaxf(fmaxf(y.x, y.y), fmaxf(y.z, y.w)));
             }
-            v = ((uint64_t)score_key(best) << 32) | (uint32_t)(0xffffffffu - (uint32_t)p);
+            v[i] = ((uint64_t)score_key(best) << 32) | (uint32_t)(0xffffffffu - (uint32_t)p);
         }
-        s[p] = v;
     }
-    __syncthreads();
-    bitonic_desc(s, n_sort, n_sort, U64Less{});
+    bitonic_desc_regs<E>(v, n_sort, s0, s1);
     // selected takes ranks < take_stride; the fine table every rank < take
     // (v1_query.cuh:44-48), bounded by the sorted pages and the table width
     const int32_t ft_ranks = a.fill_table ? min(min(take, a.pages), a.ft_cols) : 0;
-    for (int r = threadIdx.x; r < max(a.take_stride, ft_ranks); r += blockDim.x) {
-        const int32_t p = (int32_t)(0xffffffffu - (uint32_t)s[r]);
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const int r = e0 + i;
+        const int32_t p = (int32_t)(0xffffffffu - (uint32_t)v[i]);
         if (r < a.take_stride) selected[r] = (Index)p;
         if (r < ft_ranks) ft[r] = rt[p];
     }
@@ -152,11 +220,20 @@ extern "C" int v1_route(const v1_route_args* a, void* stream) {
     V1_REQUIRE(a->selected_bits == 32 || a->selected_bits == 64, "route: selected must be int32 or int64");
     V1_REQUIRE((reinterpret_cast<uintptr_t>(a->scores) & 15) == 0, "route: scores must be 16-byte aligned");
     if (a->batch == 0) return V1_OK;
-    const int n_sort = pow2_at_least(a->pages);
-    if (a->selected_bits == 32)
-        hipLaunchKernelGGL(route_kernel<int32_t>, dim3(a->batch), dim3(512), 0, as_stream(stream), *a, n_sort);
-    else
-        hipLaunchKernelGGL(route_kernel<int64_t>, dim3(a->batch), dim3(512), 0, as_stream(stream), *a, n_sort);
+    const int n_sort = pow2_at_least(a->pages);  // 64 .. 4096: E = n_sort / 512 keys per thread, at least 1
+    hipStream_t st = as_stream(stream);
+    const dim3 g(a->batch), b(512);
+    if (a->selected_bits == 32) {
+        if (n_sort <= 512) hipLaunchKernelGGL((route_kernel<int32_t, 1>), g, b, 0, st, *a, n_sort);
+        else if (n_sort == 1024) hipLaunchKernelGGL((route_kernel<int32_t, 2>), g, b, 0, st, *a, n_sort);
+        else if (n_sort == 2048) hipLaunchKernelGGL((route_kernel<int32_t, 4>), g, b, 0, st, *a, n_sort);
+        else hipLaunchKernelGGL((route_kernel<int32_t, 8>), g, b, 0, st, *a, n_sort);
+    } else {
+        if (n_sort <= 512) hipLaunchKernelGGL((route_kernel<int64_t, 1>), g, b, 0, st, *a, n_sort);
+        else if (n_sort == 1024) hipLaunchKernelGGL((route_kernel<int64_t, 2>), g, b, 0, st, *a, n_sort);
+        else if (n_sort == 2048) hipLaunchKernelGGL((route_kernel<int64_t, 4>), g, b, 0, st, *a, n_sort);
+        else hipLaunchKernelGGL((route_kernel<int64_t, 8>), g, b, 0, st, *a, n_sort);
+    }
     return V1_LAUNCHED("route");
 }
 

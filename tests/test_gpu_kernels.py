@@ -159,7 +159,7 @@ def test_route_reference_example(dev, kats):
     assert torch.equal(ft.cpu()[:, RX.TAKE:], (RX.CAP + torch.arange(68, dtype=torch.int32))[None].expand(B, -1))
 
 
-@pytest.mark.parametrize("pages,bits", [(64, 32), (128, 64), (512, 32), (2048, 64), (4096, 32)])
+@pytest.mark.parametrize("pages,bits", [(64, 32), (128, 64), (256, 64), (512, 32), (1024, 32), (2048, 64), (4096, 32)])
 def test_route_random_vs_oracle(dev, pages, bits):
     g = np.random.default_rng(pages)
     B = 24
