@@ -1314,30 +1314,43 @@ __global__ __launch_bounds__(kBlock, 8) void transform_merge(TransformParams p, 
 
 // ------------------------------------------------------ unfused mask/map
 // sglang/srt/layers/attention/v1_deepseek/kernels.py:444-472.
-__global__ void mask_fine_kernel(float* scores, int64_t stride, const void* selected, int32_t sel64,
-                                 const int32_t* rt, const int32_t* members, const int32_t* lens,
-                                 const int32_t* takes, int32_t maxp, int32_t take_stride, int32_t width,
-                                 int32_t sink_cap, int32_t window) {
+// One thread per 4 consecutive columns (they share one 64-column page, so
+// its rank, table entry and 4 members come from 3 loads); only columns that
+// are masked are written.
+__global__ __launch_bounds__(256) void mask_fine_kernel(float* scores, int64_t stride, const void* selected,
+                                                        int32_t sel64, const int32_t* rt, const int32_t* members,
+                                                        const int32_t* lens, const int32_t* takes, int32_t maxp,
+                                                        int32_t take_stride, int32_t width, int32_t sink_cap,
+                                                        int32_t window, int32_t vec) {
     const int64_t row = blockIdx.y;
-    const int32_t j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= width) return;
+    const int32_t j0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (j0 >= width) return;
     const int32_t n = lens[row];
     const int32_t take = takes[row];
     const int32_t sink = min(n, sink_cap);
     const int32_t tail = max(sink, min(max(n - 1, 0) / 1024 * 1024, max(sink, n - window)));
     const int32_t count = take * 64 + sink + n - tail;
-    const bool fine = j < take * 64;
-    int32_t logical = -1;
-    if (fine && j / 64 < take_stride) {
-        const int32_t rank = sel64 ? (int32_t) static_cast<const int64_t*>(selected)[row * take_stride + j / 64]
-                                   : static_cast<const int32_t*>(selected)[row * take_stride + j / 64];
+    const bool fine = j0 < take * 64;  // (take * 64 is a multiple of 4: the 4 columns agree)
+    int4 lg = make_int4(-1, -1, -1, -1);
+    if (fine && j0 / 64 < take_stride) {
+        const int32_t rank = sel64 ? (int32_t) static_cast<const int64_t*>(selected)[row * take_stride + j0 / 64]
+                                   : static_cast<const int32_t*>(selected)[row * take_stride + j0 / 64];
         if (rank >= 0 && rank < maxp) {
             const int32_t page = rt[row * maxp + rank];
-            if (page >= 0) logical = members[(int64_t)page * 64 + (j & 63)];
+            if (page >= 0) {
+                const int32_t* m = members + (int64_t)page * 64 + (j0 & 63);
+                lg = vec ? *reinterpret_cast<const int4*>(m) : make_int4(m[0], m[1], m[2], m[3]);
+            }
         }
     }
-    const bool good = j < count && (!fine || (logical >= sink && logical < tail));
-    if (!good) scores[row * stride + j] = -__builtin_huge_valf();
+    const int32_t l4[4] = {lg.x, lg.y, lg.z, lg.w};
+    float* out = scores + row * stride + j0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int32_t j = j0 + e;
+        const bool good = j < count && (!fine || (l4[e] >= sink && l4[e] < tail));
+        if (j < width && !good) out[e] = -__builtin_huge_valf();
+    }
 }
 
 // sglang/srt/layers/attention/v1_deepseek/kernels.py:323-376.
@@ -1481,9 +1494,10 @@ extern "C" int v1_mask_fine(float* scores, int64_t score_stride, const void* sel
     V1_REQUIRE(rows >= 0 && width >= 0 && maxp > 0, "mask_fine: bad shape");
     V1_REQUIRE(selected_bits == 32 || selected_bits == 64, "mask_fine: selected must be int32 or int64");
     if (rows == 0 || width == 0) return V1_OK;
-    hipLaunchKernelGGL(mask_fine_kernel, dim3((uint32_t)cdiv(width, 256), rows), dim3(256), 0, as_stream(stream),
+    const int32_t vec = (reinterpret_cast<uintptr_t>(members) & 15) == 0 ? 1 : 0;
+    hipLaunchKernelGGL(mask_fine_kernel, dim3((uint32_t)cdiv(width, 1024), rows), dim3(256), 0, as_stream(stream),
                        scores, score_stride, selected, selected_bits == 64, rt, members, lens, takes, maxp,
-                       take_stride, width, sink, window);
+                       take_stride, width, sink, window, vec);
     return V1_LAUNCHED("mask_fine");
 }
 

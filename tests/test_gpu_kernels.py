@@ -320,12 +320,21 @@ def test_topk_transform_vs_oracle(dev, B, cols, topk):
     assert np.array_equal(H(raw)[rows], e_raw) and np.array_equal(H(out)[rows], e_out)
 
 
-def test_mask_fine_and_output_ids_vs_oracle(dev):
+@pytest.mark.parametrize("cols,offset", [(3000, 0), (2999, 1)])
+def test_mask_fine_and_output_ids_vs_oracle(dev, cols, offset):
+    """mask_fine takes 4 columns per thread (one 16-byte member load when the
+    member table is 16-byte aligned); a width that is not a multiple of 4 and a
+    member table at a 4-byte offset take the partial and scalar paths."""
     g = np.random.default_rng(11)
-    B, cols, topk = 40, 3000, 512
+    B, topk = 40, 512
     c = _v1_case(g, B, cols, 40, True)
     w_d = T(c["scores"], dev)
-    K.mask_fine[(B, -(-cols // 256))](w_d, T(c["sel"], dev), T(c["rt"], dev), T(c["members"], dev), T(c["lens"], dev),
+    mem = T(c["members"], dev)
+    if offset:
+        buf = torch.empty(mem.numel() + offset, device=dev, dtype=torch.int32)
+        buf[offset:] = mem.reshape(-1)
+        mem = buf[offset:].view(mem.shape)
+    K.mask_fine[(B, -(-cols // 256))](w_d, T(c["sel"], dev), T(c["rt"], dev), mem, T(c["lens"], dev),
                                       T(c["takes"], dev), 64, 40, cols, cols, 64, 64)
     w_o = c["scores"].copy()
     O.mask_fine(w_o, c["sel"], c["rt"], c["members"], c["lens"], c["takes"], cols, 64, 64)
