@@ -527,6 +527,32 @@ __device__ __forceinline__ void small_bin_select(const uint32_t (&ck)[kN], const
     r = __builtin_amdgcn_readfirstlane(sm.bc[1]);
 }
 
+// Step 3: the T-th largest key tau of the keys held in ck[] across the
+// work-group (block statistics cmax / cmin of the real keys, at least T of
+// them), and r, the number of keys equal to tau that are taken.
+template <int kN>
+__device__ __forceinline__ void radix_tau(const uint32_t (&ck)[kN], uint32_t cmax, uint32_t cmin, uint32_t T,
+                                          SelSmem& sm, uint32_t& tau, uint32_t& r) {
+    tau = cmax;
+    r = T;
+    if (cmax == cmin) return;
+    Radix rx;
+    rx.start(cmax, cmin, T);
+    while (rx.shift > 0) {
+#pragma unroll
+        for (int i = 0; i < kN; ++i)
+            if (rx.counts(ck[i], true)) atomicAdd(&sm.hist[rx.digit(ck[i])], 1u);
+        __syncthreads();
+        const uint32_t inbin = rx.finish(sm);
+        if (rx.shift > 0 && inbin <= (uint32_t)kWave) {
+            small_bin_select(ck, rx, inbin, sm, tau, r);
+            return;
+        }
+    }
+    tau = rx.prefix;
+    r = rx.remaining;
+}
+
 // Steps 3 and 4 over ncand (T <= ncand <= kCandMax) buffered candidates.
 // Ends with a barrier.
 template <class Src, class Emit>
@@ -542,28 +568,8 @@ __device__ void select_candidates(uint32_t ncand, uint32_t T, SelSmem& sm, const
         key_stats(ck[i], cmax, cmin, cc);
     }
     block_stats(cmax, cmin, cc, sm);
-    uint32_t tau = cmax, r = T;
-    if (cmax != cmin) {
-        Radix rx;
-        rx.start(cmax, cmin, T);
-        bool done = false;
-        while (rx.shift > 0) {
-#pragma unroll
-            for (int i = 0; i < kCandPerThread; ++i)
-                if (rx.counts(ck[i], true)) atomicAdd(&sm.hist[rx.digit(ck[i])], 1u);
-            __syncthreads();
-            const uint32_t inbin = rx.finish(sm);
-            if (rx.shift > 0 && inbin <= (uint32_t)kWave) {
-                small_bin_select(ck, rx, inbin, sm, tau, r);
-                done = true;
-                break;
-            }
-        }
-        if (!done) {
-            tau = rx.prefix;
-            r = rx.remaining;
-        }
-    }
+    uint32_t tau, r;
+    radix_tau(ck, cmax, cmin, T, sm, tau, r);
     // 4. position ranks
 #pragma unroll
     for (int i = 0; i < kCandPerThread; ++i) {
@@ -735,6 +741,63 @@ __device__ void select_exact(const Src& src, uint32_t T, SelSmem& sm, const Emit
             at[e] = (p + e < n && k[e] >= tau) ? Ranker::slot(sm, p + e, k[e] > tau, r) : -1;
         }
         emit(at, pp, k);
+    }
+    __syncthreads();
+}
+
+// Rows of at most kShort columns: the whole row is loaded into registers at
+// once (kShortPer keys per thread, position 4 * (g * kBlock + t) + e for load
+// g), so no sample, pivot or candidate stream is needed: the radix passes run
+// over the registers, then the ranks.  Rows with fewer than T keys above -inf
+// take the exact steps.  Ends with a barrier.
+constexpr int kShort = 8192;
+constexpr int kShortPer = kShort / kBlock;  // 16
+static_assert(kShortPer % 4 == 0, "whole 16-byte loads per thread");
+
+template <class Src, class Emit>
+__device__ void select_short(const Src& src, uint32_t T, SelSmem& sm, const Emit& emit) {
+    const int t = threadIdx.x;
+    const int32_t n = src.n;
+    clear_hist(sm);  // (the barrier of block_stats orders these before any use)
+    Ranker::clear(sm);
+    uint32_t ck[kShortPer];
+#pragma unroll
+    for (int g = 0; g < kShortPer / 4; ++g) {
+        uint32_t v[4];
+        src.load_raw4(g * 4 * kBlock + 4 * t, v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ck[4 * g + e] = Src::kFloats ? score_key(__uint_as_float(v[e])) : v[e];
+    }
+    uint32_t cmax = 0, cmin = 0xffffffffu, cc = 0;
+#pragma unroll
+    for (int i = 0; i < kShortPer; ++i) key_stats(ck[i], cmax, cmin, cc);
+    block_stats(cmax, cmin, cc, sm);
+    if (cc < T) {
+        __syncthreads();  // every thread has read sm.red
+        select_exact(src, T, sm, emit);
+        return;
+    }
+    uint32_t tau, r;
+    radix_tau(ck, cmax, cmin, T, sm, tau, r);
+    auto pos = [&](int i) { return (uint32_t)(4 * ((i >> 2) * kBlock + t) + (i & 3)); };
+#pragma unroll
+    for (int i = 0; i < kShortPer; ++i)
+        if ((int32_t)pos(i) < n) Ranker::mark(sm, pos(i), ck[i] > tau, ck[i] == tau);
+    __syncthreads();
+    Ranker::scan(sm);
+    // the winners go out in batches of one load's four keys
+#pragma unroll
+    for (int g = 0; g < kShortPer / 4; ++g) {
+        int32_t at[4];
+        uint32_t cp[4], kk[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * g + e;
+            cp[e] = pos(i);
+            kk[e] = ck[i];
+            at[e] = ((int32_t)cp[e] < n && ck[i] >= tau) ? Ranker::slot(sm, cp[e], ck[i] > tau, r) : -1;
+        }
+        emit(at, cp, kk);
     }
     __syncthreads();
 }
@@ -1019,6 +1082,8 @@ __device__ __forceinline__ V1Src v1_source(const V1Params& p, int64_t row, const
 }
 
 // --------------------------------------------------------- single pass
+// kShortRows: every row of the call has at most kShort columns (select_short).
+template <bool kShortRows>
 __global__ __launch_bounds__(kBlock, 8) void v1_topk_rows(V1Params p) {
     __shared__ SelSmem sm;
     const int64_t row = blockIdx.x;
@@ -1039,15 +1104,20 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_rows(V1Params p) {
             v1_emit(p, row, ri, tx, tx < L ? tx : -1, inf);
         }
     } else {
-        select_stream(src, (uint32_t)T, sm, [&](const auto& at, const auto& pos, const auto& key) {
+        auto emit = [&](const auto& at, const auto& pos, const auto& key) {
 #pragma unroll
             for (int i = 0; i < (int)(sizeof(at) / sizeof(at[0])); ++i)
                 if (at[i] >= 0) v1_emit(p, row, ri, at[i], (int32_t)pos[i], key[i] == kNegInfKey);
-        });
+        };
+        if constexpr (kShortRows)
+            select_short(src, (uint32_t)T, sm, emit);
+        else
+            select_stream(src, (uint32_t)T, sm, emit);
     }
     v1_pad_expansion(p, row);
 }
 
+template <bool kShortRows>
 __global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
     __shared__ SelSmem sm;
     const int64_t row = blockIdx.x;
@@ -1069,10 +1139,7 @@ __global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
     const bool staged = bits >= kTableBits;
     const int32_t entries = staged ? min(p.page_table_cols, kSpan >> bits) : 0;
     const int32_t entry = (int32_t)threadIdx.x < entries ? table[threadIdx.x] : 0;
-    uint32_t sk[4];
-    src.load4(sample_pos(L), sk);
-    if (staged) sm.maskpage[threadIdx.x] = entry;  // read after select_sampled's first barrier
-    select_sampled(src, sk, (uint32_t)T, sm, [&](const auto& at, const auto& pos, const auto&) {
+    auto emit = [&](const auto& at, const auto& pos, const auto&) {
         constexpr int N = sizeof(at) / sizeof(at[0]);
         int32_t raw[N];
 #pragma unroll
@@ -1087,7 +1154,16 @@ __global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
         } else {
             transform_emit_batch<N>(table, p.page_table_cols, bits, out, raws, at, raw);
         }
-    });
+    };
+    if constexpr (kShortRows) {
+        if (staged) sm.maskpage[threadIdx.x] = entry;  // read after select_short's first barrier
+        select_short(src, (uint32_t)T, sm, emit);
+    } else {
+        uint32_t sk[4];
+        src.load4(sample_pos(L), sk);
+        if (staged) sm.maskpage[threadIdx.x] = entry;  // read after select_sampled's first barrier
+        select_sampled(src, sk, (uint32_t)T, sm, emit);
+    }
     if (!staged) return;
     // (the selection ends with a barrier: every slot is staged) slots in
     // order, four per thread and 16-byte stores where the rows allow them
@@ -1396,15 +1472,16 @@ __global__ void output_ids_kernel(const int32_t* raw_in, const float* scores, in
 
 
 template <typename P>
-int launch_topk(void (*single)(P), void (*seg)(P, Workspace), void (*merge)(P, Workspace), int32_t cols,
-                int32_t batch, int32_t topk, void* wsp, int64_t ws_bytes, const P& p, hipStream_t st,
+int launch_topk(void (*single)(P), void (*single_short)(P), void (*seg)(P, Workspace), void (*merge)(P, Workspace),
+                int32_t cols, int32_t batch, int32_t topk, void* wsp, int64_t ws_bytes, const P& p, hipStream_t st,
                 const char* name) {
     const SegPlan plan = plan_segments(batch, cols, topk);
     const int64_t need = workspace_bytes(batch, plan, topk);
     // rows within one work-group's span also run in one pass when the caller
-    // gives no (or too small a) workspace for the split
+    // gives no (or too small a) workspace for the split; calls whose rows
+    // all fit kShort columns hold each row in registers
     if (plan.nseg == 1 || (cols <= kSpan && (wsp == nullptr || ws_bytes < need))) {
-        hipLaunchKernelGGL(single, dim3(batch), dim3(kBlock), 0, st, p);
+        hipLaunchKernelGGL(cols <= kShort ? single_short : single, dim3(batch), dim3(kBlock), 0, st, p);
         return V1_LAUNCHED(name);
     }
     V1_REQUIRE(wsp != nullptr && ws_bytes >= need, "%s: rows longer than %d columns need a workspace of %lld bytes",
@@ -1470,7 +1547,8 @@ extern "C" int v1_topk(const v1_topk_args* a, void* stream) {
                a->pages, a->selected, a->selected_bits == 64, a->take_stride, a->lens, a->takes, a->physical,
                a->logical, a->raw, a->topk, a->window, a->mask, a->expanded, a->expansion_stride,
                a->physical_output, a->bucket_from_rank, a->fine_table, a->fine_table_cols, a->direct_fine};
-    return launch_topk<V1Params>(v1_topk_rows, v1_topk_segments, v1_topk_merge, a->cols, a->batch, a->topk,
+    return launch_topk<V1Params>(v1_topk_rows<false>, v1_topk_rows<true>, v1_topk_segments, v1_topk_merge, a->cols,
+                                 a->batch, a->topk,
                                  a->workspace, a->workspace_bytes, p, as_stream(stream), "v1_topk");
 }
 
@@ -1482,7 +1560,8 @@ extern "C" int v1_topk_transform(const v1_topk_transform_args* a, void* stream) 
     if (a->batch == 0) return V1_OK;
     TransformParams p{a->scores, a->score_stride, a->cols, a->seq_lens, a->page_table, a->page_table_stride,
                       a->page_table_cols, a->page_bits, a->page_indices, a->raw_indices, a->topk};
-    return launch_topk<TransformParams>(transform_rows, transform_segments, transform_merge, a->cols, a->batch,
+    return launch_topk<TransformParams>(transform_rows<false>, transform_rows<true>, transform_segments,
+                                        transform_merge, a->cols, a->batch,
                                         a->topk, a->workspace, a->workspace_bytes, p, as_stream(stream),
                                         "topk_transform");
 }

@@ -687,7 +687,7 @@ def _adversarial_rows(kind, g, cols):
 
 @pytest.mark.parametrize("kind", ["plateau", "ascending", "descending", "neg_inf_heavy", "two_values", "tiny_spread",
                                   "signed_zero", "nan_sprinkled", "nan_heavy"])
-@pytest.mark.parametrize("cols", [2049, 9000, 32768, 100000])
+@pytest.mark.parametrize("cols", [2049, 8192, 9000, 32768, 100000])
 def test_topk_adversarial_rows(dev, kind, cols):
     g = np.random.default_rng(cols)
     B = 4
@@ -734,13 +734,15 @@ def test_topk_large_batch_vs_oracle(dev, cols):
 
 @pytest.mark.parametrize("page_size", [16, 64, 128, 1024])
 @pytest.mark.parametrize("short_table", [False, True])
-def test_topk_transform_page_sizes(dev, page_size, short_table):
+@pytest.mark.parametrize("cols", [32768, 6000])
+def test_topk_transform_page_sizes(dev, page_size, short_table, cols):
     """Page sizes either side of 64 tokens (the register-resident rows take
     tables of at most 512 entries, smaller pages stream), a page table that
     covers only part of each row (positions past it map to -1), rows of every
-    length class, more rows than CUs, and no raw output on half the calls."""
+    length class, more rows than CUs, and no raw output on half the calls;
+    at 6000 columns every row is held in registers (the short-row kernel)."""
     g = np.random.default_rng(page_size + short_table)
-    B, cols = 700, 32768
+    B = 700
     scores = np.round(g.standard_normal((B, cols)) * 30).astype(np.float32)
     lens = g.integers(1, cols + 1, B).astype(np.int32)
     lens[:4] = [cols, 2048, 2049, 1]
