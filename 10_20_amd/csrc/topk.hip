@@ -1332,7 +1332,11 @@ __device__ __forceinline__ CandSrc cand_source(const Workspace& ws, int64_t row)
     return CandSrc{ws.keys + ws.at(row, 0), ws.count + row * ws.nseg, ws.T, ws.nseg, ws.nseg * ws.T};
 }
 
-__global__ __launch_bounds__(kBlock, 8) void v1_topk_merge(V1Params p, Workspace ws) {
+// kShortMerge: the segments' candidates (nseg * T) fit kShort (select_short);
+// one work-group per row, so that instance may take more registers than the
+// 64 that four work-groups per CU allow.
+template <bool kShortMerge>
+__global__ __launch_bounds__(kBlock, kShortMerge ? 4 : 8) void v1_topk_merge(V1Params p, Workspace ws) {
     __shared__ SelSmem sm;
     const int64_t row = blockIdx.x;
     const RowInfo ri = v1_row_info(p, row);
@@ -1352,15 +1356,20 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_merge(V1Params p, Workspace
         for (int tx = threadIdx.x; tx < T; tx += kBlock) v1_emit(p, row, ri, tx, pos[tx], keys[tx] == kNegInfKey);
     } else {
         const int32_t* pos = ws.pos + ws.at(row, 0);
-        select_stream(cand_source(ws, row), (uint32_t)T, sm, [&](const auto& at, const auto& q, const auto& key) {
+        auto emit = [&](const auto& at, const auto& q, const auto& key) {
 #pragma unroll
             for (int i = 0; i < (int)(sizeof(at) / sizeof(at[0])); ++i)
                 if (at[i] >= 0) v1_emit(p, row, ri, at[i], pos[q[i]], key[i] == kNegInfKey);
-        });
+        };
+        if constexpr (kShortMerge)
+            select_short(cand_source(ws, row), (uint32_t)T, sm, emit);
+        else
+            select_stream(cand_source(ws, row), (uint32_t)T, sm, emit);
     }
     v1_pad_expansion(p, row);
 }
 
+template <bool kShortMerge>
 __global__ __launch_bounds__(kBlock, 8) void transform_merge(TransformParams p, Workspace ws) {
     __shared__ SelSmem sm;
     const int64_t row = blockIdx.x;
@@ -1377,7 +1386,7 @@ __global__ __launch_bounds__(kBlock, 8) void transform_merge(TransformParams p, 
         return;
     }
     const int32_t nq = ws.nseg * T;
-    select_stream(cand_source(ws, row), (uint32_t)T, sm, [&](const auto& at, const auto& q, const auto&) {
+    auto emit = [&](const auto& at, const auto& q, const auto&) {
         constexpr int N = sizeof(at) / sizeof(at[0]);
         int32_t raw[N];
 #pragma unroll
@@ -1385,7 +1394,11 @@ __global__ __launch_bounds__(kBlock, 8) void transform_merge(TransformParams p, 
         transform_emit_batch<N>(p.page_table + row * p.page_table_stride, p.page_table_cols, p.page_bits,
                                 p.page_indices + row * p.topk, p.raw_indices ? p.raw_indices + row * p.topk : nullptr,
                                 at, raw);
-    });
+    };
+    if constexpr (kShortMerge)
+        select_short(cand_source(ws, row), (uint32_t)T, sm, emit);
+    else
+        select_stream(cand_source(ws, row), (uint32_t)T, sm, emit);
 }
 
 // ------------------------------------------------------ unfused mask/map
@@ -1473,8 +1486,8 @@ __global__ void output_ids_kernel(const int32_t* raw_in, const float* scores, in
 
 template <typename P>
 int launch_topk(void (*single)(P), void (*single_short)(P), void (*seg)(P, Workspace), void (*merge)(P, Workspace),
-                int32_t cols, int32_t batch, int32_t topk, void* wsp, int64_t ws_bytes, const P& p, hipStream_t st,
-                const char* name) {
+                void (*merge_short)(P, Workspace), int32_t cols, int32_t batch, int32_t topk, void* wsp,
+                int64_t ws_bytes, const P& p, hipStream_t st, const char* name) {
     const SegPlan plan = plan_segments(batch, cols, topk);
     const int64_t need = workspace_bytes(batch, plan, topk);
     // rows within one work-group's span also run in one pass when the caller
@@ -1493,7 +1506,8 @@ int launch_topk(void (*single)(P), void (*single_short)(P), void (*seg)(P, Works
     hipLaunchKernelGGL(seg, dim3(ws.nseg, batch), dim3(kBlock), 0, st, p, ws);
     int rc = V1_LAUNCHED(name);
     if (rc != V1_OK) return rc;
-    hipLaunchKernelGGL(merge, dim3(batch), dim3(kBlock), 0, st, p, ws);
+    hipLaunchKernelGGL((int64_t)ws.nseg * topk <= kShort ? merge_short : merge, dim3(batch), dim3(kBlock), 0, st, p,
+                       ws);
     return V1_LAUNCHED(name);
 }
 
@@ -1547,8 +1561,8 @@ extern "C" int v1_topk(const v1_topk_args* a, void* stream) {
                a->pages, a->selected, a->selected_bits == 64, a->take_stride, a->lens, a->takes, a->physical,
                a->logical, a->raw, a->topk, a->window, a->mask, a->expanded, a->expansion_stride,
                a->physical_output, a->bucket_from_rank, a->fine_table, a->fine_table_cols, a->direct_fine};
-    return launch_topk<V1Params>(v1_topk_rows<false>, v1_topk_rows<true>, v1_topk_segments, v1_topk_merge, a->cols,
-                                 a->batch, a->topk,
+    return launch_topk<V1Params>(v1_topk_rows<false>, v1_topk_rows<true>, v1_topk_segments, v1_topk_merge<false>,
+                                 v1_topk_merge<true>, a->cols, a->batch, a->topk,
                                  a->workspace, a->workspace_bytes, p, as_stream(stream), "v1_topk");
 }
 
@@ -1561,7 +1575,7 @@ extern "C" int v1_topk_transform(const v1_topk_transform_args* a, void* stream) 
     TransformParams p{a->scores, a->score_stride, a->cols, a->seq_lens, a->page_table, a->page_table_stride,
                       a->page_table_cols, a->page_bits, a->page_indices, a->raw_indices, a->topk};
     return launch_topk<TransformParams>(transform_rows<false>, transform_rows<true>, transform_segments,
-                                        transform_merge, a->cols, a->batch,
+                                        transform_merge<false>, transform_merge<true>, a->cols, a->batch,
                                         a->topk, a->workspace, a->workspace_bytes, p, as_stream(stream),
                                         "topk_transform");
 }

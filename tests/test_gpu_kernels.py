@@ -263,8 +263,11 @@ def _v1_case(g, B, cols, take_max, ties):
 
 @pytest.mark.parametrize("cols,topk,ties", [(700, 256, True), (2688, 2048, True), (6000, 2048, False),
                                              (20000, 2048, True), (32768, 2048, False), (70000, 2048, True),
-                                             (40000, 512, False)])
+                                             (40000, 512, False), (200000, 2048, True)])
 def test_fused_topk_random_vs_oracle(dev, cols, topk, ties):
+    """Register-resident rows (<= 8192 columns), streamed rows, and segmented
+    rows whose merge holds the candidates in registers (<= 4 segments at
+    T = 2048) or streams them (7 segments at 200000 columns)."""
     g = np.random.default_rng(cols + topk)
     B = 513
     c = _v1_case(g, B, cols, 40, ties)
@@ -304,8 +307,12 @@ def test_fused_topk_rejects_like_reference(dev):
 
 
 @pytest.mark.parametrize("B,cols,topk", [(16, 5000, 2048), (128, 131072, 2048), (3, 100000, 64), (600, 3000, 700),
-                                         (6, 70000, 2047)])
+                                         (6, 70000, 2047), (4, 200000, 2048)])
 def test_topk_transform_vs_oracle(dev, B, cols, topk):
+    """Single-pass rows (register-resident up to 8192 columns) and segmented
+    rows; the merge holds the segments' candidates in registers while they
+    fit 8192 (up to 4 segments at T = 2048) and streams them past that
+    (7 segments at 200000 columns)."""
     g = np.random.default_rng(B * cols)
     scores = np.round(g.standard_normal((B, cols)) * 50).astype(np.float32)
     lens = g.integers(1, cols + 1, B).astype(np.int32)
