@@ -13,12 +13,19 @@ namespace v1 {
 namespace {
 
 constexpr int kThreads = 256;
-// Slots per work-group.  Measured on MI355X with 656-byte rows: when the
-// pool's rows come from HBM (a pool well above the caches), 64-slot tiles
-// (42 KB of output per work-group) beat 256-slot ones by 5%; when a small pool
-// stays cache-resident, 256-slot tiles are 2-3% faster.
+// Tiles, measured on MI355X with 656-byte rows.  When the pool's rows come
+// from HBM (a pool well above the caches), 64-slot tiles (42 KB of output per
+// 256-thread work-group) beat 256-slot ones by 5%.  When a small pool stays
+// cache-resident, the workspace writes set the pace, and they run fastest with
+// few concurrent write streams: 512-slot tiles (336 KB) copied by 1024-thread
+// work-groups, one per CU (1.006-1.010 ms for 4096 x 2048 rows against
+// 1.034-1.046 ms for 256-slot tiles of 256 threads, eight per CU; two of the
+// 1024-thread work-groups per CU take 1.030 ms).  The one-per-CU residency
+// is set by reserving more than half of the CU's 160 KB of LDS.
 constexpr int kTileSmall = 64;
-constexpr int kTileLarge = 256;
+constexpr int kTileCached = 512;
+constexpr int kThreadsCached = 1024;
+constexpr size_t kOneWgPerCuLds = 84u << 10;
 constexpr int64_t kCachedPoolBytes = 64ll << 20;
 constexpr int kUnroll = 8;       // independent 16-byte copies in flight per thread
 
@@ -56,14 +63,14 @@ struct RowMap {
 };
 
 // Copies `chunks` 16-byte chunks per slot for slots [tile*kTileSlots, ...).
-template <int kTileSlots>
-__global__ __launch_bounds__(kThreads) void gather_rows16(
+template <int kTileSlots, int kThr>
+__global__ __launch_bounds__(kThr) void gather_rows16(
     const uint8_t* __restrict__ pool, RowMap rm, int64_t total_slots, int32_t chunks,
     uint32_t chunk_magic, int64_t out_row_bytes, uint8_t* __restrict__ out) {
     __shared__ int64_t src[kTileSlots];
     const int64_t first = (int64_t)blockIdx.x * kTileSlots;
     const int tid = threadIdx.x;
-    for (int s = tid; s < kTileSlots; s += kThreads) {
+    for (int s = tid; s < kTileSlots; s += kThr) {
         const int64_t t = first + s;
         src[s] = t < total_slots ? rm(t) : -1;
     }
@@ -72,12 +79,12 @@ __global__ __launch_bounds__(kThreads) void gather_rows16(
     const int slots = left < kTileSlots ? (int)left : kTileSlots;
     const uint32_t n = (uint32_t)slots * (uint32_t)chunks;
     uint8_t* out_tile = out + first * out_row_bytes;
-    for (uint32_t base = 0; base < n; base += kThreads * kUnroll) {
+    for (uint32_t base = 0; base < n; base += kThr * kUnroll) {
         u32x4 v[kUnroll];
         uint32_t g[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            g[u] = base + u * kThreads + tid;
+            g[u] = base + u * kThr + tid;
             v[u] = u32x4{0u, 0u, 0u, 0u};
             if (g[u] < n) {
                 const uint32_t s = chunks == 1 ? g[u] : small_div(g[u], chunk_magic);
@@ -118,11 +125,11 @@ int launch_rows(const uint8_t* pool, const RowMap& rm, int64_t total, int64_t ro
     const int32_t chunks = (int32_t)(row_bytes / 16);
     const uint32_t magic = chunks == 1 ? 0u : small_div_magic((uint32_t)chunks);
     if (pool_bytes > kCachedPoolBytes)
-        hipLaunchKernelGGL(gather_rows16<kTileSmall>, dim3((uint32_t)cdiv(total, kTileSmall)), dim3(kThreads), 0, st,
-                           pool, rm, total, chunks, magic, row_bytes, out);
+        hipLaunchKernelGGL((gather_rows16<kTileSmall, kThreads>), dim3((uint32_t)cdiv(total, kTileSmall)), dim3(kThreads),
+                           0, st, pool, rm, total, chunks, magic, row_bytes, out);
     else
-        hipLaunchKernelGGL(gather_rows16<kTileLarge>, dim3((uint32_t)cdiv(total, kTileLarge)), dim3(kThreads), 0, st,
-                           pool, rm, total, chunks, magic, row_bytes, out);
+        hipLaunchKernelGGL((gather_rows16<kTileCached, kThreadsCached>), dim3((uint32_t)cdiv(total, kTileCached)),
+                           dim3(kThreadsCached), kOneWgPerCuLds, st, pool, rm, total, chunks, magic, row_bytes, out);
     return V1_LAUNCHED("gather_rows16");
 }
 
