@@ -14,8 +14,11 @@ namespace {
 
 constexpr int kThreads = 256;
 // Tiles, measured on MI355X with 656-byte rows.  When the pool's rows come
-// from HBM (a pool well above the caches), 64-slot tiles (42 KB of output per
-// 256-thread work-group) beat 256-slot ones by 5%.  When a small pool stays
+// from HBM (a pool well above the caches), 64-slot tiles (42 KB of output)
+// beat 256-slot ones by 5%, and copied by 512 threads with 5 loads in flight
+// each (one pass over a tile's 2624 chunks) they take 417 us for 1024 x 2048
+// rows from a 688 MB pool, against 431 us with 256 threads and 8 loads each
+// (32-slot and 128-slot tiles, 1024 threads and 4-8 loads: 418-442 us).  When a small pool stays
 // cache-resident, the workspace writes set the pace, and they run fastest with
 // few concurrent write streams: 512-slot tiles (336 KB) copied by 1024-thread
 // work-groups, one per CU (1.006-1.010 ms for 4096 x 2048 rows against
@@ -23,11 +26,13 @@ constexpr int kThreads = 256;
 // 1024-thread work-groups per CU take 1.030 ms).  The one-per-CU residency
 // is set by reserving more than half of the CU's 160 KB of LDS.
 constexpr int kTileSmall = 64;
+constexpr int kThreadsSmall = 512;
+constexpr int kUnrollSmall = 5;
 constexpr int kTileCached = 512;
 constexpr int kThreadsCached = 1024;
 constexpr size_t kOneWgPerCuLds = 84u << 10;
 constexpr int64_t kCachedPoolBytes = 64ll << 20;
-constexpr int kUnroll = 8;       // independent 16-byte copies in flight per thread
+constexpr int kUnrollCached = 8;  // independent 16-byte copies in flight per thread
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -63,7 +68,7 @@ struct RowMap {
 };
 
 // Copies `chunks` 16-byte chunks per slot for slots [tile*kTileSlots, ...).
-template <int kTileSlots, int kThr>
+template <int kTileSlots, int kThr, int kUnroll>
 __global__ __launch_bounds__(kThr) void gather_rows16(
     const uint8_t* __restrict__ pool, RowMap rm, int64_t total_slots, int32_t chunks,
     uint32_t chunk_magic, int64_t out_row_bytes, uint8_t* __restrict__ out) {
@@ -125,10 +130,10 @@ int launch_rows(const uint8_t* pool, const RowMap& rm, int64_t total, int64_t ro
     const int32_t chunks = (int32_t)(row_bytes / 16);
     const uint32_t magic = chunks == 1 ? 0u : small_div_magic((uint32_t)chunks);
     if (pool_bytes > kCachedPoolBytes)
-        hipLaunchKernelGGL((gather_rows16<kTileSmall, kThreads>), dim3((uint32_t)cdiv(total, kTileSmall)), dim3(kThreads),
-                           0, st, pool, rm, total, chunks, magic, row_bytes, out);
+        hipLaunchKernelGGL((gather_rows16<kTileSmall, kThreadsSmall, kUnrollSmall>), dim3((uint32_t)cdiv(total, kTileSmall)),
+                           dim3(kThreadsSmall), 0, st, pool, rm, total, chunks, magic, row_bytes, out);
     else
-        hipLaunchKernelGGL((gather_rows16<kTileCached, kThreadsCached>), dim3((uint32_t)cdiv(total, kTileCached)),
+        hipLaunchKernelGGL((gather_rows16<kTileCached, kThreadsCached, kUnrollCached>), dim3((uint32_t)cdiv(total, kTileCached)),
                            dim3(kThreadsCached), kOneWgPerCuLds, st, pool, rm, total, chunks, magic, row_bytes, out);
     return V1_LAUNCHED("gather_rows16");
 }

@@ -52,6 +52,7 @@ PEAK_FP8_TFLOPS = 5000.0
 TRAFFIC = {
     4: (ROOT / "profiles" / "prefill_chunk_4096x32k.md",
         {"score": ("score_prep", "score_shared", "score_exact"), "topk": ("transform_rows",), "gather": ("gather_rows16",)}),
+    3: (ROOT / "profiles" / "slot_gather_1024x2048.md", {"gather": ("gather_rows16",)}),
     6: (ROOT / "profiles" / "index_build_2048x1024.md", {"build": ("build_buckets_kernel",)}),
     2: (ROOT / "profiles" / "page_management_4096req.md",
         {"insert": ("pb_init", "pb_hash", "pb_classify", "pb_slow_live", "pb_slow", "pb_allocate", "pb_table",
