@@ -1,10 +1,11 @@
 // Slot gather: copies one source row per (query row, top slot) into a dense
-// workspace, zero-filling padding ids.  Pure HBM work: each block first maps
-// its tile of slots to source byte offsets in LDS (one id / map lookup per
-// slot), then all 256 threads stream the tile as 16-byte chunks so that both
-// the workspace writes and the per-row reads are fully coalesced.  Workspace
+// workspace, zero-filling padding ids.  Pure HBM work: each work-group first
+// maps its tile of slots to source byte offsets in LDS (one id / map lookup
+// per slot), then copies the tile as 16-byte chunks in one pass: every lane
+// issues all of its loads, then all of its stores, and exits.  Both the
+// workspace writes and the per-row reads are fully coalesced.  Workspace
 // stores are non-temporal: the workspace is written once per call and read by
-// the attention consumer, while the (smaller) source pool stays cache resident.
+// the attention consumer.
 //
 // Semantics follow sglang/srt/layers/attention/v1_native/kernels.py:62-77.
 #include "common.h"
@@ -13,26 +14,26 @@ namespace v1 {
 namespace {
 
 constexpr int kThreads = 256;
-// Tiles, measured on MI355X with 656-byte rows.  When the pool's rows come
-// from HBM (a pool well above the caches), 64-slot tiles (42 KB of output)
-// beat 256-slot ones by 5%, and copied by 512 threads with 5 loads in flight
-// each (one pass over a tile's 2624 chunks) they take 417 us for 1024 x 2048
-// rows from a 688 MB pool, against 431 us with 256 threads and 8 loads each
-// (32-slot and 128-slot tiles, 1024 threads and 4-8 loads: 418-442 us).  When a small pool stays
-// cache-resident, the workspace writes set the pace, and they run fastest with
-// few concurrent write streams: 512-slot tiles (336 KB) copied by 1024-thread
-// work-groups, one per CU (1.006-1.010 ms for 4096 x 2048 rows against
-// 1.034-1.046 ms for 256-slot tiles of 256 threads, eight per CU; two of the
-// 1024-thread work-groups per CU take 1.030 ms).  The one-per-CU residency
-// is set by reserving more than half of the CU's 160 KB of LDS.
-constexpr int kTileSmall = 64;
-constexpr int kThreadsSmall = 512;
-constexpr int kUnrollSmall = 5;
-constexpr int kTileCached = 512;
-constexpr int kThreadsCached = 1024;
-constexpr size_t kOneWgPerCuLds = 84u << 10;
+// Copy shapes, measured on MI355X with 656-byte rows (41 chunks) and
+// 1024 x 2048 or 4096 x 2048 slots.  A tile is the largest power of two of
+// slots whose chunks fit one pass of kThr x kUnroll loads; tiles that are not
+// a power of two end mid-row on the XCDs' round-robin and take 1.2-1.8x as
+// long.  A small pool (at most 64 MB) stays cache-resident and the workspace
+// writes set the pace: 1024 threads x 11 loads (256-slot tiles, two
+// work-groups per CU) copy 4096 x 2048 rows of a 21.5 MB pool in 0.88 ms,
+// against 0.96-0.98 ms for 512-slot tiles (21 loads, or 8 loads over three
+// passes), 0.93 ms for 128-slot tiles and 1.04-1.06 ms for 64-slot ones.  A
+// pool well above the caches streams from HBM and favours short tiles:
+// 512 threads x 6 loads (64-slot tiles) copy 1024 x 2048 rows of a 688 MB
+// pool in 410 us, against 412-418 us for 128- and 256-slot tiles.
+constexpr int kThreadsCached = 1024, kUnrollCached = 11;
+constexpr int kThreadsStream = 512, kUnrollStream = 6;
+constexpr int kMaxTile = 1024;  // LDS offsets per work-group
 constexpr int64_t kCachedPoolBytes = 64ll << 20;
-constexpr int kUnrollCached = 8;  // independent 16-byte copies in flight per thread
+// Word 3 of a raw buffer descriptor (stride 0, 32-bit dwords): stores at byte
+// offsets at or past the descriptor's length are dropped.
+constexpr int32_t kRawDword = 0x00020000;
+constexpr int kNonTemporal = 2;  // buffer store cache policy: nt
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -67,48 +68,57 @@ struct RowMap {
     }
 };
 
-// Copies `chunks` 16-byte chunks per slot for slots [tile*kTileSlots, ...).
-template <int kTileSlots, int kThr, int kUnroll>
+// Copies the (1 << tile_shift)-slot tile blockIdx.x of `chunks` 16-byte
+// chunks per slot into the dense workspace `out`.  The copy has no branches:
+// lanes of padding slots, and lanes past the tile's last chunk, load the
+// pool's first chunk and zero it, and the stores go through a descriptor
+// that ends at the tile's last byte, so the hardware drops those past it.
+// Without branches the compiler waits for each load just before its store;
+// with per-lane conditions around loads and stores it waited for every
+// outstanding store before issuing the next loads.  `pool` must hold at
+// least one row.
+template <int kThr, int kUnroll>
 __global__ __launch_bounds__(kThr) void gather_rows16(
     const uint8_t* __restrict__ pool, RowMap rm, int64_t total_slots, int32_t chunks,
-    uint32_t chunk_magic, int64_t out_row_bytes, uint8_t* __restrict__ out) {
-    __shared__ int64_t src[kTileSlots];
-    const int64_t first = (int64_t)blockIdx.x * kTileSlots;
+    uint32_t chunk_magic, int32_t tile_shift, uint8_t* __restrict__ out) {
+    __shared__ int64_t src[kMaxTile];
+    const int tile = 1 << tile_shift;
+    const int64_t first = (int64_t)blockIdx.x << tile_shift;
     const int tid = threadIdx.x;
-    for (int s = tid; s < kTileSlots; s += kThr) {
+    for (int s = tid; s < tile; s += kThr) {
         const int64_t t = first + s;
         src[s] = t < total_slots ? rm(t) : -1;
     }
     __syncthreads();
     const int64_t left = total_slots - first;
-    const int slots = left < kTileSlots ? (int)left : kTileSlots;
+    const int slots = left < tile ? (int)left : tile;
     const uint32_t n = (uint32_t)slots * (uint32_t)chunks;
-    uint8_t* out_tile = out + first * out_row_bytes;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(out + first * (int64_t)chunks * 16, 0, (int32_t)(n * 16u),
+                                                      kRawDword);
     for (uint32_t base = 0; base < n; base += kThr * kUnroll) {
         u32x4 v[kUnroll];
-        uint32_t g[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            g[u] = base + u * kThr + tid;
-            v[u] = u32x4{0u, 0u, 0u, 0u};
-            if (g[u] < n) {
-                const uint32_t s = chunks == 1 ? g[u] : small_div(g[u], chunk_magic);
-                const uint32_t c = g[u] - s * (uint32_t)chunks;
-                const int64_t off = src[s];
-                if (off >= 0)
-                    v[u] = *reinterpret_cast<const u32x4*>(pool + off + (int64_t)c * 16);
-            }
+            const uint32_t g = base + u * kThr + tid;
+            uint32_t sl = chunks == 1 ? g : small_div(g, chunk_magic);
+            sl = sl < (uint32_t)slots ? sl : (uint32_t)(slots - 1);
+            const uint32_t c = g - sl * (uint32_t)chunks;
+            const int64_t off = src[sl];
+            const bool ok = off >= 0 && g < n;
+            v[u] = *reinterpret_cast<const u32x4*>(ok ? pool + off + (int64_t)c * 16 : pool);
+            if (!ok) v[u] = u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            if (g[u] < n) {
-                const uint32_t s = chunks == 1 ? g[u] : small_div(g[u], chunk_magic);
-                const uint32_t c = g[u] - s * (uint32_t)chunks;
-                u32x4* dst = reinterpret_cast<u32x4*>(out_tile + (int64_t)s * out_row_bytes + (int64_t)c * 16);
-                __builtin_nontemporal_store(v[u], dst);
-            }
-        }
+        for (int u = 0; u < kUnroll; ++u)
+            __builtin_amdgcn_raw_buffer_store_b128(v[u], rs, (int32_t)((base + u * kThr + tid) * 16u), 0, kNonTemporal);
     }
+}
+
+// Largest power-of-two tile (log2) whose chunks fit one pass of `per_pass`.
+int tile_shift_for(int32_t chunks, int per_pass) {
+    int shift = 0;
+    while ((1 << (shift + 1)) <= kMaxTile && (int64_t)chunks << (shift + 1) <= per_pass) ++shift;
+    return shift;
 }
 
 // Element-wise fallback for strided rows (any element stride, 128 elements).
@@ -128,13 +138,22 @@ int launch_rows(const uint8_t* pool, const RowMap& rm, int64_t total, int64_t ro
                 uint8_t* out, hipStream_t st) {
     if (total == 0) return V1_OK;
     const int32_t chunks = (int32_t)(row_bytes / 16);
+    if (pool_bytes == 0) {
+        // every slot is a padding slot: zero rows, with no pool row to load
+        hipLaunchKernelGGL(gather_strided<uint8_t>, dim3((uint32_t)cdiv(total * row_bytes, kThreads)), dim3(kThreads), 0,
+                           st, pool, rm, total, (int64_t)1, (int32_t)row_bytes, out);
+        return V1_LAUNCHED("gather_strided");
+    }
     const uint32_t magic = chunks == 1 ? 0u : small_div_magic((uint32_t)chunks);
-    if (pool_bytes > kCachedPoolBytes)
-        hipLaunchKernelGGL((gather_rows16<kTileSmall, kThreadsSmall, kUnrollSmall>), dim3((uint32_t)cdiv(total, kTileSmall)),
-                           dim3(kThreadsSmall), 0, st, pool, rm, total, chunks, magic, row_bytes, out);
-    else
-        hipLaunchKernelGGL((gather_rows16<kTileCached, kThreadsCached, kUnrollCached>), dim3((uint32_t)cdiv(total, kTileCached)),
-                           dim3(kThreadsCached), kOneWgPerCuLds, st, pool, rm, total, chunks, magic, row_bytes, out);
+    if (pool_bytes > kCachedPoolBytes) {
+        const int shift = tile_shift_for(chunks, kThreadsStream * kUnrollStream);
+        hipLaunchKernelGGL((gather_rows16<kThreadsStream, kUnrollStream>), dim3((uint32_t)cdiv(total, 1ll << shift)),
+                           dim3(kThreadsStream), 0, st, pool, rm, total, chunks, magic, shift, out);
+    } else {
+        const int shift = tile_shift_for(chunks, kThreadsCached * kUnrollCached);
+        hipLaunchKernelGGL((gather_rows16<kThreadsCached, kUnrollCached>), dim3((uint32_t)cdiv(total, 1ll << shift)),
+                           dim3(kThreadsCached), 0, st, pool, rm, total, chunks, magic, shift, out);
+    }
     return V1_LAUNCHED("gather_rows16");
 }
 

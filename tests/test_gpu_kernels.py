@@ -89,6 +89,40 @@ def test_gather_rows_vs_oracle(dev, row_bytes, paged):
     assert np.array_equal(H(out), O.gather_rows(pool, ids, table, 6 if paged else 0))
 
 
+@pytest.mark.parametrize("row_bytes", [16, 656, 65520])
+@pytest.mark.parametrize("big", [False, True])
+def test_gather_rows_tiles_and_passes(dev, row_bytes, big):
+    """Both copy shapes: pools up to 64 MB (1024 threads x 11 loads per pass)
+    and larger ones (512 threads x 6), with tiles of 1024 one-chunk rows, 256
+    or 64 rows of 41 chunks, and 4095-chunk rows that take one slot per tile
+    and two passes (larger pool) or two slots in one pass; slot counts that
+    end in a partial tile, padding ids and per-row page tables."""
+    g = np.random.default_rng(row_bytes * 2 + big)
+    pool_bytes = (72 << 20) if big else (3 << 20)
+    pool_rows = max(64, (pool_bytes // row_bytes) // 64 * 64)
+    rows, top = (3, 37) if row_bytes > 4096 else (5, 1111)
+    pool = g.integers(0, 256, (pool_rows, row_bytes), dtype=np.uint8)
+    pages = pool_rows // 64
+    table = np.stack([g.permutation(pages)[:min(pages, 16)] for _ in range(rows)]).astype(np.int32)
+    ids = g.integers(0, table.shape[1] * 64, (rows, top)).astype(np.int32)
+    ids[g.random((rows, top)) < 0.05] = -1
+    out = torch.full((rows, top, row_bytes), 7, device=dev, dtype=torch.uint8)
+    NK.gather_rows(T(pool, dev), T(ids, dev), out, T(table, dev), 6)
+    assert np.array_equal(H(out), O.gather_rows(pool, ids, table, 6))
+
+
+def test_gather_slots_empty_pool(dev):
+    """A pool with no slots: every slot is padding and comes out as zeros."""
+    kp = torch.empty((0, 2, 128), device=dev, dtype=torch.bfloat16)
+    req = torch.tensor([0, 1], device=dev, dtype=torch.int32)
+    ids = torch.tensor([[0, 1, -1]], device=dev, dtype=torch.int32)
+    out_k = torch.full((1, 3, 1, 128), 5.0, device=dev, dtype=torch.bfloat16)
+    out_v = torch.full_like(out_k, 5.0)
+    NK._gather_slots[(1,)](kp, kp, req, ids, out_k, out_v, 1, 3, 0, *kp.stride(), *kp.stride(), ids.stride(0), 32,
+                           num_warps=4)
+    assert not H(out_k.float()).any() and not H(out_v.float()).any()
+
+
 def test_gather_rows_shared_map_and_bad_ids(dev):
     pool = np.arange(64 * 32, dtype=np.int64).astype(np.uint8).reshape(64, 32)
     req = np.int32([5, 1, 70, 0])  # entry 2 points past the pool
