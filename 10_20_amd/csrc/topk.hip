@@ -949,6 +949,93 @@ __device__ __forceinline__ void v1_emit(const V1Params& p, int64_t row, const Ro
     }
 }
 
+// v1_emit for four slots [tx0, tx0 + 4) at once: every level of the
+// selected -> rt -> members -> nt chain is loaded for the four slots together,
+// at indices clamped into their arrays, and v1_emit's conditions are applied
+// to the loaded values afterwards, so a thread waits for four dependent loads
+// instead of four per slot.  Slots at or past T are skipped.
+__device__ __forceinline__ void v1_emit4(const V1Params& p, int64_t row, const RowInfo& ri, int32_t tx0,
+                                         const int32_t (&raw)[4], const bool (&neg_inf)[4]) {
+    int32_t page[4], logical[4], physical[4];
+    bool live[4], member[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        live[i] = raw[i] >= 0 && !neg_inf[i];
+        member[i] = raw[i] < ri.take * 64;
+        page[i] = -1;
+    }
+    const int32_t last_rank = max(ri.take - 1, 0);
+    if (ri.take > 0) {
+        if (p.direct_fine) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                page[i] = p.fine_table[row * p.fine_table_cols + min(max(raw[i], 0) / 64, last_rank)];
+        } else {
+            int32_t rank[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rank[i] = sel_rank(p, row, min(max(raw[i], 0) / 64, last_rank));
+            if (p.pages > 0) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int32_t pg = p.rt[row * p.pages + min(max(rank[i], 0), p.pages - 1)];
+                    page[i] = rank[i] >= 0 && rank[i] < p.pages ? pg : -1;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) logical[i] = -1;
+    if (p.member_pages > 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int32_t m = p.members[(int64_t)min(max(page[i], 0), p.member_pages - 1) * 64 + (raw[i] & 63)];
+            logical[i] = page[i] >= 0 && page[i] < p.member_pages ? m : -1;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int32_t off = raw[i] - ri.take * 64;
+        if (!member[i]) logical[i] = off < ri.sink ? off : ri.tail + off - ri.sink;
+        if (!live[i]) logical[i] = -1;
+        physical[i] = -1;
+    }
+    if (p.pages > 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool ok = logical[i] >= 0 && logical[i] < ri.n && logical[i] / 64 < p.pages;
+            const int32_t np = p.nt[row * p.pages + min(max(logical[i], 0) / 64, p.pages - 1)];
+            physical[i] = ok ? np * 64 + (logical[i] & 63) : -1;
+            if (!ok) logical[i] = -1;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) logical[i] = -1;
+    }
+    const int32_t T = p.topk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int32_t tx = tx0 + i;
+        if (tx >= T) continue;
+        const int64_t dst = row * T + tx;
+        p.logical[dst] = logical[i];
+        if (p.physical_output) {
+            p.physical[dst] = physical[i];
+            p.raw[dst] = raw[i];
+        }
+        if (p.expansion_stride) {
+            const int32_t b = logical[i] * 4;
+            int4 v = logical[i] < 0 ? make_int4(-1, -1, -1, -1) : make_int4(b, b + 1, b + 2, b + 3);
+            *reinterpret_cast<int4*>(p.expanded + row * p.expansion_stride + 4 * tx) = v;
+        }
+    }
+}
+
+// Winners staged by slot in the candidate-key array (free once the ranks are
+// taken): a raw position, or a merge's workspace candidate index, with bit 31
+// set for a -inf key.
+constexpr uint32_t kStagedNegInf = 0x80000000u;
+__device__ __forceinline__ uint32_t* v1_stage(SelSmem& sm) { return sm.cand_key; }
+
 __device__ __forceinline__ void v1_pad_expansion(const V1Params& p, int64_t row) {
     if (p.expansion_stride)
         for (int j = p.topk * 4 + threadIdx.x; j < p.expansion_stride; j += kBlock)
@@ -1104,15 +1191,28 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_rows(V1Params p) {
             v1_emit(p, row, ri, tx, tx < L ? tx : -1, inf);
         }
     } else {
+        uint32_t* stage = v1_stage(sm);
         auto emit = [&](const auto& at, const auto& pos, const auto& key) {
 #pragma unroll
             for (int i = 0; i < (int)(sizeof(at) / sizeof(at[0])); ++i)
-                if (at[i] >= 0) v1_emit(p, row, ri, at[i], (int32_t)pos[i], key[i] == kNegInfKey);
+                if (at[i] >= 0) stage[at[i]] = (uint32_t)pos[i] | (key[i] == kNegInfKey ? kStagedNegInf : 0u);
         };
         if constexpr (kShortRows)
             select_short(src, (uint32_t)T, sm, emit);
         else
             select_stream(src, (uint32_t)T, sm, emit);
+        // (the selection ends with a barrier: every slot is staged)
+        for (int32_t tx0 = 4 * threadIdx.x; tx0 < T; tx0 += 4 * kBlock) {
+            int32_t raw[4];
+            bool inf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t v = tx0 + i < T ? stage[tx0 + i] : 0u;
+                raw[i] = (int32_t)(v & ~kStagedNegInf);
+                inf[i] = (v & kStagedNegInf) != 0;
+            }
+            v1_emit4(p, row, ri, tx0, raw, inf);
+        }
     }
     v1_pad_expansion(p, row);
 }
@@ -1353,18 +1453,41 @@ __global__ __launch_bounds__(kBlock, kShortMerge ? 4 : 8) void v1_topk_merge(V1P
         // one non-empty segment: its list is the row's Top-T in position order
         const int32_t* pos = ws.pos + ws.at(row, 0);
         const uint32_t* keys = ws.keys + ws.at(row, 0);
-        for (int tx = threadIdx.x; tx < T; tx += kBlock) v1_emit(p, row, ri, tx, pos[tx], keys[tx] == kNegInfKey);
+        for (int32_t tx0 = 4 * threadIdx.x; tx0 < T; tx0 += 4 * kBlock) {
+            int32_t raw[4];
+            bool inf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int32_t tx = min(tx0 + i, T - 1);
+                raw[i] = pos[tx];
+                inf[i] = keys[tx] == kNegInfKey;
+            }
+            v1_emit4(p, row, ri, tx0, raw, inf);
+        }
     } else {
         const int32_t* pos = ws.pos + ws.at(row, 0);
+        uint32_t* stage = v1_stage(sm);
         auto emit = [&](const auto& at, const auto& q, const auto& key) {
 #pragma unroll
             for (int i = 0; i < (int)(sizeof(at) / sizeof(at[0])); ++i)
-                if (at[i] >= 0) v1_emit(p, row, ri, at[i], pos[q[i]], key[i] == kNegInfKey);
+                if (at[i] >= 0) stage[at[i]] = (uint32_t)q[i] | (key[i] == kNegInfKey ? kStagedNegInf : 0u);
         };
         if constexpr (kShortMerge)
             select_short(cand_source(ws, row), (uint32_t)T, sm, emit);
         else
             select_stream(cand_source(ws, row), (uint32_t)T, sm, emit);
+        // (the selection ends with a barrier: every slot holds a candidate index)
+        for (int32_t tx0 = 4 * threadIdx.x; tx0 < T; tx0 += 4 * kBlock) {
+            int32_t raw[4];
+            bool inf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t v = stage[min(tx0 + i, T - 1)];
+                raw[i] = pos[min(v & ~kStagedNegInf, (uint32_t)(ws.nseg * T - 1))];
+                inf[i] = (v & kStagedNegInf) != 0;
+            }
+            v1_emit4(p, row, ri, tx0, raw, inf);
+        }
     }
     v1_pad_expansion(p, row);
 }

@@ -147,6 +147,55 @@ def config1(seed=19, rows=1024):
              WIDTH=2688))
 
 
+def config9(seed=9, rows=1024, heads=64, buckets=64, bucket_tokens=1024, page_fraction=0.5, sink=64,
+            window=2048, route_pages=2048, pool_pages=4096):
+    """The reference's published whole-query shape (coarse score + route +
+    fine score + fused Top-K + x4 at 1024 queries and 64K context,
+    sglang/srt/layers/attention/v1_deepseek/README.txt:117) with synthetic FP8
+    N(0,1) keys and the runtime's default geometry (runtime.py:24-28, 75:
+    page_fraction 0.5, sink 64, window 2048): 1024 queries x 64 heads with
+    U(0,1) weights, 65536 keys in 64 built 1K buckets (members reversed per
+    bucket) plus one unbuilt token, coarse scores over the 8192 centers (8 per
+    built page), route of 512 of the 1024 built pages, 512 x 64 + 64 + 2048 =
+    34880 fine candidates (query i sees the first 34880 - 1023 + i), Top-2048,
+    native table = random pages of a 4096-page pool, 656-byte row gather."""
+    g = rng(seed)
+    B, PG = rows, route_pages
+    NB = buckets * bucket_tokens
+    N = NB + 1
+    built = NB // PAGE
+    TAKE = max(-(-built * int(page_fraction * 1000) // 1000), -(-TOPK // PAGE))
+    CAP = PG
+    nt_row = g.permutation(pool_pages)[:PG].astype(np.int32)
+    rt_row = g.permutation(CAP).astype(np.int32)
+    q8, _ = quantize_rows(g.standard_normal((B * heads, DIM), dtype=np.float32))
+    w = g.random((B, heads), dtype=np.float32)
+    k8, ks = quantize_rows(g.standard_normal((N, DIM), dtype=np.float32))
+    native = scatter_pages(pool_pages, pack_pages(k8, ks), nt_row)
+    logical_order = np.arange(NB, dtype=np.int32).reshape(buckets, bucket_tokens)[:, ::-1].reshape(built, PAGE).copy()
+    members = np.full((CAP, PAGE), -1, dtype=np.int32)
+    members[rt_row[:built]] = logical_order
+    fine = np.zeros((CAP + 68, PAGE_BYTES), dtype=np.uint8)
+    ro_k8, ro_ks = k8[logical_order.reshape(-1)], ks[logical_order.reshape(-1)]
+    fine[rt_row[:built]] = pack_pages(ro_k8, ro_ks)
+    dq = decode_table()[ro_k8] * ro_ks[:, None]
+    mean = dq.reshape(NB // 8, 8, DIM).sum(axis=1, dtype=np.float32) / np.float32(8.0)
+    del dq
+    c8, cs = quantize_rows(mean)
+    centers = pack_pages(c8, cs)
+    WIDTH = TAKE * PAGE + sink + window
+    fine_lens = np.minimum(WIDTH, WIDTH - (B - 1) + np.arange(B)).astype(np.int32)
+    lat_pool = g.integers(0, 256, size=(pool_pages * PAGE, MLA_ROW_BYTES), dtype=np.uint8)
+    return Workload("config9", seed, dict(
+        q8=q8.reshape(B, heads, DIM), w=w, native=native, fine=fine, members=members, centers=centers,
+        nt=np.broadcast_to(nt_row, (B, PG)).copy(), rt=np.broadcast_to(rt_row, (B, PG)).copy(),
+        center_table=np.arange(centers.shape[0], dtype=np.int32), lens=np.full(B, N, np.int32),
+        takes=np.full(B, TAKE, np.int32), tail_rows=np.zeros(B, np.int32), fine_lens=fine_lens,
+        latent=lat_pool),
+        dict(B=B, P=PG, CAP=CAP, TAKE=TAKE, N=N, WINDOW=window, SINK=sink, TOPK=TOPK, H=heads, FT_COLS=TAKE + 68,
+             WIDTH=WIDTH, CENTERS=NB // 8, BUILT=built))
+
+
 def splitmix64(x):
     """SplitMix64 finaliser (Steele, Lea, Flood 2014) of uint64 values."""
     z = np.asarray(x, dtype=np.uint64) + np.uint64(0x9E3779B97F4A7C15)

@@ -105,7 +105,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6, 7, 8])
+    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES bytes (HBM counter calibration) and exit")
@@ -250,6 +250,68 @@ def setup_example(P, dev, torch, np):
                         "2688 candidates, fused Top-2048 with mask, unfused C4 x4 expansion, 656-byte row gather",
             "global_batch": B, "seq_len": WIDTH, "parallelism": "single GPU"}
     return B, stages, work_units, cpu, meta, "synthetic (PCG64 seed 19)"
+
+
+def setup_whole(P, dev, torch, np):
+    """Configuration 9: the reference's published whole-query shape (coarse
+    score + route + fine score + fused Top-K + x4 at 1024 queries and 64K
+    context, sglang/srt/layers/attention/v1_deepseek/README.txt:117) on
+    synthetic data with the runtime's default geometry; no gather."""
+    wl = P.workloads.config9()
+    a, prm = wl.arrays, wl.params
+    B, PG, CAP, TAKE, WIDTH, T = prm["B"], prm["P"], prm["CAP"], prm["TAKE"], prm["WIDTH"], prm["TOPK"]
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in a.items() if k != "latent"}
+    q = d["q8"].view(torch.float8_e4m3fn)
+    center_lens = torch.full((B,), prm["CENTERS"], device=dev, dtype=torch.int32)
+    ctab = d["center_table"][None].expand(B, -1)
+    coarse = torch.empty((B, PG * 8), device=dev)
+    sel = torch.empty((B, TAKE), device=dev, dtype=torch.int32)
+    ft = torch.empty((B, prm["FT_COLS"]), device=dev, dtype=torch.int32)
+    logits = torch.empty((B, WIDTH), device=dev)
+    physical = torch.empty((B, T), device=dev, dtype=torch.int32)
+    logical = torch.empty_like(physical)
+    raw = torch.empty_like(physical)
+    no_exp = torch.empty_strided((B, 0), (0, 1), device=dev, dtype=torch.int32)
+    expanded = torch.empty((B, 4 * T + 64), device=dev, dtype=torch.int32)
+    fused = P.query_fused.module()
+    stages = [
+        ("coarse", lambda: P.scoring.fp8_paged_mqa_logits(q, d["centers"], d["w"], center_lens, ctab, None, PG * 8,
+                                                           clean_logits=True, out=coarse)),
+        ("route", lambda: fused.route(coarse, d["lens"], d["takes"], sel, PG, d["rt"], ft, d["tail_rows"], CAP, True)),
+        ("stage", lambda: P.kernels.stage_tail_shared[(-(-B // 32), 68)](
+            d["native"], None, d["nt"], d["lens"], d["fine"], None, d["tail_rows"], CAP, PG, 68, prm["SINK"],
+            prm["WINDOW"], ROWS=B, GROUP=32)),
+        ("score", lambda: P.scoring.fp8_paged_mqa_logits(q, d["fine"], d["w"], d["fine_lens"], ft, None, WIDTH,
+                                                          clean_logits=True, out=logits)),
+        ("topk", lambda: fused.topk(logits, d["fine_lens"], d["members"], d["rt"], d["nt"], sel, d["lens"],
+                                    d["takes"], physical, logical, raw, prm["WINDOW"], True, no_exp, True, True, ft,
+                                    False)),
+        ("expand", lambda: P.kernels.expand_logical[(B,)](logical, expanded, T, expanded.shape[1],
+                                                          1 << (expanded.shape[1] - 1).bit_length())),
+    ]
+    fl = a["fine_lens"].astype(np.int64)
+    H = prm["H"]
+    tail_bytes = 2.0 * (prm["SINK"] + prm["WINDOW"]) / 64 * 8448
+    work_units = {
+        "coarse": (_score_flops(H, np.full(B, prm["CENTERS"])) / 1e12, "TFLOP/s", PEAK_FP8_TFLOPS, "mfma"),
+        "route": ((32.0 * prm["BUILT"] * B + 4.0 * B * (TAKE + prm["FT_COLS"])) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "stage": (tail_bytes / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "score": (_score_flops(H, fl) / 1e12, "TFLOP/s", PEAK_FP8_TFLOPS, "mfma"),
+        "topk": ((4.0 * fl.sum() + 12.0 * B * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        "expand": ((4.0 * B * T + 4.0 * expanded.numel()) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+    }
+
+    def cpu(budget):
+        from oracle import cpu_baseline
+        qps, n, threads = cpu_baseline.whole_query_queries_per_second(a, prm, budget)
+        return qps, threads, f"{n} of {B} queries (64-head coarse and fine scores, route, Top-2048, x4 positions)"
+
+    meta = {"workload": "whole V1 query at the reference's published shape: 1024 queries x 64 heads FP8, 64K-token "
+                        "context in 64 built 1K buckets, coarse score over 8192 centers, route 512 of 1024 pages "
+                        "(page_fraction 0.5), sink 64 + window 2048, 34880 fine candidates, fused Top-2048 with "
+                        "mask, x4 expansion (no gather)",
+            "global_batch": B, "seq_len": WIDTH, "parallelism": "single GPU"}
+    return B, stages, work_units, cpu, meta, "synthetic (PCG64 seed 9)"
 
 
 def setup_gather(P, dev, torch, np):
@@ -657,9 +719,10 @@ def setup_consumer(P, dev, torch, np):
 
 
 SETUPS = {1: setup_example, 2: setup_pages, 3: setup_gather, 4: setup_prefill, 5: setup_decode, 6: setup_build,
-          7: setup_union, 8: setup_consumer}
+          7: setup_union, 8: setup_consumer, 9: setup_whole}
 RATE_UNITS = {2: "requests/s", 6: "tokens/s"}
-METRICS = {6: "index-build tokens/sec (initialize+bisection+assemble) and % of HBM roofline"}
+METRICS = {6: "index-build tokens/sec (initialize+bisection+assemble) and % of HBM roofline",
+           9: "whole V1 queries/sec (coarse+route+fine score+Top2048+x4) and % of FP8-MFMA/HBM roofline"}
 
 
 def main():

@@ -58,6 +58,46 @@ def _dequant_pages(native, pages):
     return k, torch.from_numpy(np.ascontiguousarray(ks))
 
 
+def whole_query_queries_per_second(a, prm, budget_s=10.0, min_rows=2):
+    """The example's torch path per query at many heads
+    (sglang/srt/layers/attention/v1_deepseek/example_v1_query_single_head.py:38-70
+    with the score sum_h w_h relu(q_h . k) of sra/v1_deepseek/kernels.py:310-313):
+    coarse scores over the centers, page max, top-`TAKE` pages, candidate keys
+    (their members, sink, tail), masked fine scores, Top-2048, logical
+    positions and their x4 expansion."""
+    threads = torch.get_num_threads()
+    B, take, n, window, sink_cap = prm["B"], prm["TAKE"], prm["N"], prm["WINDOW"], prm["SINK"]
+    built = prm["BUILT"]
+    centers, cs = _dequant_pages(a["centers"], np.arange(a["centers"].shape[0]))
+    centers = (centers * cs[:, None])[: prm["CENTERS"]]
+    nt = a["nt"][0]
+    keys, ks = _dequant_pages(a["native"], nt[: -(-n // 64)])
+    keys = keys * ks[:, None]
+    members = torch.from_numpy(a["members"].astype(np.int64))
+    rt = torch.from_numpy(a["rt"][0].astype(np.int64))
+    sink = min(n, sink_cap)
+    tail = max(sink, min((n - 1) // 1024 * 1024, max(sink, n - window)))
+    fixed = torch.cat((torch.arange(sink), torch.arange(tail, n)))
+    qs = torch.from_numpy(a["q8"]).view(torch.float8_e4m3fn)
+    w = torch.from_numpy(a["w"])
+    done, t0 = 0, time.perf_counter()
+    while done < B and (done < min_rows or time.perf_counter() - t0 < budget_s):
+        q = qs[done].float()
+        coarse = (torch.relu(centers @ q.T) * w[done]).sum(1)
+        pages = coarse.view(built, 8).amax(1).topk(take).indices
+        chosen = members[rt[pages]].reshape(-1)
+        cand = torch.cat((chosen, fixed))
+        valid = torch.ones(cand.shape[0], dtype=torch.bool)
+        valid[: take * 64] = (chosen >= sink) & (chosen < tail)
+        valid &= torch.arange(cand.shape[0]) < int(a["fine_lens"][done])
+        scores = (torch.relu(keys[cand.clamp(0, n - 1)] @ q.T) * w[done]).sum(1).masked_fill(~valid, float("-inf"))
+        lg = cand[scores.topk(min(2048, scores.shape[0])).indices]
+        expanded = (lg[:, None] * 4 + torch.arange(4)).reshape(-1)
+        assert expanded.shape[0] == 4 * lg.shape[0]
+        done += 1
+    return done / (time.perf_counter() - t0), done, threads
+
+
 def example_queries_per_second(a, prm, budget_s=10.0, min_rows=8):
     """The reference example's torch path per query
     (sglang/srt/layers/attention/v1_deepseek/example_v1_query_single_head.py:38-70):

@@ -105,6 +105,79 @@ def test_config1_query_chain(dev):
     assert np.array_equal(H(out), O.gather_rows(a["latent"], exp["physical"]))
 
 
+def test_config9_whole_query(dev):
+    """The reference's published whole-query shape (1024 queries x 64 heads,
+    64K context, route of 512 of 1024 pages, 34880 candidates): coarse score
+    -> route (+ fine table) -> shared tail staging -> fine score -> fused
+    Top-2048 with mask (rows above 32768 columns: segments and merge) -> x4
+    expansion, as bench.py runs it.  Route, table, staging and expansion are
+    compared on every row, the scores and the Top-K on sampled rows (the
+    Top-K oracle on the GPU's logits)."""
+    wl = W.config9()
+    a, prm = wl.arrays, wl.params
+    B, P, CAP, TAKE, WIDTH, TOP = prm["B"], prm["P"], prm["CAP"], prm["TAKE"], prm["WIDTH"], prm["TOPK"]
+    rows = _sample_rows(B, np.random.default_rng(9))
+    q = T(a["q8"], dev).view(torch.float8_e4m3fn)
+    w = T(a["w"], dev)
+    center_lens = np.full(B, prm["CENTERS"], np.int32)
+    ctab = np.broadcast_to(a["center_table"], (B, a["center_table"].shape[0]))
+    coarse = SC.fp8_paged_mqa_logits(q, T(a["centers"], dev), w, T(center_lens, dev),
+                                     T(a["center_table"], dev)[None].expand(B, -1), None, P * 8, clean_logits=True)
+    coarse_h = H(coarse)
+    args = (a["q8"][rows], a["w"][rows], a["centers"], ctab[rows], center_lens[rows], P * 8)
+    assert_scores_close(coarse_h[rows].astype(np.float64), O.paged_logits(*args), O.paged_logits(*args, magnitude=True))
+
+    sel = torch.empty((B, TAKE), device=dev, dtype=torch.int32)
+    ft = torch.empty((B, prm["FT_COLS"]), device=dev, dtype=torch.int32)
+    QF.module().route(coarse, T(a["lens"], dev), T(a["takes"], dev), sel, P, T(a["rt"], dev), ft,
+                      T(a["tail_rows"], dev), CAP, True)
+    e_sel = np.full((B, TAKE), -1, np.int32)
+    e_ft = np.full((B, prm["FT_COLS"]), -1, np.int32)
+    O.route(coarse_h, a["lens"], a["takes"], e_sel, P, a["rt"], e_ft, a["tail_rows"], CAP, True)
+    sel_h, ft_h = H(sel), H(ft)
+    assert np.array_equal(sel_h, e_sel) and np.array_equal(ft_h, e_ft)
+
+    fine = a["fine"].copy()
+    fine_d = T(fine, dev)
+    K.stage_tail_shared[(-(-B // 32), 68)](T(a["native"], dev), None, T(a["nt"], dev), T(a["lens"], dev), fine_d, None,
+                                           T(a["tail_rows"], dev), CAP, P, 68, prm["SINK"], prm["WINDOW"], ROWS=B,
+                                           GROUP=32)
+    O.stage_tail(a["native"], a["nt"], a["lens"], fine, CAP, 68, prm["SINK"], prm["WINDOW"], tail_rows=a["tail_rows"],
+                 rows=B)
+    fine_h = H(fine_d)
+    assert np.array_equal(fine_h, fine)
+
+    fl = a["fine_lens"]
+    logits = SC.fp8_paged_mqa_logits(q, fine_d, w, T(fl, dev), ft, None, WIDTH, clean_logits=True)
+    logits_h = H(logits)
+    args = (a["q8"][rows], a["w"][rows], fine_h, ft_h[rows], fl[rows], WIDTH)
+    assert_scores_close(logits_h[rows].astype(np.float64), O.paged_logits(*args), O.paged_logits(*args, magnitude=True))
+
+    physical = torch.empty((B, TOP), device=dev, dtype=torch.int32)
+    logical = torch.empty_like(physical)
+    raw = torch.empty_like(physical)
+    no_exp = torch.empty_strided((B, 0), (0, 1), device=dev, dtype=torch.int32)
+    QF.module().topk(logits, T(fl, dev), T(a["members"], dev), T(a["rt"], dev), T(a["nt"], dev), sel,
+                     T(a["lens"], dev), T(a["takes"], dev), physical, logical, raw, prm["WINDOW"], True, no_exp,
+                     True, True, ft, False)
+    expanded = torch.full((B, 4 * TOP + 64), 5, device=dev, dtype=torch.int32)
+    K.expand_logical[(B,)](logical, expanded, TOP, expanded.shape[1], 1 << (expanded.shape[1] - 1).bit_length())
+    masked = logits_h[rows].copy()
+    exp = O.fused_topk(masked, fl[rows], a["members"], a["rt"][rows], a["nt"][rows], sel_h[rows], a["lens"][rows],
+                       a["takes"][rows], TOP, prm["WINDOW"], True, 0, True, True, ft_h[rows], False)
+    assert np.array_equal(H(logits)[rows], masked)
+    for name, got in (("raw", raw), ("logical", logical), ("physical", physical)):
+        assert np.array_equal(H(got)[rows], exp[name]), name
+    logical_h = H(logical)
+    e_exp = np.full((B, 4 * TOP + 64), 5, np.int32)
+    O.expand_logical(logical_h, e_exp, 1 << (e_exp.shape[1] - 1).bit_length())
+    assert np.array_equal(H(expanded), e_exp)
+    # every row: 2048 distinct candidates inside its fine width
+    r = H(raw)
+    assert ((r >= 0) & (r < fl[:, None])).all()
+    assert all(len(np.unique(x)) == TOP for x in r)
+
+
 def test_config3_gather_full(dev):
     """1024 x 2048 ids (5% -1) through per-row 512-page windows of a 1M-row
     pool of 656-byte rows, every output byte compared."""
