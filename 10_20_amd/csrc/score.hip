@@ -67,6 +67,7 @@ struct ScoreParams {
     int32_t items;          // shared-table kernel: groups x levels
     uint32_t* work;         // shared-table kernel: next work item (zeroed by score_prep)
     int32_t bulk;           // shared-table kernel: levels of full-size ranges (chunks [L*F, (L+1)*F))
+    int32_t full;           // shared-table kernel: F, the chunks of a full-size range
     int32_t lvl_start[16];  // shared-table kernel: chunk range of each later level's items
     int32_t lvl_chunks[16];
     uint32_t* exact_pages;  // shared-table ReLU path: per row, a bitmap of pages for score_exact
@@ -362,9 +363,8 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     if (item >= p.items) break;
     const int32_t group = item % p.groups, level = item / p.groups;
     const int64_t row0 = (int64_t)group * kQueriesPerGroup;
-    constexpr int32_t kFull = kMaxRangePages / kChunkPages;
-    const int32_t c_begin = level < p.bulk ? level * kFull : p.lvl_start[level - p.bulk];
-    const int32_t nchunk = level < p.bulk ? kFull : p.lvl_chunks[level - p.bulk];
+    const int32_t c_begin = level < p.bulk ? level * p.full : p.lvl_start[level - p.bulk];
+    const int32_t nchunk = level < p.bulk ? p.full : p.lvl_chunks[level - p.bulk];
     const int32_t page_begin = c_begin * kChunkPages;
     const int32_t grows = (int32_t)min<int64_t>(kQueriesPerGroup, (int64_t)p.rows - row0);  // rows of the group
 
@@ -1006,15 +1006,21 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         // Work items: each row group's chunks cut into ranges that halve in
         // size (at most kMaxRangePages pages), all groups' largest ranges
         // first; work-groups pull them in that order, so the last ones taken
-        // are short and the work-groups end together.
+        // are short and the work-groups end together.  With few row groups
+        // the full range shrinks so that the chunks make at least two items
+        // per work-group: 1024 queries over 128 center pages (16 chunks of
+        // max_context_len, 8 of them real) otherwise put each group's work in
+        // one 128-page item on 128 of the 512 work-groups.
         const int64_t groups = cdiv(a->rows, kQueriesPerGroup);
         const int64_t wgs = 2 * (int64_t)v1::device_cus();
-        constexpr int64_t kFull = kMaxRangePages / kChunkPages;
-        p.bulk = (int32_t)((int64_t)chunks > 2 * kFull ? ((int64_t)chunks - kFull) / kFull : 0);
+        const int64_t full = std::max<int64_t>(
+            1, std::min<int64_t>(kMaxRangePages / kChunkPages, groups * (int64_t)chunks / (2 * wgs)));
+        p.full = (int32_t)full;
+        p.bulk = (int32_t)((int64_t)chunks > 2 * full ? ((int64_t)chunks - full) / full : 0);
         int nlevels = 0;
-        for (int64_t c = (int64_t)p.bulk * kFull; c < (int64_t)chunks;) {
+        for (int64_t c = (int64_t)p.bulk * full; c < (int64_t)chunks;) {
             const int64_t left = (int64_t)chunks - c;
-            const int64_t size = std::min<int64_t>(left == 1 ? 1 : (left + 1) / 2, kFull);
+            const int64_t size = std::min<int64_t>(left == 1 ? 1 : (left + 1) / 2, full);
             p.lvl_start[nlevels] = (int32_t)c;
             p.lvl_chunks[nlevels] = (int32_t)size;
             ++nlevels;
