@@ -145,7 +145,12 @@ int launch_rows(const uint8_t* pool, const RowMap& rm, int64_t total, int64_t ro
         return V1_LAUNCHED("gather_strided");
     }
     const uint32_t magic = chunks == 1 ? 0u : small_div_magic((uint32_t)chunks);
-    if (pool_bytes > kCachedPoolBytes) {
+    // The copy is write-bound, and takes the cached shape, when the pool
+    // stays in the caches or when it writes every pool byte four or more
+    // times on average (1024 x 2048 rows drawn from 2688 candidates of a
+    // 172 MB pool: 214 us against 254 us with the streamed shape).
+    const bool cached = pool_bytes <= kCachedPoolBytes || total * row_bytes >= 4 * pool_bytes;
+    if (!cached) {
         const int shift = tile_shift_for(chunks, kThreadsStream * kUnrollStream);
         hipLaunchKernelGGL((gather_rows16<kThreadsStream, kUnrollStream>), dim3((uint32_t)cdiv(total, 1ll << shift)),
                            dim3(kThreadsStream), 0, st, pool, rm, total, chunks, magic, shift, out);
