@@ -11,8 +11,9 @@
 // specified order): every 128-wide fp32 sum keeps four partial sums over dims
 // d = r (mod 4), each in ascending d with one rounding per product and per
 // addition (no fused multiply-add), then (p0 + p1) + (p2 + p3).  Unit vectors
-// are u_d = c_d * f with f = s / max(sqrt(sum (c_d s)^2), 1e-12), c_d the FP8
-// key and s its scale.  Center means add the 8 members in order, times 1/8.
+// follow kernels.py:17-28: x_d = fl(c_d * s), m = max(sqrt(sum x_d^2), 1e-12),
+// u_d = fl(x_d / m), c_d the FP8 key and s its scale.  Center means add the 8
+// members in order, times 1/8.
 //
 // Two forms: per-kernel drop-ins with the reference's launch shapes, and one
 // fused kernel that builds a batch of buckets, one 1024-thread work-group per
@@ -55,8 +56,8 @@ struct Acc4 {
     __device__ __forceinline__ float total() const { return ((a0 + a1) + (a2 + a3)); }
 };
 
-// Unit factor f of a token: s / max(||x||, 1e-12), x_d = c_d * s.
-__device__ __forceinline__ float unit_factor(const uint32_t (&c)[kWords], float s) {
+// Divisor m of a token's unit vector: max(||x||, 1e-12), x_d = c_d * s.
+__device__ __forceinline__ float unit_norm(const uint32_t (&c)[kWords], float s) {
     Acc4 acc;
 #pragma unroll
     for (int w = 0; w < kWords; ++w) {
@@ -64,7 +65,19 @@ __device__ __forceinline__ float unit_factor(const uint32_t (&c)[kWords], float 
         const float x2 = (fp8_at<2>(c[w]) * s), x3 = (fp8_at<3>(c[w]) * s);
         acc.add((x0 * x0), (x1 * x1), (x2 * x2), (x3 * x3));
     }
-    return s / fmaxf(sqrtf(acc.total()), 1e-12f);
+    return fmaxf(sqrtf(acc.total()), 1e-12f);
+}
+
+// fl(x / m) from r = fl(1 / m): q0 = fl(x * r), then one correction with the
+// exact residual x - q0 * m (an FMA).  With a correctly rounded reciprocal the
+// corrected quotient is the correctly rounded one (Markstein's division
+// theorem; checked against the division on 3.9e8 x = fp8 * s, m >= |x| pairs,
+// significands of m all ones and near powers of two included).  x = -0 gives
+// +0 where the division gives -0: the dots cannot tell, every partial sum
+// starts at +0.
+__device__ __forceinline__ float unit_div(float x, float m, float r) {
+    const float q0 = x * r;
+    return __builtin_fmaf(__builtin_fmaf(-q0, m, x), r, q0);
 }
 
 __device__ __forceinline__ void load_key(const uint8_t* row, uint32_t (&c)[kWords]) {
@@ -102,12 +115,12 @@ __global__ __launch_bounds__(64) void initialize_kernel(const uint8_t* __restric
     uint32_t c[kWords];
     load_key(K + page * V1_PAGE_BYTES + slot * 128, c);
     const float s = KS[page * kPageWords + kScaleWord + slot];
-    const float f = unit_factor(c, s);
+    const float m = unit_norm(c, s);
     float4* dst = reinterpret_cast<float4*>(unit + (int64_t)i * 128);
 #pragma unroll
     for (int w = 0; w < kWords; ++w)
-        dst[w] = make_float4((fp8_at<0>(c[w]) * f), (fp8_at<1>(c[w]) * f),
-                             (fp8_at<2>(c[w]) * f), (fp8_at<3>(c[w]) * f));
+        dst[w] = make_float4((fp8_at<0>(c[w]) * s) / m, (fp8_at<1>(c[w]) * s) / m,
+                             (fp8_at<2>(c[w]) * s) / m, (fp8_at<3>(c[w]) * s) / m);
     perm[i] = i;
 }
 
@@ -203,11 +216,11 @@ constexpr int kLevels = 7;      // groups of 1024, 512, ..., 16
 constexpr int kSlots = 64;      // anchor and stage slots: four per wave
 constexpr int kAncStride = 33;  // float4 per anchor slot, one of padding
 
-// A token's FP8 key and unit factor, staged for the lanes that expand it.
+// A token's FP8 key, scale and unit divisor, staged for the lanes that expand it.
 struct Stage {
     uint32_t c[kWords];
-    float f;
-    uint32_t pad[3];
+    float s, m;
+    uint32_t pad[2];
 };
 
 struct BuildSmem {
@@ -219,7 +232,8 @@ struct BuildSmem {
         struct {
             uint2 c[kWords / 2][kTokens];    // keys by position, 8 bytes of every row per plane
             int32_t tok[kTokens];
-            float f[kTokens];
+            float s[kTokens];                // scales
+            float m[kTokens];                // unit divisors
         } x;                                 // live during a block-wide exchange and the final assembly
     } u1;
     union {
@@ -325,11 +339,13 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
 
     int32_t tok = p;
     uint32_t c[kWords];
-    float f;
+    float s, m, rm;  // the token's scale, unit divisor and its reciprocal
     {
         const int64_t page = page_of(tok);
         load_key(pool + page * V1_PAGE_BYTES + (tok % 64) * 128, c);
-        f = unit_factor(c, pool_f[page * kPageWords + kScaleWord + tok % 64]);
+        s = pool_f[page * kPageWords + kScaleWord + tok % 64];
+        m = unit_norm(c, s);
+        rm = 1.0f / m;
     }
 
     // slot of position q's group within q's wave (groups of `width` <= 64
@@ -342,7 +358,8 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
         uint4* dst = reinterpret_cast<uint4*>(st.c);
 #pragma unroll
         for (int i = 0; i < kWords / 4; ++i) dst[i] = make_uint4(c[4 * i], c[4 * i + 1], c[4 * i + 2], c[4 * i + 3]);
-        st.f = f;
+        st.s = s;
+        st.m = m;
     };
     // anchor slot `slot` <- unit vector of the staged token; the `width`
     // lanes sharing the slot expand one or two key words each
@@ -350,14 +367,15 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
         const int32_t j = p & (width - 1);
         const int32_t per = width >= 32 ? 1 : 32 / width;  // 1 or 2 (width >= 16)
         if (j * per < kWords) {
-            const float fa = st.f;
+            const float sa = st.s, ma = st.m;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 if (q < per) {
                     const int32_t w = j * per + q;
                     const uint32_t cw = st.c[w];
                     const float2 lo = fp8_pair<false>(cw), hi = fp8_pair<true>(cw);
-                    sm.u1.d.anc[slot][w] = make_float4((lo.x * fa), (lo.y * fa), (hi.x * fa), (hi.y * fa));
+                    sm.u1.d.anc[slot][w] =
+                        make_float4((lo.x * sa) / ma, (lo.y * sa) / ma, (hi.x * sa) / ma, (hi.y * sa) / ma);
                 }
             }
         }
@@ -373,7 +391,8 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
         for (int w = 0; w < kWords; ++w) {
             const float4 av = a[w];
             const float2 lo = fp8_pair<false>(c[w]), hi = fp8_pair<true>(c[w]);
-            acc.add(((lo.x * f) * av.x), ((lo.y * f) * av.y), ((hi.x * f) * av.z), ((hi.y * f) * av.w));
+            acc.add((unit_div(lo.x * s, m, rm) * av.x), (unit_div(lo.y * s, m, rm) * av.y),
+                    (unit_div(hi.x * s, m, rm) * av.z), (unit_div(hi.y * s, m, rm) * av.w));
         }
         return acc.total();
     };
@@ -439,7 +458,8 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
 #pragma unroll
             for (int w = 0; w < kWords / 2; ++w) sm.u1.x.c[w][p] = make_uint2(c[2 * w], c[2 * w + 1]);
             sm.u1.x.tok[p] = tok;
-            sm.u1.x.f[p] = f;
+            sm.u1.x.s[p] = s;
+            sm.u1.x.m[p] = m;
             __syncthreads();
 #pragma unroll
             for (int w = 0; w < kWords / 2; ++w) {
@@ -448,7 +468,9 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
                 c[2 * w + 1] = v.y;
             }
             tok = sm.u1.x.tok[from];
-            f = sm.u1.x.f[from];
+            s = sm.u1.x.s[from];
+            m = sm.u1.x.m[from];
+            rm = 1.0f / m;
             if (p < 2 * kSlots) (&sm.amin[0][0])[p] = ~0ull;
             if (level + 1 < kLevels && (p & (half - 1)) == 0)
                 stage_put(sm.u2.st0[half > kWave ? p / half : wslot(p, half)]);
@@ -458,7 +480,9 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
 #pragma unroll
             for (int w = 0; w < kWords; ++w) c[w] = (uint32_t)__shfl((int)c[w], src, kWave);
             tok = __shfl(tok, src, kWave);
-            f = __shfl(f, src, kWave);
+            s = __shfl(s, src, kWave);
+            m = __shfl(m, src, kWave);
+            rm = __shfl(rm, src, kWave);
             if (level + 1 < kLevels && (p & (half - 1)) == 0) stage_put(sm.u2.st0[wslot(p, half)]);
             wave_sync();
         }
@@ -466,7 +490,6 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
 
     // final order: perm, the assembled pages, member map and centers
     const int64_t page = page_of(tok);
-    const float s = pool_f[page * kPageWords + kScaleWord + tok % 64];
     perm_out[b * kTokens + p] = tok;
     map_out[b * kTokens + p] = starts[b] + tok;
     uint8_t* tp = tmp_out + (b * 16 + p / 64) * V1_PAGE_BYTES;
@@ -477,7 +500,7 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
     __syncthreads();  // every wave is past its last dot
 #pragma unroll
     for (int w = 0; w < kWords / 2; ++w) sm.u1.x.c[w][p] = make_uint2(c[2 * w], c[2 * w + 1]);
-    sm.u1.x.f[p] = s;
+    sm.u1.x.s[p] = s;
     wave_sync();  // a center's 8 members are rows of this wave
     // center p / 8: lane r of the 8 members computes dims 16r .. 16r+15
     const int32_t r = p & 7, m0 = p & ~7;
@@ -485,7 +508,7 @@ __global__ __launch_bounds__(kTokens) void build_buckets_kernel(const uint8_t* _
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint2 w01 = sm.u1.x.c[2 * r][m0 + j], w23 = sm.u1.x.c[2 * r + 1][m0 + j];
-        const float sj = sm.u1.x.f[m0 + j];
+        const float sj = sm.u1.x.s[m0 + j];
         const uint32_t words[4] = {w01.x, w01.y, w23.x, w23.y};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {

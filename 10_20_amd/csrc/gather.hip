@@ -134,6 +134,8 @@ __global__ __launch_bounds__(kThreads) void gather_strided(
     out[t * dim + d] = off >= 0 ? pool[off + d * elem_stride] : T(0);
 }
 
+// pool_bytes: the bytes of the pool the copy can read (0: an empty pool);
+// it picks the copy shape.
 int launch_rows(const uint8_t* pool, const RowMap& rm, int64_t total, int64_t row_bytes, int64_t pool_bytes,
                 uint8_t* out, hipStream_t st) {
     if (total == 0) return V1_OK;
@@ -214,7 +216,9 @@ extern "C" int v1_gather_slots(const void* k_pool, const void* v_pool, int64_t p
         if (fast) {
             rm.pool_stride_bytes = s0[w] * elem_bytes;
             rm.base_offset_bytes = (int64_t)head * s1[w] * elem_bytes;
-            rc = launch_rows(static_cast<const uint8_t*>(pools[w]), rm, total, row_bytes, pool_slots * s0[w] * elem_bytes,
+            // (the copy reads one head's row of each slot: pool_slots rows of
+            // row_bytes, whatever the slot stride)
+            rc = launch_rows(static_cast<const uint8_t*>(pools[w]), rm, total, row_bytes, pool_slots * row_bytes,
                              static_cast<uint8_t*>(outs[w]), st);
         } else {
             rm.pool_stride_bytes = s0[w];  // element units for the strided kernel

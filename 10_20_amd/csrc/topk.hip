@@ -57,7 +57,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 static_assert(kHist == 4 * kBlock && kWords % kBlock == 0 && kCandMax % kBlock == 0, "work split");
 static_assert(kSampleRuns * 32 == 4 * kBlock, "eight threads per sample run");
 
-struct SelSmem {  // (arrays at 16-byte offsets: read as 16-byte words)
+struct alignas(16) SelSmem {  // (arrays at 16-byte offsets: read as 16-byte words)
     uint32_t hist[kHist];      // radix histograms; bitmap word prefixes
     uint32_t cand_key[kCandMax];  // (after the ranks of a transform row: its selected positions in slot order)
     uint16_t cand_pos[kCandMax];
@@ -69,6 +69,7 @@ struct SelSmem {  // (arrays at 16-byte offsets: read as 16-byte words)
     int32_t maskpage[kSpan / 64];  // V1 mask: page per selected rank, -1 when unmasked; or a row's page table
 };
 static_assert(sizeof(SelSmem) <= 40 * 1024, "four work-groups per CU");
+static_assert(alignof(SelSmem) >= 16, "16-byte LDS words at any placement of the struct");
 static_assert(offsetof(SelSmem, gt_bits) % 16 == 0 && offsetof(SelSmem, eq_bits) % 16 == 0, "16-byte words");
 static_assert(offsetof(SelSmem, cand_key) % 8 == 0 && kCandMax * 4 >= 2 * 2048, "T <= 2048 staged positions");
 
@@ -274,7 +275,11 @@ struct Ranker {
 
 // Pivot from the sampled keys sk (threads 8r..8r+7 hold run r of 32 keys;
 // block statistics smax / smin / scnt) such that about target * T of the n
-// keys are expected at or above it.  Ends with a barrier.
+// keys are expected at or above it.  With a histogram (scnt > 0 and
+// smax != smin) it ends with find_bin's barrier; otherwise it passes no
+// barrier.  Either way it leaves sm.hist clear, and it writes no LDS word on
+// the no-histogram branch, so the caller may append candidates (sm.cand_*,
+// sm.ncand) at once but must pass a barrier before writing sm.red or sm.bc.
 __device__ uint32_t choose_pivot(const uint32_t (&sk)[4], uint32_t smax, uint32_t smin, uint32_t scnt, int32_t n,
                                  uint32_t T, float target, SelSmem& sm) {
     uint32_t pivot = kNegInfKey + 1;

@@ -32,7 +32,11 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
 
 Prints one JSON line: queries/sec, per-stage times, the roofline of the
 dominant kernel and the CPU baseline (the reference's torch expressions on
-the host cores, on a bounded sample of the same workload).
+the host cores, on a bounded sample of the same workload).  With the default
+config 4 the line also carries "configs": configs 1, 2, 3 and 5 measured the
+same way at their own shapes (--with selects others, "" none), each with its
+rate, step time, stage times, dominant-kernel roofline and a shorter CPU
+sample (--with-cpu-budget seconds).
 """
 import argparse
 import importlib
@@ -107,6 +111,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
+    ap.add_argument("--with", dest="with_configs", default=None, metavar="LIST",
+                    help="comma-separated further configs measured after the main one and reported under "
+                         "\"configs\" (default with config 4: 1,2,3,5; \"\" for none)")
+    ap.add_argument("--with-cpu-budget", type=float, default=3.0,
+                    help="seconds of CPU baseline work per further config")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES bytes (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -725,22 +734,10 @@ METRICS = {6: "index-build tokens/sec (initialize+bisection+assemble) and % of H
            9: "whole V1 queries/sec (coarse+route+fine score+Top2048+x4) and % of FP8-MFMA/HBM roofline"}
 
 
-def main():
-    args = parse()
-    if args.copy_calibration:
-        copy_calibration(args.copy_calibration)
-        return
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
-              file=sys.stderr)
-        sys.exit(2)
-    import numpy as np
-    import torch
-
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    P = Pkg()
-    rows, stages, work_units, cpu_fn, meta, data = SETUPS[args.config](P, dev, torch, np)
+def run(config, steps, warmup, cpu_budget, P, dev, torch, np):
+    """Sets up one workload, times `steps` steps after `warmup`, and returns
+    its JSON record (the bench line without the run-wide fields)."""
+    rows, stages, work_units, cpu_fn, meta, data = SETUPS[config](P, dev, torch, np)
     extra = meta.pop("_extra", [])
     names = [n for n, _ in stages]
     ev = {n: [] for n in names}
@@ -758,35 +755,35 @@ def main():
                 ev[name].append((prev, e))
                 prev = e
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step(False)
     torch.cuda.synchronize()
     # The timed steps record no events: an event between every pair of stages
     # added ~36 us to the 9-stage decode step (0.325 against 0.289 ms).  The
     # per-stage breakdown comes from as many steps again, with events.
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step(False)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    for _ in range(args.steps):
+    ms_step = (t1 - t0) * 1e3 / steps
+    for _ in range(steps):
         step(True)
     torch.cuda.synchronize()
-    stage_ms = {n: sum(x.elapsed_time(y) for x, y in ev[n]) / args.steps for n in names}
+    stage_ms = {n: sum(x.elapsed_time(y) for x, y in ev[n]) / steps for n in names}
 
     # alternatives timed beside the chain (not part of a step)
     alternatives = {}
     for name, fn, unit in extra:
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             fn()
         a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a0.record()
-        for _ in range(args.steps):
+        for _ in range(steps):
             fn()
         a1.record()
         a1.synchronize()
-        ms = a0.elapsed_time(a1) / args.steps
+        ms = a0.elapsed_time(a1) / steps
         amount = unit[0]() if callable(unit[0]) else unit[0]
         alternatives[name] = {"ms": round(ms, 4), "achieved": round(amount / (ms / 1e3), 1), "unit": unit[1],
                               "bound": unit[3], "frac": round(amount / (ms / 1e3) / unit[2], 4)}
@@ -802,28 +799,74 @@ def main():
     amount, unit, peak, bound = work_units[dom]
     achieved = amount / (stage_ms[dom] / 1e3)
 
-    rate_unit = RATE_UNITS.get(args.config, "queries/s")
+    rate_unit = RATE_UNITS.get(config, "queries/s")
     cpu = None
-    if args.cpu_budget > 0:
-        qps_cpu, threads, sample = cpu_fn(args.cpu_budget)
+    if cpu_budget > 0:
+        qps_cpu, threads, sample = cpu_fn(cpu_budget)
         cpu = {"value": round(qps_cpu, 3), "unit": rate_unit, "cores": threads, "kind": "port",
                "sample": f"{sample}, torch CPU, {os.cpu_count()} host cpus visible", "cpu": cpu_model()}
 
-    qps = rows * args.steps / (t1 - t0)
+    qps = rows * steps / (t1 - t0)
     line = {
-        "metric": METRICS.get(args.config, "indexed queries/sec (score+Top2048+gather) and % of FP8-MFMA/HBM roofline"),
-        "value": round(qps, 1), "unit": rate_unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp8-e4m3 score / fp32 accumulate / int32 indices / u8 rows", "data": data,
+        "metric": METRICS.get(config, "indexed queries/sec (score+Top2048+gather) and % of FP8-MFMA/HBM roofline"),
+        "value": round(qps, 1), "unit": rate_unit, "ms_per_step": round(ms_step, 4), "data": data,
         "config": meta,
         "stages": stage_info,
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4),
-                     "traffic": measured_traffic(args.config, dom)},
+                     "traffic": measured_traffic(config, dom)},
         "cpu_baseline": cpu,
     }
     if alternatives:
         line["alternatives"] = alternatives
+    return line
+
+
+def main():
+    args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+    import gc
+
+    import numpy as np
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    P = Pkg()
+    rec = run(args.config, args.steps, args.warmup, args.cpu_budget, P, dev, torch, np)
+    line = {"metric": rec.pop("metric"), "value": rec.pop("value"), "unit": rec.pop("unit"), "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": rec.pop("ms_per_step"),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp8-e4m3 score / fp32 accumulate / int32 indices / u8 rows", **rec}
+    more = args.with_configs
+    if more is None:
+        more = "1,2,3,5" if args.config == 4 else ""
+    configs = [int(c) for c in more.split(",") if c.strip()]
+    if configs:
+        # the other workloads of the metric, each at its own synthetic shape,
+        # measured after the headline one (secondary records: same timing,
+        # roofline of the dominant kernel, a shorter CPU sample)
+        line["configs"] = {}
+        for c in configs:
+            gc.collect()
+            torch.cuda.empty_cache()
+            r = run(c, args.steps, args.warmup, args.with_cpu_budget, P, dev, torch, np)
+            rl = r["roofline"]
+            line["configs"][str(c)] = {
+                "workload": r["config"]["workload"], "metric": r["metric"], "value": r["value"], "unit": r["unit"],
+                "ms_per_step": r["ms_per_step"], "data": r["data"],
+                "stages": {n: {"ms": v["ms"], "frac": v["frac"], "bound": v["bound"]} for n, v in r["stages"].items()},
+                "roofline": {k: rl[k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac", "traffic")},
+                "cpu_baseline": r["cpu_baseline"],
+            }
+            print(f"config {c}: {r['value']} {r['unit']}, {r['ms_per_step']} ms per step", file=sys.stderr,
+                  flush=True)
     print(json.dumps(line), flush=True)
 
 

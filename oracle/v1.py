@@ -151,6 +151,102 @@ def fused_topk(scores, fine_lens, members, rt, nt, selected, lens, takes, T, win
     return dict(physical=physical, logical=logical, raw=raw_out, expanded=expanded)
 
 
+# ------------------------------------------- the same selections, all rows
+# Every-row checks at the benchmark shapes (thousands of rows of 32K+ columns)
+# use these batch forms; tests pin them equal to the per-row functions above.
+def topk_select_rows(scores, lens, T, chunk=256):
+    """topk_select for every row at once: rows with L <= T take [0, L); others
+    the T largest of row[:L] by score_key, ties toward the lower index, in
+    ascending index order.  Each column gets the unique 64-bit composite
+    (key << 32) | (2^32 - 1 - index) (padding past L is 0, below every real
+    composite), and a row's T winners are the composites at or above its
+    T-th largest one (np.partition)."""
+    scores = np.asarray(scores, dtype=np.float32)
+    B, cols = scores.shape
+    lens = np.minimum(np.asarray(lens, dtype=np.int64), cols)
+    out = np.full((B, T), -1, dtype=np.int64)
+    col = np.arange(cols, dtype=np.uint64)
+    for b0 in range(0, B, chunk):
+        L = lens[b0:b0 + chunk]
+        big = np.nonzero(L > T)[0]
+        for k in np.nonzero(L <= T)[0]:
+            out[b0 + k, :max(int(L[k]), 0)] = np.arange(max(int(L[k]), 0))
+        if big.size == 0:
+            continue
+        comp = (score_key(scores[b0 + big]).astype(np.uint64) << np.uint64(32)) | (np.uint64(0xffffffff) - col)
+        comp[col[None, :] >= L[big, None].astype(np.uint64)] = 0
+        thr = np.partition(comp, cols - T, axis=1)[:, cols - T]
+        _, j = np.nonzero(comp >= thr[:, None])
+        out[b0 + big] = j.reshape(big.size, T)
+    return out
+
+
+def transform_topk_rows(scores, seq_lens, page_table, T, page_bits):
+    """transform_topk with the batch selection: returns (page_indices, raw)."""
+    raws = topk_select_rows(scores, np.minimum(np.asarray(seq_lens, np.int64), scores.shape[1]), T)
+    ok = raws >= 0
+    safe = np.where(ok, raws, 0)
+    entry = np.take_along_axis(np.asarray(page_table, np.int64), safe >> page_bits, axis=1)
+    out = np.where(ok, (entry << page_bits) | (safe & ((1 << page_bits) - 1)), -1)
+    return out.astype(np.int32), raws.astype(np.int32)
+
+
+def v1_mask_rows(scores, members, rt, selected, lens, takes, window, bucket_from_rank, chunk=128):
+    """fused_topk's in-place sink/tail mask (v1_query.cuh:71-107) for every
+    row at once: rank r < take of a row whose bucket overlaps the sink or the
+    tail gets -inf at the columns r * 64 + j whose member lies outside
+    [sink, tail)."""
+    B, cols = scores.shape
+    K = selected.shape[1]
+    r = np.arange(K)
+    colr = r[:, None] * 64 + np.arange(64)[None, :]
+    for b0 in range(0, B, chunk):
+        b1 = min(B, b0 + chunk)
+        n = np.asarray(lens[b0:b1], np.int64)
+        sink = np.minimum(n, 64)
+        tail = np.maximum(sink, np.minimum(np.maximum(n - 1, 0) // 1024 * 1024, np.maximum(sink, n - window)))
+        live = r[None, :] < np.asarray(takes[b0:b1], np.int64)[:, None]
+        rank = np.where(live, np.asarray(selected[b0:b1], np.int64), 0)
+        page = np.take_along_axis(np.asarray(rt[b0:b1], np.int64), rank, axis=1)
+        if bucket_from_rank:
+            bucket = tdiv(rank, 16) * 1024
+        else:
+            bucket = tdiv(members[page, 0], 1024) * 1024
+        cond = live & ((bucket < sink[:, None]) | (bucket + 1024 > tail[:, None]))
+        lg = members[page]
+        kill = cond[:, :, None] & ((lg < sink[:, None, None]) | (lg >= tail[:, None, None])) & (colr < cols)[None]
+        bi, ri, ji = np.nonzero(kill)
+        scores[b0 + bi, ri * 64 + ji] = NEG_INF
+
+
+def fused_topk_rows(scores, fine_lens, members, rt, nt, selected, lens, takes, T, window, mask, expansion_stride,
+                    physical_output, bucket_from_rank, fine_table, direct_fine):
+    """fused_topk with the batch mask and selection (same outputs, same
+    in-place mask)."""
+    B, cols = scores.shape
+    if mask:
+        v1_mask_rows(scores, members, rt, selected, lens, takes, window, bucket_from_rank)
+    L = np.minimum(np.asarray(fine_lens, np.int64), cols)
+    raws = topk_select_rows(scores, L, T)
+    physical = np.full((B, T), -1, dtype=np.int32)
+    logical = np.full((B, T), -1, dtype=np.int32)
+    raw_out = np.full((B, T), -1, dtype=np.int32)
+    expanded = np.full((B, expansion_stride), -1, dtype=np.int32) if expansion_stride else None
+    for b in range(B):
+        n, take = int(lens[b]), int(takes[b])
+        sink, tail = _bounds(n, window)
+        lg, ph = _map_row(raws[b], int(L[b]), scores[b], take, sink, tail, n, members, rt[b], nt[b], selected[b],
+                          fine_table[b] if direct_fine else None)
+        logical[b] = lg
+        if physical_output:
+            physical[b] = ph
+            raw_out[b] = raws[b]
+        if expansion_stride:
+            ex = np.where(lg[:, None] < 0, -1, 4 * lg[:, None].astype(np.int64) + np.arange(4))
+            expanded[b, :4 * T] = ex.reshape(-1)
+    return dict(physical=physical, logical=logical, raw=raw_out, expanded=expanded)
+
+
 def transform_topk(scores, seq_lens, page_table, T, page_bits):
     """topk_impl.cuh:156-190 transform after selection: returns (page_indices, raw)."""
     B, cols = scores.shape
@@ -668,15 +764,15 @@ def bucket_tokens(native, table):
 
 
 def unit_vectors(codes, scales):
-    """kernels.py:9-30 (x = fp8 * scale, x / max(||x||, 1e-12)), in this
-    build's rounding: x_d = fl(c_d * s), ||x|| = sqrt(reduce128(x * x)),
-    f = fl(s / max(||x||, 1e-12)), unit_d = fl(c_d * f)."""
+    """kernels.py:17-28: x_d = fl(c_d * s), unit_d = fl(x_d / max(||x||, 1e-12)),
+    the reference's order of operations; ||x|| = sqrt(reduce128(x * x)) (the
+    one order the reference leaves open: tl.sum's)."""
     c = e4m3_decode(codes)
     s = np.asarray(scales, dtype=np.float32)
     x = (c * s[:, None]).astype(np.float32)
     norm = np.sqrt(reduce128((x * x).astype(np.float32))).astype(np.float32)
-    f = (s / np.maximum(norm, np.float32(1e-12))).astype(np.float32)
-    return (c * f[:, None]).astype(np.float32)
+    m = np.maximum(norm, np.float32(1e-12))
+    return (x / m[:, None]).astype(np.float32)
 
 
 def build_initialize(native, table):

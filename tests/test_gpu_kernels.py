@@ -690,6 +690,27 @@ def assert_scores_close(got, ref, bound):
                              f"ref={ref[fin][i]!r} magnitude={bound[fin][i]!r}")
 
 
+def assert_scores_rel(got, ref):
+    """The north star's bound where every head weight is >= 0 (so every
+    reference score is >= 0): each finite score within 1e-2 relative of the
+    fp64 reference, exactly +0.0 (bit for bit) where the reference is 0, and
+    the same -inf pattern."""
+    fin = np.isfinite(ref)
+    assert np.array_equal(fin, np.isfinite(got)) and (got[~fin] == ref[~fin]).all()
+    g, r = got[fin], ref[fin]
+    assert (r >= 0).all(), "negative reference score: weights below 0"
+    zero = r == 0
+    bad_zero = zero & ((g != 0) | np.signbit(g))
+    if bad_zero.any():
+        raise AssertionError(f"{int(bad_zero.sum())} scores not +0.0 where the reference is 0")
+    rel = np.abs(g[~zero] - r[~zero]) / r[~zero]
+    if rel.size and rel.max() > 1e-2:
+        i = int(np.argmax(rel))
+        raise AssertionError(f"{int((rel > 1e-2).sum())} scores beyond 1e-2 relative; worst got={g[~zero][i]!r} "
+                             f"ref={r[~zero][i]!r} rel={rel[i]:.3e}")
+    return float(rel.max()) if rel.size else 0.0
+
+
 def _adversarial_rows(kind, g, cols):
     if kind == "plateau":  # one value everywhere but a few larger ones: candidate count >> cap
         r = np.full(cols, 3.0, np.float32)

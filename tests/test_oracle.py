@@ -61,6 +61,27 @@ def test_topk_select_brute_force_with_ties(seed):
     assert list(O.topk_select(row, L, T)) == _brute(row, L, T)
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_topk_select_rows_equals_per_row(seed):
+    """The batch selection (every row at once) against the per-row one and the
+    brute force: ties, +-0, +-inf, NaN-free rows of every length class."""
+    g = np.random.default_rng(100 + seed)
+    B, cols, T = 40, 700, int(g.integers(1, 300))
+    vals = np.float32([0.0, -0.0, 1.0, -1.0, 2.5, -np.inf, np.inf, 7.0])
+    scores = g.choice(vals, size=(B, cols))
+    scores = np.where(g.random((B, cols)) < 0.5, g.standard_normal((B, cols)), scores).astype(np.float32)
+    lens = g.integers(0, cols + 50, size=B)
+    lens[:3] = [0, T, T + 1]
+    got = O.topk_select_rows(scores, lens, T, chunk=7)
+    for b in range(B):
+        L = min(int(lens[b]), cols)
+        assert got[b].tolist() == O.topk_select(scores[b], L, T).tolist() == _brute(scores[b], L, T)
+    table = g.integers(0, 1000, size=(B, cols // 4 + 1)).astype(np.int32)
+    a = O.transform_topk_rows(scores, lens, table, T, 2)
+    e = O.transform_topk(scores, lens, table, T, 2)
+    assert np.array_equal(a[0], e[0]) and np.array_equal(a[1], e[1])
+
+
 def test_topk_select_short_row_takes_all_even_neg_inf():
     row = np.float32([-np.inf, 3, -np.inf])
     assert list(O.topk_select(row, 3, 5)) == [0, 1, 2, -1, -1]
@@ -394,6 +415,28 @@ def test_unfused_mask_and_map_equal_fused(example_after_route):
                             args(d["lens"].numpy()), args(d["takes"].numpy()), w2.shape[1], RX.TOP, 64, RX.WINDOW,
                             True, False, args(ft))
     assert np.array_equal(phys, out["physical"]) and np.array_equal(lg, out["logical"])
+
+
+@pytest.mark.parametrize("bucket_from_rank,direct", [(True, False), (False, True), (False, False)])
+def test_fused_topk_rows_equals_per_row(example_after_route, bucket_from_rank, direct):
+    """The batch mask + selection + map against fused_topk, on the reference
+    example rows (masked sink/tail buckets, short and long rows)."""
+    d, sel, ft, f = example_after_route
+    rows = 96
+    args = lambda a: a[:rows]
+    w1 = f["fine_scores"].numpy()[:rows].copy()
+    w1[5, 100:400] = w1[5, 99]  # a long run of ties across the selection boundary
+    w2 = w1.copy()
+    fl = f["fine_lens"].numpy()[:rows].copy()
+    fl[7] = 1000  # a row of fewer candidates than T
+    common = (d["members"].numpy(), args(d["rt"].numpy()), args(d["nt"].numpy()), args(sel),
+              args(d["lens"].numpy()), args(d["takes"].numpy()), RX.TOP, RX.WINDOW, True, 4 * RX.TOP + 64, True,
+              bucket_from_rank, args(ft), direct)
+    a = O.fused_topk(w1, fl, *common)
+    b = O.fused_topk_rows(w2, fl, *common)
+    assert np.array_equal(w1, w2)
+    for k in ("physical", "logical", "raw", "expanded"):
+        assert np.array_equal(a[k], b[k]), k
 
 
 def test_transform_closed_form():

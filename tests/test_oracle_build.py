@@ -108,6 +108,32 @@ def test_unit_vectors_kat_and_norm():
     np.testing.assert_allclose(unit, x / np.linalg.norm(x, axis=1, keepdims=True), rtol=0, atol=3e-7)
 
 
+def test_unit_vectors_divide_after_the_product():
+    """kernels.py:17-28 forms x = k * scale first and divides x by the norm:
+    every unit component must be the correctly rounded quotient of fl(c * s)
+    by m = max(||x||, 1e-12), checked in exact rational arithmetic (within half
+    an ulp, no exact ties).  Scaling c by a rounded fl(s / m) instead rounds
+    differently on some components of these tokens, which this test sees."""
+    from fractions import Fraction
+    native, table = _bucket(7)
+    codes, scales = O.bucket_tokens(native, table)
+    codes, scales = codes[:48], scales[:48] * np.float32(1.2345678)  # significands beyond a power of two
+    unit = O.unit_vectors(codes, scales)
+    c = O.e4m3_decode(codes)
+    x = (c * scales[:, None]).astype(np.float32)
+    m = np.maximum(np.sqrt(O.reduce128((x * x).astype(np.float32))), np.float32(1e-12)).astype(np.float32)
+    other = (c * (scales / m).astype(np.float32)[:, None]).astype(np.float32)
+    assert (other != unit).any(), "the two orders agree on every component: the test cannot tell them apart"
+    for t in range(len(codes)):
+        mt = Fraction(float(m[t]))
+        for d in range(128):
+            q = Fraction(float(x[t, d])) / mt
+            u = float(unit[t, d])
+            ulp = Fraction(float(np.spacing(np.float32(abs(u)) if u != 0 else np.float32(0))))
+            err = abs(Fraction(u) - q)
+            assert err * 2 < ulp or (q == 0 and u == 0), (t, d, u, float(q))
+
+
 def test_e4m3_encode_matches_torch():
     g = np.random.default_rng(0)
     x = np.concatenate([g.standard_normal(20000) * 50, g.uniform(-448, 448, 20000),

@@ -13,7 +13,7 @@ import torch
 
 from conftest import pkg
 from oracle import v1 as O
-from test_gpu_kernels import H, T, assert_scores_close
+from test_gpu_kernels import H, T, assert_scores_close, assert_scores_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -49,6 +49,11 @@ def test_config1_query_chain(dev):
     ref = O.paged_logits(a["q8"], a["w"], a["centers"], ctab, center_lens, P * 8)
     bound = O.paged_logits(a["q8"], a["w"], a["centers"], ctab, center_lens, P * 8, magnitude=True)
     coarse_h = H(coarse)
+    # One head: a dot at or just below 0 can come out of the fp32 MFMA
+    # accumulation slightly positive (its FP8 products span more than the 24
+    # bits of an fp32 sum), and ReLU keeps it, so scores near 0 get the
+    # accumulation allowance; the 64-head workloads below use the plain
+    # relative bound with exact zeros.
     assert_scores_close(coarse_h.astype(np.float64), ref, bound)
 
     # route with the fine-table fill
@@ -125,7 +130,7 @@ def test_config9_whole_query(dev):
                                      T(a["center_table"], dev)[None].expand(B, -1), None, P * 8, clean_logits=True)
     coarse_h = H(coarse)
     args = (a["q8"][rows], a["w"][rows], a["centers"], ctab[rows], center_lens[rows], P * 8)
-    assert_scores_close(coarse_h[rows].astype(np.float64), O.paged_logits(*args), O.paged_logits(*args, magnitude=True))
+    assert_scores_rel(coarse_h[rows].astype(np.float64), O.paged_logits(*args))
 
     sel = torch.empty((B, TAKE), device=dev, dtype=torch.int32)
     ft = torch.empty((B, prm["FT_COLS"]), device=dev, dtype=torch.int32)
@@ -151,7 +156,7 @@ def test_config9_whole_query(dev):
     logits = SC.fp8_paged_mqa_logits(q, fine_d, w, T(fl, dev), ft, None, WIDTH, clean_logits=True)
     logits_h = H(logits)
     args = (a["q8"][rows], a["w"][rows], fine_h, ft_h[rows], fl[rows], WIDTH)
-    assert_scores_close(logits_h[rows].astype(np.float64), O.paged_logits(*args), O.paged_logits(*args, magnitude=True))
+    worst = assert_scores_rel(logits_h[rows].astype(np.float64), O.paged_logits(*args))
 
     physical = torch.empty((B, TOP), device=dev, dtype=torch.int32)
     logical = torch.empty_like(physical)
@@ -162,20 +167,19 @@ def test_config9_whole_query(dev):
                      True, True, ft, False)
     expanded = torch.full((B, 4 * TOP + 64), 5, device=dev, dtype=torch.int32)
     K.expand_logical[(B,)](logical, expanded, TOP, expanded.shape[1], 1 << (expanded.shape[1] - 1).bit_length())
-    masked = logits_h[rows].copy()
-    exp = O.fused_topk(masked, fl[rows], a["members"], a["rt"][rows], a["nt"][rows], sel_h[rows], a["lens"][rows],
-                       a["takes"][rows], TOP, prm["WINDOW"], True, 0, True, True, ft_h[rows], False)
-    assert np.array_equal(H(logits)[rows], masked)
+    # every row: the in-place mask, the Top-K and its raw -> logical ->
+    # physical map against the oracle on the GPU's logits
+    masked = logits_h.copy()
+    exp = O.fused_topk_rows(masked, fl, a["members"], a["rt"], a["nt"], sel_h, a["lens"], a["takes"], TOP,
+                            prm["WINDOW"], True, 0, True, True, ft_h, False)
+    assert np.array_equal(H(logits), masked)
     for name, got in (("raw", raw), ("logical", logical), ("physical", physical)):
-        assert np.array_equal(H(got)[rows], exp[name]), name
+        assert np.array_equal(H(got), exp[name]), name
     logical_h = H(logical)
     e_exp = np.full((B, 4 * TOP + 64), 5, np.int32)
     O.expand_logical(logical_h, e_exp, 1 << (e_exp.shape[1] - 1).bit_length())
     assert np.array_equal(H(expanded), e_exp)
-    # every row: 2048 distinct candidates inside its fine width
-    r = H(raw)
-    assert ((r >= 0) & (r < fl[:, None])).all()
-    assert all(len(np.unique(x)) == TOP for x in r)
+    print(f"config 9: {B} rows mask/Top-K/map equal; fine scores of {len(rows)} rows within {worst:.2e} relative")
 
 
 def test_config3_gather_full(dev):
@@ -191,9 +195,10 @@ def test_config3_gather_full(dev):
 
 def test_config4_prefill_chunk(dev):
     """4096 queries x 64 heads over a 32768-token causal context: score, Top-2048
-    slot map and gather for every row on the GPU; sampled rows against the oracle,
-    and for every row: slots inside the query's context, strictly ascending
-    candidate order, no duplicates."""
+    slot map and gather for every row on the GPU.  The Top-K indices and slots
+    of every row equal the oracle's Top-K on the GPU's logits; scores of sampled
+    rows are within 1e-2 relative of the fp64 reference (exact zeros bit for
+    bit); gathered bytes of 64 rows are compared byte for byte."""
     wl = W.config4()
     a, prm = wl.arrays, wl.params
     rows, ctx, TOP = prm["rows"], prm["ctx"], prm["topk"]
@@ -211,16 +216,17 @@ def test_config4_prefill_chunk(dev):
     lg = H(logits[torch.from_numpy(pick).to(dev)]).astype(np.float64)
     full = np.broadcast_to(a["table"], (len(pick), a["table"].shape[0]))
     ref = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], full, a["lens"][pick], ctx)
-    bound = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], full, a["lens"][pick], ctx, magnitude=True)
-    assert_scores_close(lg, ref, bound)
-    e_slots, e_raw = O.transform_topk(lg.astype(np.float32), a["lens"][pick], full, TOP, 6)
+    worst = assert_scores_rel(lg, ref)
+    # every row's Top-K and slots against the oracle on the GPU's logits
+    table_all = np.broadcast_to(a["table"], (rows, a["table"].shape[0]))
+    e_slots, e_raw = O.transform_topk_rows(H(logits), a["lens"], table_all, TOP, 6)
     raw_h, slots_h = H(raw), H(slots)
-    assert np.array_equal(raw_h[pick], e_raw) and np.array_equal(slots_h[pick], e_slots)
-    assert np.array_equal(H(out[torch.from_numpy(pick).to(dev)]), O.gather_rows(a["latent"], e_slots))
-    # every row: T distinct candidates, ascending, below the row's length
-    assert (raw_h >= 0).all() and (np.diff(raw_h, axis=1) > 0).all()
-    assert (raw_h < a["lens"][:, None]).all()
-    assert np.array_equal(slots_h, (a["table"][raw_h >> 6] << 6) | (raw_h & 63))
+    assert np.array_equal(raw_h, e_raw) and np.array_equal(slots_h, e_slots)
+    # gathered bytes: 64 rows (first, last and a seeded sample)
+    grows = np.unique(np.concatenate([[0, rows - 1], g.choice(rows, 62, replace=False)]))
+    assert np.array_equal(H(out[torch.from_numpy(grows).to(dev)]), O.gather_rows(a["latent"], e_slots[grows]))
+    print(f"config 4: {rows} rows Top-K/slots equal; scores of {len(pick)} rows within {worst:.2e} relative; "
+          f"gather of {len(grows)} rows equal")
 
 
 def test_config5_decode_batch(dev):
@@ -250,9 +256,7 @@ def test_config5_decode_batch(dev):
     pick = _sample_rows(rows, g, extra=(int(np.argmax(a["lens"])), int(np.argmin(a["lens"]))))
     lg = H(logits[torch.from_numpy(pick).to(dev)]).astype(np.float64)
     ref = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], a["table"][pick], a["lens"][pick], max_ctx)
-    bound = O.paged_logits(a["q8"][pick], a["w"][pick], a["native"], a["table"][pick], a["lens"][pick], max_ctx,
-                           magnitude=True)
-    assert_scores_close(lg, ref, bound)
+    assert_scores_rel(lg, ref)
     e_slots, e_raw = O.transform_topk(lg.astype(np.float32), a["lens"][pick], a["table"][pick], TOP, 6)
     raw_h, slots_h = H(raw), H(slots)
     assert np.array_equal(raw_h[pick], e_raw) and np.array_equal(slots_h[pick], e_slots)
@@ -309,9 +313,7 @@ def test_config5_route_chain(dev, config5_route):
                                      clean_logits=True)
     coarse_h = H(coarse)
     ref = O.paged_logits(a["q8"][pick], a["w"][pick], a["centers"], a["center_table"][pick], meta[3][pick], P * 8)
-    bound = O.paged_logits(a["q8"][pick], a["w"][pick], a["centers"], a["center_table"][pick], meta[3][pick], P * 8,
-                           magnitude=True)
-    assert_scores_close(coarse_h[pick].astype(np.float64), ref, bound)
+    assert_scores_rel(coarse_h[pick].astype(np.float64), ref)
 
     # fused route (no table fill, runtime.py:445-448), then fine_table_shared
     sel, ft = i32(rows, TAKE), i32(rows, FP)
@@ -340,8 +342,7 @@ def test_config5_route_chain(dev, config5_route):
     scores = SC.fp8_paged_mqa_logits(q, fine_d, d["w"], dg_lens, ft, None, WIDTH, clean_logits=True)
     pre = H(scores[pick_d])
     ref = O.paged_logits(a["q8"][pick], a["w"][pick], fine_h, ft_h[pick], meta[2][pick], WIDTH)
-    bound = O.paged_logits(a["q8"][pick], a["w"][pick], fine_h, ft_h[pick], meta[2][pick], WIDTH, magnitude=True)
-    assert_scores_close(pre.astype(np.float64), ref, bound)
+    assert_scores_rel(pre.astype(np.float64), ref)
     K.mask_fine[(rows, -(-WIDTH // 256))](scores, sel, d["rt"], d["members"], d["lens"], takes, P, TAKE,
                                           scores.stride(0), WIDTH, SINK, WIN)
     post = H(scores)
