@@ -17,8 +17,12 @@
 // Shared-table rows (a prefill chunk of one request) are tiled 8 queries per
 // work-group: each 8448-byte key page is staged once in LDS (chunks of each
 // key row swizzled so that the 16-byte fragment reads are bank-conflict free)
-// and reused by 8 queries x 64 heads.  Rows with their own tables (decode) run one
-// query per work-group, each wave streaming whole pages straight from HBM.
+// and reused by 8 queries x 64 heads.  Rows with their own tables run one
+// query per work-group, each wave streaming whole pages straight from HBM
+// (decode batches), or, for more than 512 rows (a prefill chunk's rows share
+// most of their pages), through the same LDS page ring over the union of each
+// 8-row group's table pages (score_union_plan + the union form of
+// score_shared), each wave skipping the pages neither of its queries lists.
 #include <algorithm>
 #include <mutex>
 
@@ -72,6 +76,15 @@ struct ScoreParams {
     int32_t lvl_chunks[16];
     uint32_t* exact_pages;  // shared-table ReLU path: per row, a bitmap of pages for score_exact
     int32_t exact_words;    // 32-bit words per row of exact_pages (score_exact)
+    // union form (per-row tables through the page ring), built by score_union_plan:
+    const int32_t* u_pages;    // [groups * u_cap] pool page of each union entry (-1: none, reads zeros)
+    const uint32_t* u_mask;    // [groups * u_cap] rows of the group that list the entry (bit q)
+    const int32_t* u_slots;    // [groups * u_cap * 8] the table slot of row q (where its mask bit is set)
+    const int32_t* u_items;    // [kUnionLevels * u_level_stride] (group, first entry | entries << 16)
+    const int32_t* u_level_n;  // [kUnionLevels] items per level
+    int32_t u_cap;             // union entries per group (8 * table pages of max_context_len)
+    int32_t u_level_stride;
+    const int32_t* row_filter;  // score_rows: rows whose entry is 0 are skipped (nullptr: every row)
 };
 constexpr int kMaxLevels = 16;
 
@@ -134,10 +147,11 @@ __device__ __forceinline__ float wave_all(float v, Op op) {
 // record described above.
 __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float* w, int32_t rows, int32_t heads,
                                                   int32_t relu, uint8_t* out, uint32_t* work, uint32_t* exact_pages,
-                                                  int32_t exact_words) {
+                                                  int32_t exact_words, uint32_t* clear, int32_t nclear) {
     const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int l = __lane_id();
     if (blockIdx.x == 0 && threadIdx.x == 0) *work = 0u;  // the work counter of score_shared
+    if (blockIdx.x == 0 && (int)threadIdx.x < nclear) clear[threadIdx.x] = 0u;  // the union plan's level counts
     if (row >= rows) return;
     for (int k = l; k < exact_words; k += kWave) exact_pages[row * exact_words + k] = 0u;
     // lane l owns dims 2l, 2l+1; every head's two bytes come in one round
@@ -338,7 +352,18 @@ __device__ __forceinline__ void dma4(const i32x4& rs, int32_t voff, uint32_t lds
 constexpr int kMaxRangePages = 256;
 constexpr int kMarkWords = kMaxRangePages / 32 + 1;  // an item's pages start at a multiple of 16
 
-template <int HB, bool RELU>
+// Union form (per-row tables): an item is a range of at most kUnionRange of a
+// group's union entries (one per lane of a wave); items are listed per level,
+// full ranges (level 0) before the halving tail (levels 1 ..).
+constexpr int kUnionRange = 64;
+constexpr int kUnionLevels = 10;
+static_assert(kUnionRange == kWave && kUnionRange <= kMaxRangePages, "one union entry per lane");
+
+// UNION: the item's pages are union entries of per-row tables (their columns
+// come from each row's table slot; a wave skips the MFMAs of a page neither
+// of its queries lists, while the ring, the barriers and the store count go
+// on unchanged).
+template <int HB, bool RELU, bool UNION = false>
 __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t st0[V1_PAGE_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t st1[V1_PAGE_BYTES];
@@ -351,8 +376,19 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // all zero between items.
     __shared__ uint32_t marks[RELU ? kQueriesPerGroup * kMarkWords : 1];
     const int t = threadIdx.x, l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    if (RELU)
+    if (RELU && !UNION)
         for (int i = t; i < kQueriesPerGroup * kMarkWords; i += kThreads) marks[i] = 0u;
+    // union items per level (final before this kernel starts)
+    int32_t lvl_n[UNION ? kUnionLevels : 1];
+    int32_t total_items = p.items;
+    if constexpr (UNION) {
+        total_items = 0;
+#pragma unroll
+        for (int L = 0; L < kUnionLevels; ++L) {
+            lvl_n[L] = __builtin_amdgcn_readfirstlane(p.u_level_n[L]);
+            total_items += lvl_n[L];
+        }
+    }
   for (;;) {
     // every wave has finished the previous item (its LDS is free) when the
     // next one is drawn
@@ -360,12 +396,30 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     if (t == 0) item_sh = (int32_t)atomicAdd(p.work, 1u);
     __syncthreads();
     const int32_t item = __builtin_amdgcn_readfirstlane(item_sh);
-    if (item >= p.items) break;
-    const int32_t group = item % p.groups, level = item / p.groups;
+    if (item >= total_items) break;
+    int32_t group, page_begin, nchunk = 0, ulen = 0;
+    int64_t ubase = 0;  // union: the item's first entry
+    if constexpr (UNION) {
+        int32_t idx = item, L = 0;
+#pragma unroll
+        for (int k = 0; k < kUnionLevels - 1; ++k)
+            if (L == k && idx >= lvl_n[k]) {
+                idx -= lvl_n[k];
+                L = k + 1;
+            }
+        const int2 it = reinterpret_cast<const int2*>(p.u_items)[(int64_t)L * p.u_level_stride + idx];
+        group = __builtin_amdgcn_readfirstlane(it.x);
+        page_begin = __builtin_amdgcn_readfirstlane(it.y) & 0xffff;
+        ulen = __builtin_amdgcn_readfirstlane(it.y) >> 16;
+        ubase = (int64_t)group * p.u_cap + page_begin;
+    } else {
+        group = item % p.groups;
+        const int32_t level = item / p.groups;
+        const int32_t c_begin = level < p.bulk ? level * p.full : p.lvl_start[level - p.bulk];
+        nchunk = level < p.bulk ? p.full : p.lvl_chunks[level - p.bulk];
+        page_begin = c_begin * kChunkPages;
+    }
     const int64_t row0 = (int64_t)group * kQueriesPerGroup;
-    const int32_t c_begin = level < p.bulk ? level * p.full : p.lvl_start[level - p.bulk];
-    const int32_t nchunk = level < p.bulk ? p.full : p.lvl_chunks[level - p.bulk];
-    const int32_t page_begin = c_begin * kChunkPages;
     const int32_t grows = (int32_t)min<int64_t>(kQueriesPerGroup, (int64_t)p.rows - row0);  // rows of the group
 
     // The independent loads of the prologue are all issued before the first
@@ -378,13 +432,23 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         lane_ctx = r < p.rows ? c : 0;
     }
     int32_t pid[kMaxRangePages / kThreads];
-    if (p.max_blocks > 0) {
+    static_assert(kMaxRangePages == kThreads, "one page id per thread");
+    // Union: lane l of every wave holds entry l's table slots for the wave's
+    // two queries, packed as 16-bit halves (0xffff: not listed; slots are
+    // below kUnionEntries), loaded with the prologue.
+    uint32_t uslots = 0xffffffffu;
+    if constexpr (UNION) {
+        pid[0] = p.u_pages[ubase + min(t, ulen - 1)];
+        if (t >= ulen) pid[0] = -1;
+    } else if (p.max_blocks > 0) {
 #pragma unroll
         for (int k = 0; k < kMaxRangePages / kThreads; ++k) pid[k] = page_of_unchecked(p, row0, page_begin + k * kThreads + t);
     } else {
 #pragma unroll
         for (int k = 0; k < kMaxRangePages / kThreads; ++k) pid[k] = -1;
     }
+    uint64_t umark[kQueriesPerWave] = {0ull, 0ull};  // union: item pages holding keys for the exact form
+    uint64_t use_mask = ~0ull;                         // union: item pages either of this wave's queries lists
     // Query fragments, weights and linear-term coefficients.  Rows past the
     // end read the last row (their logits are never stored).
     v8i a[kQueriesPerWave][HB];
@@ -431,13 +495,14 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     for (int q = 0; q < kQueriesPerGroup; ++q) max_ctx = max(max_ctx, __builtin_amdgcn_readlane(lane_ctx, q));
 #pragma unroll
     for (int q = 0; q < kQueriesPerWave; ++q) ctx[q] = __builtin_amdgcn_readlane(lane_ctx, wv * kQueriesPerWave + q);
-    // pages of the range below the group's longest context
-    const int32_t npages = max(0, min(nchunk * kChunkPages, (max_ctx + 63) / 64 - page_begin));
+    // pages of the range below the group's longest context (union: every entry)
+    const int32_t npages = UNION ? ulen : max(0, min(nchunk * kChunkPages, (max_ctx + 63) / 64 - page_begin));
 
     // Pages of the item past the group's longest context are computed by
     // nobody: with clean_logits their columns below max_context_len get -inf.
+    // (Union: the plan fills the columns past each row's last page.)
     auto fill_rest = [&](int32_t from_page) __attribute__((always_inline)) {
-        if (!p.clean) return;
+        if (UNION || !p.clean) return;
         for (int32_t pg = from_page; pg < nchunk * kChunkPages; ++pg) {
 #pragma unroll
             for (int q = 0; q < kQueriesPerWave; ++q)
@@ -542,17 +607,25 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // in a rarely taken scalar branch with no vector memory operation); the
     // item's end hands the marks to score_exact.
     auto store = [&](int32_t pg, bool live, const float (&part)[kQueriesPerWave][4], float scale) {
-        const int32_t col = (page_begin + pg) * 64;  // this page's first column
 #pragma unroll
         for (int q = 0; q < kQueriesPerWave; ++q) {
             const float v = reduce_scatter4(part[q]);
             const int32_t qr = wv * kQueriesPerWave + q;  // row within the group
+            // this page's first column in the query's row (union: from the
+            // row's table slot; a page the row does not list stores nothing)
+            int32_t col = (page_begin + pg) * 64;
+            bool lq = live;
+            if constexpr (UNION) {
+                const uint32_t half = ((uint32_t)__builtin_amdgcn_readlane((int)uslots, max(pg, 0)) >> (16 * q)) & 0xffffu;
+                col = (int32_t)half * 64;
+                lq = live && half != 0xffffu;
+            }
             // columns [col, col + 64) of the query: logits below its context,
             // -inf from there to max_context_len with clean_logits; the
             // descriptor covers the columns to write, lanes past it are dropped
             const int32_t valid = ctx[q] - col;
             const int32_t end = (p.clean ? p.max_context_len : ctx[q]) - col;
-            const int32_t lim = (live && qr < grows && end > 0) ? (end < 64 ? end : 64) : 0;
+            const int32_t lim = (lq && qr < grows && end > 0) ? (end < 64 ? end : 64) : 0;
             const auto rs = __builtin_amdgcn_make_buffer_rsrc(p.logits + (row0 + qr) * p.logits_stride + col, 0,
                                                               lim * 4, kRawDword);
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l < valid ? v * scale : -__builtin_huge_valf()), rs,
@@ -562,12 +635,18 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
                 // uniform conditions join on the scalar side)
                 const uint64_t near = __builtin_amdgcn_ballot_w64(fabsf(v) <= exact_thr[q]) &
                                       __builtin_amdgcn_ballot_w64(l < valid);
-                if (near != 0ull && live && qr < grows) {
-                    // (the empty asm keeps this block's address arithmetic
-                    // from being hoisted out of the loop into live registers)
-                    int32_t bit = (page_begin & 31) + pg;
-                    asm volatile("" : "+s"(bit));
-                    if (l == 0) atomicOr(&marks[(wv * kQueriesPerWave + q) * kMarkWords + (bit >> 5)], 1u << (bit & 31));
+                if (near != 0ull && lq && qr < grows) {
+                    if constexpr (UNION) {
+                        // (a scalar bit per item page; handed out at the item's end)
+                        umark[q] |= 1ull << (pg & 63);
+                    } else {
+                        // (the empty asm keeps this block's address arithmetic
+                        // from being hoisted out of the loop into live registers)
+                        int32_t bit = (page_begin & 31) + pg;
+                        asm volatile("" : "+s"(bit));
+                        if (l == 0)
+                            atomicOr(&marks[(wv * kQueriesPerWave + q) * kMarkWords + (bit >> 5)], 1u << (bit & 31));
+                    }
                 }
             }
         }
@@ -593,11 +672,19 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
 #pragma unroll
         for (int j = kTotal - kLag; j < kTotal; ++j) consume(j, part);
     };
+    // Page j is computed: it lies in the item and (union) one of this wave's
+    // queries lists it.  (The union form runs up to 48 heads: with 64 the
+    // branch around the stream costs the register allocator ~30 VGPRs past
+    // the 256 of two waves per SIMD.)
+    constexpr bool kSkip = UNION;
+    auto used = [&](int32_t j) __attribute__((always_inline)) {
+        return j >= 0 && j < npages && (!kSkip || ((use_mask >> (j & 63)) & 1ull) != 0);
+    };
     // Step i: page i's fragments are in fc; fn holds page i-1's until page
     // i+1's are read into it.
     auto step = [&](int32_t i, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn,
                     float (&pc)[kQueriesPerWave][4], float (&pp)[kQueriesPerWave][4]) {
-        if (i < npages) {
+        if (used(i)) {
 #pragma unroll
             for (int idx = 0; idx < kTotal; ++idx) {
                 mfma_at(idx, fc);
@@ -608,15 +695,18 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
                     consume(idx - kLag, pc);
                 else
                     consume(kTotal + idx - kLag, pp);
-                if (idx == kStoreAt) store(i - 1, i > 0, pp, fn.scale);
+                if (idx == kStoreAt) store(i - 1, used(i - 1), pp, fn.scale);
                 if (idx == kSyncAt) sync(i, cur);
                 if (idx == kFragAt) load_frag(next, fn);
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
-            // past the last page: finish and store it (first time only)
-            if (i == npages) drain(pp);
-            store(i - 1, i == npages, pp, fn.scale);
+            // a page not computed (past the last page, or a union page this
+            // wave's queries do not list): finish and store the previous
+            // page if it was computed; the stores and loads of the step are
+            // issued as in a computed one
+            if (used(i - 1)) drain(pp);
+            store(i - 1, used(i - 1), pp, fn.scale);
             sync(i, cur);
             load_frag(next, fn);
         }
@@ -635,6 +725,16 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
 #pragma unroll
     for (int q = 0; q < kQueriesPerWave; ++q)
         exact_thr[q] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, exact_thr[q])));
+    if constexpr (UNION) {
+        // (loaded after the prologue's wait: kept out of its register peak)
+        const int64_t e = ubase + min(l, ulen - 1);
+        const uint32_t umask = p.u_mask[e];
+        const int2 uslot2 = *reinterpret_cast<const int2*>(p.u_slots + e * kQueriesPerGroup + wv * kQueriesPerWave);
+        const bool in0 = l < ulen && ((umask >> (wv * kQueriesPerWave)) & 1u);
+        const bool in1 = l < ulen && ((umask >> (wv * kQueriesPerWave + 1)) & 1u);
+        uslots = (in0 ? (uint32_t)uslot2.x & 0xffffu : 0xffffu) | ((in1 ? (uint32_t)uslot2.y & 0xffffu : 0xffffu) << 16);
+        use_mask = __builtin_amdgcn_ballot_w64(in0 | in1);
+    }
     load_frag(st0, fa);
     for (int32_t i = 0; i < npages; i += kStages) {
         step(i, st0, st1, fa, fb, pa, pb);
@@ -642,12 +742,31 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         step(i + 2, st2, st3, fa, fb, pa, pb);
         step(i + 3, st3, st0, fb, fa, pb, pa);
     }
-    if (npages % kStages == 0) {
+    if (npages % kStages == 0 && used(npages - 1)) {
         drain(pb);
         store(npages - 1, true, pb, fb.scale);
     }
     V1_PAGE_BARRIER(0);  // the page buffers are reused by the next item
     fill_rest(npages);
+    if constexpr (UNION) {
+        // marked pages to the rows' page bitmaps, at each row's table slot
+        if (RELU) {
+            const int32_t words = (((p.max_context_len + 63) >> 6) + 31) >> 5;
+#pragma unroll
+            for (int q = 0; q < kQueriesPerWave; ++q) {
+                uint64_t m = umark[q];
+                while (m != 0ull) {
+                    const int32_t pg = __builtin_ctzll(m);
+                    m &= m - 1;
+                    const int32_t slot = (int32_t)(((uint32_t)__builtin_amdgcn_readlane((int)uslots, pg) >> (16 * q)) & 0xffffu);
+                    if (l == 0)
+                        atomicOr(p.exact_pages + (row0 + wv * kQueriesPerWave + q) * words + (slot >> 5),
+                                 1u << (slot & 31));
+                }
+            }
+        }
+        continue;
+    }
     // Marked pages go to the per-row page bitmap that score_exact reads (an
     // OR per word that has a mark; the words are cleared for the next item).
     // (The bitmaps' row length follows from max_context_len.)
@@ -675,11 +794,18 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
 // (up to kRowPids), so a page's key loads never wait on its table entry.
 constexpr int kRowPids = 2048;
 
-template <int HB, bool RELU>
+// FAST: the values of score_shared, bit for bit: the ReLU path takes the
+// linear-term pieces plus the |x| sum with the halved weights of the query's
+// record, and marks pages with a key near zero for score_exact; the signed
+// path takes the record's weights.  (The rows of a batch scored through the
+// union plan that score_rows takes instead then get the same values as the
+// plan's rows; otherwise ReLU is applied directly.)
+template <int HB, bool RELU, bool FAST = false>
 __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
     __shared__ int32_t pid_s[kRowPids];
     const int l = __lane_id(), wv = threadIdx.x / kWave;
     const int64_t row = blockIdx.y;
+    if (p.row_filter != nullptr && p.row_filter[row] == 0) return;
     const int32_t ctx = min(p.ctx[row], p.max_context_len);
     const int32_t row_pages = (ctx + 63) / 64;
     const int32_t all_pages = (p.max_context_len + 63) / 64;
@@ -705,7 +831,33 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
         v8i a[HB];
         float w[HB][4];
         load_q<HB>(p, row, a);
-        load_w<HB>(p, row, w);
+        // FAST: the record's weights, linear-term pieces (both queries of
+        // score_shared's row block are this row: its result rows of the
+        // first query are the ones kept) and exact-path threshold
+        v8i alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+        float coef[2] = {0.f, 0.f}, exact_thr = 0.f;
+        if constexpr (FAST) {
+            const uint8_t* rec = p.pieces + row * kPieceRowBytes;
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb) {
+                const v4f x = *reinterpret_cast<const v4f*>(rec + kRecWeights + (hb * 16 + 4 * (l >> 4)) * 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[hb][i] = x[i];
+            }
+            if (RELU) {
+                const float2 c2 = *reinterpret_cast<const float2*>(rec + kRecScales + 8 * (l >> 4));
+                coef[0] = c2.x;
+                coef[1] = c2.y;
+                exact_thr = *reinterpret_cast<const float*>(rec + kRecBound);
+                const int rr = l & 15;
+                const int piece = 2 * (rr >> 2) + (rr & 1);
+                const u32x4* src = reinterpret_cast<const u32x4*>(rec + piece * 128 + 32 * (l >> 4));
+                const u32x4 x = src[0], y = src[1];
+                alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+            }
+        } else {
+            load_w<HB>(p, row, w);
+        }
         auto fetch = [&](int32_t s, int32_t pg, v8i (&b)[4], float& scale) __attribute__((always_inline)) {
             const int32_t page = pool_page(s, pg);
             if (page < 0) return false;
@@ -723,8 +875,38 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
             float out = 0.f;
             if (ok) {
                 float part[4];
-                page_partials<HB, RELU>(a, b, w, part);
+                if constexpr (FAST) {
+                    // score_shared's consume order: the linear block sets the
+                    // partial, then every head block's four results in order
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb) {
+                        float acc = 0.f;
+                        if (RELU) {
+                            const v4f x = mfma_fp8(alin, b[kb]);
+                            acc = fmaf(coef[1], x[1], coef[0] * x[0]);
+                        }
+#pragma unroll
+                        for (int hb = 0; hb < HB; ++hb) {
+                            const v4f d = mfma_fp8(a[hb], b[kb]);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const float prev = (!RELU && hb == 0 && i == 0) ? 0.f : acc;
+                                acc = fmaf(w[hb][i], RELU ? fabsf(d[i]) : d[i], prev);
+                            }
+                        }
+                        part[kb] = acc;
+                    }
+                } else {
+                    page_partials<HB, RELU>(a, b, w, part);
+                }
                 out = reduce_scatter4(part);
+                if (FAST && RELU) {
+                    const uint64_t near = __builtin_amdgcn_ballot_w64(fabsf(out) <= exact_thr && pg * 64 + l < ctx);
+                    if (near != 0ull && l == 0) {
+                        const int32_t words = (((p.max_context_len + 63) >> 6) + 31) >> 5;
+                        atomicOr(p.exact_pages + row * words + (pg >> 5), 1u << (pg & 31));
+                    }
+                }
             } else {
                 scale = 0.f;
             }
@@ -799,6 +981,229 @@ __global__ __launch_bounds__(256) void score_exact(ScoreParams p) {
                 const int32_t j = pg * 64 + l;
                 if (j < ctx) p.logits[row * p.logits_stride + j] = v;
             }
+        }
+    }
+}
+
+
+// ---------------------------------------------------------- union plan
+// Per-row tables of a batch whose rows share most of their pages (the rows
+// of one prefill chunk) go through the shared-table kernel's page ring: per
+// group of 8 rows, the (row, slot) pairs of the rows' live table slots are
+// sorted by (page, row, slot); every distinct page becomes a union entry,
+// and a row that lists a page k times puts its k-th slot in the page's k-th
+// entry.  Entries hold the pool page (-1 for slots past the table or out of
+// the pool: their keys read as zeros and score 0, as in score_rows), a
+// mask of the rows that list it and each such row's slot.  The group's
+// entries are cut into items of at most kUnionRange entries, full ranges
+// first (level 0), then a halving tail (levels 1 ..), appended to per-level
+// lists; groups whose rows share too little (fewer than two rows per page
+// on average) are flagged for score_rows instead.  One work-group per group;
+// with clean_logits it also fills the columns past each row's last page.
+constexpr int kUnionEntries = 8192;  // (row, slot) pairs of a group: 8 rows x 1024 table pages
+static_assert(kUnionEntries < 0xffff, "union slots fit 16 bits");
+constexpr int kPlanThreads = 512;
+constexpr int kPlanPer = kUnionEntries / kPlanThreads;  // pairs per thread
+// LDS of the plan (dynamic, sized by the call's largest group): keys (8 B),
+// run counts (4 B) and entry masks (4 B) per pair.
+inline int64_t plan_lds_bytes(int32_t max_pairs) {
+    int64_t n = 2;
+    while (n < max_pairs) n <<= 1;
+    return 16 * n;
+}
+constexpr int kUnionMinRows = 513;   // decode batches (the reference's <= 512 rows) keep score_rows
+constexpr uint32_t kNoPage = 0x7fffffffu;
+
+struct UnionOut {
+    int32_t* pages;
+    uint32_t* mask;
+    int32_t* slots;
+    int32_t* items;     // int2 per item
+    int32_t* level_n;
+    int32_t* fallback;  // [rows] 1: the row is scored by score_rows
+};
+
+// Exclusive prefix sum (kOp 0) or exclusive running max (kOp 1, identity -1)
+// of one value per thread over the work-group; `total` is the sum / max of all.
+template <int kOp>
+__device__ __forceinline__ int32_t plan_scan(int32_t v, int32_t* part, int32_t& total) {
+    const int w = threadIdx.x / kWave, l = __lane_id();
+    int32_t inc = v;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int32_t o = __shfl_up(inc, off, kWave);
+        if (l >= off) inc = kOp == 0 ? inc + o : max(inc, o);
+    }
+    if (l == kWave - 1) part[w] = inc;
+    __syncthreads();
+    int32_t before = kOp == 0 ? 0 : -1;
+    total = kOp == 0 ? 0 : -1;
+#pragma unroll
+    for (int k = 0; k < kPlanThreads / kWave; ++k) {
+        const int32_t x = part[k];
+        if (k < w) before = kOp == 0 ? before + x : max(before, x);
+        total = kOp == 0 ? total + x : max(total, x);
+    }
+    __syncthreads();  // part is free again
+    const int32_t excl_in_wave = __shfl_up(inc, 1, kWave);
+    const int32_t wave_excl = l == 0 ? (kOp == 0 ? 0 : -1) : excl_in_wave;
+    return kOp == 0 ? before + wave_excl : max(before, wave_excl);
+}
+
+__global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, UnionOut u, int32_t lds_pairs) {
+    extern __shared__ __attribute__((aligned(16))) uint64_t plan_lds[];
+    uint64_t* key = plan_lds;                                        // [lds_pairs]
+    int32_t* run = reinterpret_cast<int32_t*>(plan_lds + lds_pairs);  // per page run: its entries, then its first
+    uint32_t* umask = reinterpret_cast<uint32_t*>(run + lds_pairs);   // per entry: the rows listing it
+    __shared__ int32_t part[kPlanThreads / kWave];
+    const int t = threadIdx.x;
+    const int32_t g = blockIdx.x;
+    const int64_t row0 = (int64_t)g * kQueriesPerGroup;
+    const int32_t grows = (int32_t)min<int64_t>(kQueriesPerGroup, (int64_t)p.rows - row0);
+    const int64_t gbase = (int64_t)g * p.u_cap;
+    // live table slots per row and their offsets in the pair list
+    int32_t off[kQueriesPerGroup + 1];
+    off[0] = 0;
+#pragma unroll
+    for (int q = 0; q < kQueriesPerGroup; ++q) {
+        const int32_t c = q < grows ? min(p.ctx[row0 + q], p.max_context_len) : 0;
+        off[q + 1] = off[q] + (max(c, 0) + 63) / 64;
+    }
+    const int32_t E = off[kQueriesPerGroup];  // <= kUnionEntries (8 * table pages of max_context_len)
+    int32_t N = 2;
+    while (N < E) N <<= 1;
+    for (int32_t e = t; e < N; e += kPlanThreads) {
+        uint64_t k = ~0ull;
+        if (e < E) {
+            int q = 0;
+#pragma unroll
+            for (int j = 1; j < kQueriesPerGroup; ++j) q += e >= off[j] ? 1 : 0;
+            const int32_t slot = e - off[q];
+            const int32_t page = page_of(p, row0 + q, slot);
+            k = ((uint64_t)(page >= 0 ? (uint32_t)page : kNoPage) << 32) | ((uint64_t)q << 24) | (uint32_t)slot;
+            run[e] = 0;
+            umask[e] = 0u;
+        }
+        key[e] = k;
+    }
+    __syncthreads();
+    // ascending bitonic sort of the N keys
+    for (int32_t k = 2; k <= N; k <<= 1) {
+        for (int32_t j = k >> 1; j > 0; j >>= 1) {
+            for (int32_t i = t; i < N / 2; i += kPlanThreads) {
+                const int32_t a = ((i & ~(j - 1)) << 1) | (i & (j - 1)), b = a + j;
+                const uint64_t x = key[a], y = key[b];
+                if ((x > y) == ((a & k) == 0)) {
+                    key[a] = y;
+                    key[b] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // thread t owns pairs [t * c, t * c + c)
+    const int32_t c = (E + kPlanThreads - 1) / kPlanThreads;
+    int32_t P[kPlanPer], Q[kPlanPer], S[kPlanPer], R[kPlanPer], K[kPlanPer];
+    int32_t nstart = 0, last = -1;
+#pragma unroll
+    for (int j = 0; j < kPlanPer; ++j) {
+        const int32_t i = t * c + j;
+        P[j] = -1;
+        if (j < c && i < E) {
+            const uint64_t x = key[i], y = i > 0 ? key[i - 1] : ~0ull;
+            P[j] = (int32_t)(x >> 32);
+            Q[j] = (int32_t)((x >> 24) & 0xff);
+            S[j] = (int32_t)(x & 0xffffff);
+            const bool ps = i == 0 || (x >> 32) != (y >> 32);
+            const bool pqs = ps || ((x >> 24) & 0xff) != ((y >> 24) & 0xff);
+            nstart += ps ? 1 : 0;
+            R[j] = nstart;  // page starts up to here within the chunk
+            if (pqs) last = i;
+            K[j] = last;    // last (page, row) start up to here within the chunk
+        }
+    }
+    int32_t runs, dummy;
+    const int32_t run_before = plan_scan<0>(nstart, part, runs);
+    const int32_t last_before = plan_scan<1>(last, part, dummy);
+#pragma unroll
+    for (int j = 0; j < kPlanPer; ++j) {
+        if (P[j] == -1) continue;
+        const int32_t i = t * c + j;
+        R[j] += run_before - 1;                        // page run of the pair
+        K[j] = i - max(K[j], last_before);             // its occurrence among the row's slots of the page
+        atomicMax(&run[R[j]], K[j] + 1);
+    }
+    __syncthreads();
+    // entries per run -> first entry per run (exclusive sum over the runs)
+    int32_t cnt[kPlanPer];
+    int32_t local = 0;
+#pragma unroll
+    for (int j = 0; j < kPlanPer; ++j) {
+        const int32_t r = t * c + j;
+        cnt[j] = (j < c && r < runs) ? run[r] : 0;
+        local += cnt[j];
+    }
+    int32_t U;
+    int32_t first = plan_scan<0>(local, part, U);
+#pragma unroll
+    for (int j = 0; j < kPlanPer; ++j) {
+        const int32_t r = t * c + j;
+        if (j < c && r < runs) run[r] = first;
+        first += cnt[j];
+    }
+    __syncthreads();
+    // two or more rows per union page on average
+    const bool shared = 2 * U <= E;
+#pragma unroll
+    for (int j = 0; j < kPlanPer; ++j) {
+        if (P[j] == -1 || !shared) continue;
+        const int32_t e = run[R[j]] + K[j];
+        u.slots[(gbase + e) * kQueriesPerGroup + Q[j]] = S[j];
+        u.pages[gbase + e] = P[j] == (int32_t)kNoPage ? -1 : P[j];  // (every pair of the entry writes the same page)
+        atomicOr(&umask[e], 1u << Q[j]);
+    }
+    __syncthreads();
+    if (shared)
+        for (int32_t e = t; e < U; e += kPlanThreads) u.mask[gbase + e] = umask[e];
+    if (t < grows) u.fallback[row0 + t] = shared ? 0 : 1;
+    if (shared && p.clean) {
+        // columns past each row's last live page (score_rows fills them for flagged rows)
+        for (int q = 0; q < grows; ++q) {
+            float* rp = p.logits + (row0 + q) * p.logits_stride;
+            for (int32_t j = (off[q + 1] - off[q]) * 64 + t; j < p.max_context_len; j += kPlanThreads)
+                rp[j] = -__builtin_huge_valf();
+        }
+    }
+    if (shared && t < kUnionLevels) {
+        // thread 0: the full ranges (level 0); thread L >= 1: the L-th range
+        // of the halving tail, if the group's entries reach it
+        const int32_t bulk = U > 2 * kUnionRange ? (U - kUnionRange) / kUnionRange : 0;
+        int32_t first = 0, count = 0, start = 0, len = 0;
+        if (t == 0) {
+            count = bulk;
+        } else {
+            int32_t e = bulk * kUnionRange;
+            for (int L = 1; L <= t && e < U; ++L) {
+                const int32_t left = U - e;
+                const int32_t size = min(left == 1 ? 1 : (left + 1) / 2, kUnionRange);
+                if (L == t) {
+                    start = e;
+                    len = size;
+                    count = 1;
+                }
+                e += size;
+            }
+        }
+        if (count > 0) first = atomicAdd(u.level_n + t, count);
+        int32_t* it = u.items + 2 * ((int64_t)t * p.u_level_stride + first);
+        if (t == 0) {
+            for (int32_t b = 0; b < bulk; ++b) {
+                it[2 * b] = g;
+                it[2 * b + 1] = (b * kUnionRange) | (kUnionRange << 16);
+            }
+        } else if (count > 0) {
+            it[0] = g;
+            it[1] = start | (len << 16);
         }
     }
 }
@@ -944,10 +1349,22 @@ struct Shared {
         hipLaunchKernelGGL((score_shared<HB, RELU>), g, dim3(kThreads), 0, st, p);
     }
 };
+struct SharedUnion {  // (v1_score takes the union form from 17 to 48 heads only)
+    template <int HB, bool RELU>
+    static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
+        if constexpr (HB == 2 || HB == 3) hipLaunchKernelGGL((score_shared<HB, RELU, true>), g, dim3(kThreads), 0, st, p);
+    }
+};
 struct Rows {
     template <int HB, bool RELU>
     static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
         hipLaunchKernelGGL((score_rows<HB, RELU>), g, dim3(kThreads), 0, st, p);
+    }
+};
+struct RowsFast {  // (the flagged rows of the union form: 17 to 48 heads)
+    template <int HB, bool RELU>
+    static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
+        if constexpr (HB == 2 || HB == 3) hipLaunchKernelGGL((score_rows<HB, RELU, true>), g, dim3(kThreads), 0, st, p);
     }
 };
 
@@ -981,6 +1398,44 @@ static int32_t exact_words(int32_t max_context_len) { return (int32_t)cdiv(cdiv(
 extern "C" int64_t v1_score_workspace(int32_t rows, int32_t max_context_len) {
     if (rows <= 0 || max_context_len < 0) return 0;
     return (int64_t)rows * kPieceRowBytes + 256 + (int64_t)rows * exact_words(max_context_len) * 4;
+}
+
+// Per-row tables through the union plan: the shared-table workspace, then
+// the plan (entries, masks, slots, items, level counts, row flags), each
+// part 256-byte aligned.
+namespace {
+struct UnionLayout {
+    int64_t pages, mask, slots, items, level_n, fallback, total;
+    int32_t cap, level_stride;
+};
+static int64_t align_up(int64_t x) { return (x + 255) & ~int64_t(255); }
+UnionLayout union_layout(int32_t rows, int32_t max_context_len) {
+    UnionLayout L{};
+    const int64_t groups = cdiv(rows, kQueriesPerGroup);
+    L.cap = (int32_t)(kQueriesPerGroup * cdiv(max_context_len, 64));
+    L.level_stride = (int32_t)(groups * (L.cap / kUnionRange + 2));
+    int64_t at = align_up(v1_score_workspace(rows, max_context_len));
+    L.pages = at;
+    at = align_up(at + groups * L.cap * 4);
+    L.mask = at;
+    at = align_up(at + groups * L.cap * 4);
+    L.slots = at;
+    at = align_up(at + groups * L.cap * 4 * kQueriesPerGroup);
+    L.items = at;
+    at = align_up(at + (int64_t)kUnionLevels * L.level_stride * 8);
+    L.level_n = at;
+    at = align_up(at + kUnionLevels * 4);
+    L.fallback = at;
+    L.total = align_up(at + (int64_t)rows * 4);
+    return L;
+}
+}  // namespace
+
+extern "C" int64_t v1_score_tables_workspace(int32_t rows, int32_t max_context_len) {
+    if (rows < kUnionMinRows || max_context_len <= 0 ||
+        (int64_t)kQueriesPerGroup * cdiv(max_context_len, 64) > kUnionEntries)
+        return 0;
+    return union_layout(rows, max_context_len).total;
 }
 
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
@@ -1039,11 +1494,83 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         p.exact_words = a->relu ? exact_words(a->max_context_len) : 0;
         const dim3 row_waves((uint32_t)cdiv(a->rows, 4));
         hipLaunchKernelGGL(score_prep, row_waves, dim3(256), 0, st, a->q, a->weights, a->rows, a->heads, a->relu, ws,
-                           p.work, p.exact_pages, p.exact_words);
+                           p.work, p.exact_pages, p.exact_words, nullptr, 0);
         int rc = V1_LAUNCHED("score_prep");
         if (rc != V1_OK) return rc;
         launch_hb<Shared>(hb, a->relu != 0, dim3((uint32_t)std::min<int64_t>(items, wgs)), st, p);
         rc = V1_LAUNCHED("score_shared");
+        if (rc != V1_OK || !a->relu) return rc;
+        switch (hb) {
+            case 1: hipLaunchKernelGGL(score_exact<1>, row_waves, dim3(256), 0, st, p); break;
+            case 2: hipLaunchKernelGGL(score_exact<2>, row_waves, dim3(256), 0, st, p); break;
+            case 3: hipLaunchKernelGGL(score_exact<3>, row_waves, dim3(256), 0, st, p); break;
+            default: hipLaunchKernelGGL(score_exact<4>, row_waves, dim3(256), 0, st, p); break;
+        }
+        return V1_LAUNCHED("score_exact");
+    }
+    // Per-row tables of more than 512 rows with a large enough workspace:
+    // the union plan, the shared-table kernel over each group's union, and
+    // score_rows for the rows of groups that share too little.
+    // Measured: with one head block score_rows' cost per page (a few MFMAs)
+    // is below the ring's, and with 64 heads, where every union page is
+    // computed for all 8 rows, the plan lost to score_rows at the reference's
+    // page_fraction 0.5 (1024 rows x 545 pages: 0.545 against 0.514 ms); from
+    // 17 to 48 heads the waves skip the pages their rows do not list (4096
+    // rows x 32 heads, 40 routed pages: 0.31 -> 0.23 ms).
+    const int64_t plan_need = v1_score_tables_workspace(a->rows, a->max_context_len);
+    const bool plan = plan_need > 0 && a->heads > 16 && a->heads <= 48 && a->workspace != nullptr &&
+                      a->workspace_bytes >= plan_need && (reinterpret_cast<uintptr_t>(a->workspace) & 255) == 0;
+    if (plan) {
+        const UnionLayout L = union_layout(a->rows, a->max_context_len);
+        const int64_t groups = cdiv(a->rows, kQueriesPerGroup);
+        uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+        p.pieces = ws;
+        p.work = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes);
+        p.exact_pages = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes + 256);
+        p.exact_words = a->relu ? exact_words(a->max_context_len) : 0;
+        p.groups = (int32_t)groups;
+        p.u_cap = L.cap;
+        p.u_level_stride = L.level_stride;
+        UnionOut u{reinterpret_cast<int32_t*>(ws + L.pages), reinterpret_cast<uint32_t*>(ws + L.mask),
+                   reinterpret_cast<int32_t*>(ws + L.slots), reinterpret_cast<int32_t*>(ws + L.items),
+                   reinterpret_cast<int32_t*>(ws + L.level_n), reinterpret_cast<int32_t*>(ws + L.fallback)};
+        p.u_pages = u.pages;
+        p.u_mask = u.mask;
+        p.u_slots = u.slots;
+        p.u_items = u.items;
+        p.u_level_n = u.level_n;
+        const dim3 row_waves((uint32_t)cdiv(a->rows, 4));
+        hipLaunchKernelGGL(score_prep, row_waves, dim3(256), 0, st, a->q, a->weights, a->rows, a->heads, a->relu, ws,
+                           p.work, p.exact_pages, p.exact_words, reinterpret_cast<uint32_t*>(u.level_n),
+                           (int32_t)kUnionLevels);
+        int rc = V1_LAUNCHED("score_prep");
+        if (rc != V1_OK) return rc;
+        const int32_t max_pairs = (int32_t)(kQueriesPerGroup * cdiv(a->max_context_len, 64));
+        const int32_t lds_pairs = (int32_t)(plan_lds_bytes(max_pairs) / 16);
+        // (dynamic LDS past 64 KiB is allowed once per process)
+        static std::once_flag lds_once;
+        static hipError_t lds_err = hipSuccess;
+        std::call_once(lds_once, [] {
+            lds_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&score_union_plan),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)plan_lds_bytes(kUnionEntries));
+        });
+        if (lds_err != hipSuccess) return hip_status(lds_err, "score: hipFuncSetAttribute(score_union_plan)");
+        hipLaunchKernelGGL(score_union_plan, dim3((uint32_t)groups), dim3(kPlanThreads), plan_lds_bytes(max_pairs), st,
+                           p, u, lds_pairs);
+        rc = V1_LAUNCHED("score_union_plan");
+        if (rc != V1_OK) return rc;
+        launch_hb<SharedUnion>(hb, a->relu != 0, dim3((uint32_t)(2 * (int64_t)v1::device_cus())), st, p);
+        rc = V1_LAUNCHED("score_shared (union)");
+        if (rc != V1_OK) return rc;
+        // flagged rows with the plan's arithmetic (every row of the call gets
+        // the same values whichever kernel scores it), on score_rows' grid
+        ScoreParams pr = p;
+        pr.row_filter = u.fallback;
+        int64_t per_row = std::max<int64_t>(1, std::min<int64_t>(chunks, cdiv(24 * (int64_t)v1::device_cus(), a->rows)));
+        if (per_row > 1 && per_row % 2 == 0) --per_row;
+        launch_hb<RowsFast>(hb, a->relu != 0, dim3((uint32_t)per_row, (uint32_t)a->rows), st, pr);
+        rc = V1_LAUNCHED("score_rows (flagged rows)");
         if (rc != V1_OK || !a->relu) return rc;
         switch (hb) {
             case 1: hipLaunchKernelGGL(score_exact<1>, row_waves, dim3(256), 0, st, p); break;

@@ -1093,52 +1093,12 @@ __device__ __forceinline__ void transform_emit_batch(const int32_t* __restrict__
     }
 }
 
-// A V1 row with the sink/tail mask applied on the fly: positions of masked
-// pages (sm.maskpage) whose member lies outside [sink, tail) read as -inf.
-struct V1Src {
-    static constexpr bool kFloats = true;
-    static constexpr bool kBuffer = false;
-    RowSrc base;
-    const int32_t* members;
-    const int32_t* maskpage;  // LDS, indexed by (position - segment start) / 64
-    int32_t masked_end;       // positions below it may be masked (take * 64 - lo)
-    int32_t sink, tail;
-    int32_t n;
-    __device__ __forceinline__ void load_raw4(int32_t p, uint32_t (&v)[4]) const {
-        base.load_raw4(p, v);
-        if (p < masked_end) {
-            const int32_t page = maskpage[p >> 6];
-            if (page >= 0) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (p + e < n) {
-                        const int32_t lg = members[(int64_t)page * 64 + ((p + e) & 63)];
-                        if (lg < sink || lg >= tail) v[e] = kNegInfBits;
-                    }
-                }
-            }
-        }
-    }
-    __device__ __forceinline__ void load4(int32_t p, uint32_t (&k)[4]) const {
-        base.load4(p, k);
-        if (p < masked_end) {
-            const int32_t page = maskpage[p >> 6];
-            if (page >= 0) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (p + e < n) {
-                        const int32_t lg = members[(int64_t)page * 64 + ((p + e) & 63)];
-                        if (lg < sink || lg >= tail) k[e] = kNegInfKey;
-                    }
-                }
-            }
-        }
-    }
-};
-
 // Sets sm.maskpage for the ranks touching [lo, lo + span) (span <= kSpan) and
 // writes -inf in place for every masked position below min(take * 64, cols)
-// in that range.
+// in that range, so the selection then reads the masked row as it lies in
+// memory: the closing barrier is a work-group release / acquire, which
+// orders these stores before every later load of the work-group (its waves
+// share one CU and its vector L1, which stores write through).
 // sglang/kernels/jit/csrc/deepseek_v4/v1_query.cuh:71-107.  Ends with a barrier.
 __device__ void v1_prepare_mask(const V1Params& p, int64_t row, const RowInfo& ri, int32_t lo, int32_t span, SelSmem& sm,
                                 int32_t& masked_end) {
@@ -1159,18 +1119,10 @@ __device__ void v1_prepare_mask(const V1Params& p, int64_t row, const RowInfo& r
     __syncthreads();
 }
 
-__device__ __forceinline__ V1Src v1_source(const V1Params& p, int64_t row, const RowInfo& ri, int32_t lo, int32_t n,
-                                           int32_t masked_end, const SelSmem& sm) {
+// Columns [lo, lo + n) of a V1 row, masked in place by v1_prepare_mask.
+__device__ __forceinline__ RowSrc v1_source(const V1Params& p, int64_t row, int32_t lo, int32_t n) {
     const float* rp = p.scores + row * p.score_stride + lo;
-    V1Src s;
-    s.base = RowSrc{rp, n, (reinterpret_cast<uintptr_t>(rp) & 15) == 0};
-    s.members = p.members;
-    s.maskpage = sm.maskpage;
-    s.masked_end = masked_end;
-    s.sink = ri.sink;
-    s.tail = ri.tail;
-    s.n = n;
-    return s;
+    return RowSrc{rp, n, (reinterpret_cast<uintptr_t>(rp) & 15) == 0};
 }
 
 // --------------------------------------------------------- single pass
@@ -1183,7 +1135,7 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_rows(V1Params p) {
     const int32_t L = max(0, min(p.fine_lens[row], p.cols));
     int32_t masked_end;
     v1_prepare_mask(p, row, ri, 0, kSpan, sm, masked_end);
-    const V1Src src = v1_source(p, row, ri, 0, L, masked_end, sm);
+    const RowSrc src = v1_source(p, row, 0, L);
     const int32_t T = p.topk;
     if (L <= T) {
         for (int tx = threadIdx.x; tx < T; tx += kBlock) {
@@ -1385,7 +1337,7 @@ __global__ __launch_bounds__(kBlock, 8) void v1_topk_segments(V1Params p, Worksp
     v1_prepare_mask(p, row, ri, lo, ws.seg, sm, masked_end);
     if (L <= p.topk) return;  // the merge kernel takes every candidate
     const int32_t n = max(0, min(L - lo, ws.seg));
-    segment_select(v1_source(p, row, ri, lo, n, masked_end, sm), lo, p.topk, ws, row, s, sm);
+    segment_select(v1_source(p, row, lo, n), lo, p.topk, ws, row, s, sm);
 }
 
 __global__ __launch_bounds__(kBlock, 8) void transform_segments(TransformParams p, Workspace ws) {

@@ -62,6 +62,11 @@ class V1QueryModule:
 
     def topk(self, scores, fine_lens, members, rt, nt, selected, lens, takes, physical, logical, raw, window, mask,
              expanded, physical_output, bucket_from_rank, fine_table, direct_fine):
+        self._topk(scores, fine_lens, members, rt, nt, selected, lens, takes, physical, logical, raw, window, mask,
+                   expanded, physical_output, bucket_from_rank, fine_table, direct_fine, min_batch=513)
+
+    def _topk(self, scores, fine_lens, members, rt, nt, selected, lens, takes, physical, logical, raw, window, mask,
+              expanded, physical_output, bucket_from_rank, fine_table, direct_fine, min_batch):
         _lib.require_gpu(scores, fine_lens, members, rt, nt, selected, lens, takes, physical, logical, raw,
                          expanded, fine_table)
         B, L, S = _scores(scores)
@@ -89,7 +94,7 @@ class V1QueryModule:
         es = expanded.shape[1]
         _need(es == 0 or es == T * 4 + 64, "Invalid expansion buffer")
         _need(es == 0 or expanded.is_contiguous(), "expanded must be contiguous")
-        _need(B > 512 and 0 < T <= 2048 and 0 <= window <= 4096, "Unsupported fused V1 TopK")
+        _need(B >= min_batch and 0 < T <= 2048 and 0 <= window <= 4096, "Unsupported fused V1 TopK")
         ws, ws_bytes = workspace(scores.device, _lib.lib().v1_topk_workspace(B, L, T), "topk")
         a = _lib.TopkArgs(
             _lib.ptr(scores), S, B, L, _lib.ptr(fine_lens), _lib.ptr(members), members.shape[0], _lib.ptr(rt),
@@ -98,6 +103,21 @@ class V1QueryModule:
             int(bool(physical_output)), int(bool(bucket_from_rank)), _lib.ptr(fine_table), fine_table.shape[1],
             int(bool(direct_fine)), ws, ws_bytes)
         _lib.check(_lib.lib().v1_topk(ctypes.byref(a), _lib.stream_of(scores)), "topk")
+
+
+def topk_any_batch(scores, fine_lens, members, rt, nt, selected, lens, takes, physical, logical, raw, window, mask,
+                   expanded, physical_output, bucket_from_rank, fine_table, direct_fine):
+    """module().topk for batches of any size.  The reference's fused kernel
+    takes more than 512 rows (v1_query.cuh:203) and smaller batches run
+    mask_fine -> topk_transform_512_v2 -> output_ids (runtime.py:549-634).
+    With mask on, members-derived buckets (bucket_from_rank off), fine_lens
+    equal to each row's candidate count, selected ranks inside rt and each
+    fine page's members inside one 1024-token bucket (as the index build
+    makes them), this call gives that chain's raw / logical / physical
+    outputs, in one launch pair (segments, merge) instead of three kernels
+    and a masked-score round trip."""
+    module()._topk(scores, fine_lens, members, rt, nt, selected, lens, takes, physical, logical, raw, window, mask,
+                   expanded, physical_output, bucket_from_rank, fine_table, direct_fine, min_batch=1)
 
 
 @functools.lru_cache(maxsize=None)

@@ -8,6 +8,8 @@ k / s_k come from 8448-byte native pages ([64, 1, 132] byte view: 64x128 FP8
 then 64 fp32 scales) through block_table[r, j // 64].  A block table with row
 stride 0 (e.g. `table[None].expand(rows, -1)`) marks rows that share one
 table; they are tiled together so each key page is staged once per 8 rows.
+Per-row tables of more than 512 rows (a prefill chunk's fine tables) are
+planned per 8-row group over the union of their pages, staged the same way.
 """
 import ctypes
 
@@ -53,7 +55,11 @@ def fp8_paged_mqa_logits(q, kv_cache, weights, context_lens, block_table, schedu
         out = torch.empty((rows, max_context_len), dtype=torch.float32, device=q.device)
     elif out.dtype != torch.float32 or out.shape[0] != rows or out.shape[1] < max_context_len or out.stride(1) != 1:
         raise ValueError("out must be float32 [rows, >= max_context_len]")
-    ws, ws_bytes = workspace(q.device, _lib.lib().v1_score_workspace(rows, int(max_context_len)), "score")
+    # shared tables need the workspace; per-row tables of large batches use
+    # it for the page-union plan (0 bytes: each row on its own)
+    need = (_lib.lib().v1_score_workspace(rows, int(max_context_len)) if block_table.stride(0) == 0
+            else _lib.lib().v1_score_tables_workspace(rows, int(max_context_len)))
+    ws, ws_bytes = workspace(q.device, need, "score")
     a = _lib.ScoreArgs(_lib.ptr(q), _lib.ptr(kv), kv.numel() // PAGE_BYTES, _lib.ptr(weights), _lib.ptr(lens),
                        _lib.ptr(block_table), block_table.stride(0), block_table.shape[1], _lib.ptr(out), out.stride(0),
                        int(max_context_len), rows, heads, int(bool(relu)), int(bool(clean_logits)), ws, ws_bytes)

@@ -351,10 +351,13 @@ def setup_gather(P, dev, torch, np):
 
 def setup_decode(P, dev, torch, np):
     """Configuration 5: decode batch through the V1 route path
-    (runtime.py:417-634 for <= 512 rows): center score -> fused route ->
-    fine_table_shared -> stage_tail_shared -> fine score -> mask_fine ->
-    topk_transform_512_v2 -> output_ids -> gather.  The full-scoring chain over
-    every context key (score -> Top-2048 -> gather) is timed beside it."""
+    (runtime.py:417-634): center score -> route with the fine-table fill ->
+    stage_tail_shared -> fine score -> fused Top-2048 (sink/tail mask in the
+    segment pass, raw -> logical -> physical map in the merge) -> gather.
+    Beside it: the reference's own order for <= 512 rows (fine_table_shared,
+    then mask_fine -> topk_transform_512_v2 -> output_ids as separate
+    kernels; the same outputs) and the full-scoring chain over every context
+    key (score -> Top-2048 -> gather)."""
     wl = P.workloads.config5_route()
     a, prm = wl.arrays, wl.params
     rows, heads, T, rb = prm["rows"], prm["heads"], prm["topk"], prm["row_bytes"]
@@ -377,24 +380,36 @@ def setup_decode(P, dev, torch, np):
     work = torch.empty((rows, T, rb), device=dev, dtype=torch.uint8)
     fused = P.query_fused.module()
     K = P.kernels
+    no_exp = torch.empty((rows, 0), device=dev, dtype=torch.int32)
     stages = [
         ("coarse", lambda: P.scoring.fp8_paged_mqa_logits(q, d["centers"], d["w"], center_lens, d["center_table"],
                                                            None, PG * 8, clean_logits=True, out=coarse)),
-        ("route", lambda: fused.route(coarse, d["lens"], takes, sel, PG, d["rt"], ft, tail_rows, CAP, False)),
-        ("table", lambda: K.fine_table_shared[(rows,)](d["rt"], sel, takes, d["lens"], ft, tail_rows, CAP, PG, TAKE,
-                                                       FP, 68, 1 << (FP - 1).bit_length())),
+        ("route", lambda: fused.route(coarse, d["lens"], takes, sel, PG, d["rt"], ft, tail_rows, CAP, True)),
         ("stage", lambda: K.stage_tail_shared[(rows, 68)](d["native"], None, d["nt"], d["lens"], d["fine"], None,
                                                           tail_rows, CAP, PG, 68, SINK, WIN, ROWS=rows, GROUP=1)),
         ("score", lambda: P.scoring.fp8_paged_mqa_logits(q, d["fine"], d["w"], dg_lens, ft, None, WIDTH,
                                                           clean_logits=True, out=scores)),
-        ("mask", lambda: K.mask_fine[(rows, -(-WIDTH // 256))](scores, sel, d["rt"], d["members"], d["lens"], takes,
-                                                               PG, TAKE, WIDTH, WIDTH, SINK, WIN)),
-        ("topk", lambda: P.topk.topk_transform_512_v2(scores, fl, ident, transformed, 64, None, raw)),
-        ("map", lambda: K.output_ids[(rows, -(-T // 256))](raw, scores, d["members"], d["rt"], d["nt"], sel,
-                                                           d["lens"], takes, out, logical, ft, PG, PG, TAKE, WIDTH, T,
-                                                           SINK, WIN, MAP_PHYSICAL=True, DIRECT_FINE=False, FP=FP)),
+        ("topk", lambda: P.query_fused.topk_any_batch(scores, fl, d["members"], d["rt"], d["nt"], sel, d["lens"],
+                                                      takes, out, logical, raw, WIN, True, no_exp, True, False, ft,
+                                                      False)),
         ("gather", lambda: P.native_kernels.gather_rows(latent, out, work)),
     ]
+
+    def unfused_chain():
+        # the reference's order for <= 512 rows (runtime.py:445-448, 478-509, 538-563, 603-634)
+        stages[0][1]()
+        fused.route(coarse, d["lens"], takes, sel, PG, d["rt"], ft, tail_rows, CAP, False)
+        K.fine_table_shared[(rows,)](d["rt"], sel, takes, d["lens"], ft, tail_rows, CAP, PG, TAKE, FP, 68,
+                                     1 << (FP - 1).bit_length())
+        stages[2][1]()
+        stages[3][1]()
+        K.mask_fine[(rows, -(-WIDTH // 256))](scores, sel, d["rt"], d["members"], d["lens"], takes, PG, TAKE, WIDTH,
+                                              WIDTH, SINK, WIN)
+        P.topk.topk_transform_512_v2(scores, fl, ident, transformed, 64, None, raw)
+        K.output_ids[(rows, -(-T // 256))](raw, scores, d["members"], d["rt"], d["nt"], sel, d["lens"], takes, out,
+                                           logical, ft, PG, PG, TAKE, WIDTH, T, SINK, WIN, MAP_PHYSICAL=True,
+                                           DIRECT_FINE=False, FP=FP)
+        stages[5][1]()
     meta_h = [x.cpu().numpy().astype(np.int64) for x in (fl, takes, center_lens, tail_rows)]
     F, TK_, CL, owners = meta_h[0], meta_h[1], meta_h[2], meta_h[3]
     n = a["lens"].astype(np.int64)
@@ -406,13 +421,13 @@ def setup_decode(P, dev, torch, np):
         # HBM-bound stages: algorithmic bytes from the per-row lengths
         "coarse": ((132.0 * CL.sum() + rows * heads * 132.0 + 4.0 * rows * PG * 8) / 1e9, "GB/s", PEAK_HBM_GBS,
                    "hbm"),
-        "route": ((32.0 * built.sum() + 4.0 * rows * TAKE) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
-        "table": ((8.0 * rows * FP) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        # route: center maxima read, selected ranks and the fine table written
+        "route": ((32.0 * built.sum() + 4.0 * rows * TAKE + 4.0 * rows * FP) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
         "stage": ((2.0 * 8448 * staged_pages.sum()) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
         "score": ((132.0 * F.sum() + rows * heads * 132.0 + 4.0 * rows * WIDTH) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
-        "mask": ((4.0 * (TK_ * 64).sum() + 4.0 * rows * WIDTH) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
-        "topk": ((4.0 * F.sum() + 8.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
-        "map": ((28.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
+        # Top-K: every candidate read once, three output arrays written (the
+        # map's table and member reads ride along, 4 B each per output)
+        "topk": ((4.0 * F.sum() + 12.0 * rows * T + 12.0 * rows * T) / 1e9, "GB/s", PEAK_HBM_GBS, "hbm"),
         "gather": (lambda: _gather_gb(torch, out, rb, latent.shape[0]), "GB/s", PEAK_HBM_GBS, "hbm"),
     }
 
@@ -438,7 +453,8 @@ def setup_decode(P, dev, torch, np):
                         "tables in a 2M-token pool, V1 route path (page_fraction 0.5, fine widths up to 67K), "
                         "Top-2048, 656-byte row gather",
             "global_batch": rows, "seq_len": WIDTH, "parallelism": "single GPU",
-            "_extra": [("full_scoring_chain", full_chain,
+            "_extra": [("unfused_route_chain", unfused_chain, (float(rows), "queries/s", None, None)),
+                       ("full_scoring_chain", full_chain,
                         (lambda: (132.0 * n.sum() + 4.0 * 2 * n.sum() + rows * T * (8.0 + rb * 2)) / 1e9, "GB/s",
                          PEAK_HBM_GBS, "hbm"))]}
     return rows, stages, work_units, cpu, meta, "synthetic (PCG64 seed 5)"
@@ -786,7 +802,8 @@ def run(config, steps, warmup, cpu_budget, P, dev, torch, np):
         ms = a0.elapsed_time(a1) / steps
         amount = unit[0]() if callable(unit[0]) else unit[0]
         alternatives[name] = {"ms": round(ms, 4), "achieved": round(amount / (ms / 1e3), 1), "unit": unit[1],
-                              "bound": unit[3], "frac": round(amount / (ms / 1e3) / unit[2], 4)}
+                              "bound": unit[3],
+                              "frac": None if unit[2] is None else round(amount / (ms / 1e3) / unit[2], 4)}
 
     stage_info = {}
     work_units = {n: ((u[0]() if callable(u[0]) else u[0]),) + tuple(u[1:]) for n, u in work_units.items()}

@@ -166,7 +166,8 @@ typedef struct {
     int32_t heads;               /* 1..64 */
     int32_t relu;                /* 1: DSA ReLU rule; 0: signed scores */
     int32_t clean_logits;
-    void* workspace;             /* >= v1_score_workspace(rows, max_context_len) bytes (shared tables) */
+    void* workspace;             /* shared tables: >= v1_score_workspace(rows, max_context_len) bytes;
+                                    per-row tables: optional, see v1_score_tables_workspace */
     int64_t workspace_bytes;
 } v1_score_args;
 /* Workspace of the shared-table path: per-query records, a work counter and,
@@ -174,6 +175,14 @@ typedef struct {
  * fast value is within rounding of zero get the direct ReLU sum, so keys with
  * no positive head dot score exactly 0, as kernels.py:310-313 gives). */
 int64_t v1_score_workspace(int32_t rows, int32_t max_context_len);
+/* Per-row block tables (block_table_stride != 0) of more than 512 rows with
+ * max_context_len <= 65536: given a 256-byte aligned workspace of at least
+ * this many bytes (0 when the shape does not qualify), v1_score plans each
+ * group of 8 rows over the union of their table pages and stages every page
+ * once for the group (the rows of one prefill chunk share most pages, as the
+ * fine tables of runtime.py:538-548 do); groups sharing less than two rows
+ * per page, and calls without the workspace, score each row on its own. */
+int64_t v1_score_tables_workspace(int32_t rows, int32_t max_context_len);
 int v1_score(const v1_score_args* a, void* stream);
 /* v1_score without a caller workspace and without any allocation: the
  * shared-table path's scratch is a static 16 MiB device array per GPU

@@ -83,6 +83,11 @@ def test_workspace_sizes_are_host_arithmetic(lib):
     assert h.v1_topk_workspace(4096, 65536, 2048) == 4096 * 2 * (2048 * 8 + 4)
     assert h.v1_topk_workspace(128, 131072, 2048) == 128 * 4 * (2048 * 8 + 4)
     assert h.v1_score_workspace(4096, 32768) >= 4096 * (8 * 128 + 8 * 4 + 16 * 4)
+    # per-row tables: the page-union plan only for more than 512 rows of at most 65536 columns
+    assert h.v1_score_tables_workspace(512, 34880) == 0
+    assert h.v1_score_tables_workspace(1024, 65537) == 0
+    need = h.v1_score_tables_workspace(1024, 34880)
+    assert need >= h.v1_score_workspace(1024, 34880) + 128 * 8 * 545 * (4 + 4 + 32) and need % 256 == 0
 
 
 def test_sort_rejects_bad_group_size(lib):

@@ -1,0 +1,159 @@
+"""Per-row block tables of large batches through the page-union plan.
+
+Batches of more than 512 rows with per-row tables (the fine tables of a
+prefill chunk, sglang/srt/layers/attention/v1_deepseek/runtime.py:538-548)
+are scored per group of 8 rows over the union of the rows' table pages (17
+to 48 heads, when the rows share enough of their pages).  The
+result must be the formula of kernels.py:310-313 through each row's own table,
+whatever the tables hold: partly overlapping page sets in each row's own
+order, unequal lengths (empty rows, rows past their table), a page listed
+twice by one row, entries that are -1 or past the pool (their keys read as
+zeros and score 0, as the per-row kernel gives), and groups that share too
+little (scored row by row).  The reference maps every invalid entry and every
+slot past the table to an all-zero page appended to the pool."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import pkg
+from oracle import v1 as O
+from test_gpu_kernels import H, T, assert_scores_close, assert_scores_rel
+
+pytestmark = pytest.mark.gpu
+
+SC = pkg("scoring")
+W = pkg("workloads")
+
+
+def _queries(g, rows, heads, live):
+    """FP8 queries and weights >= 0; heads past `live` are zero (few live
+    heads put many keys on the ReLU zero plateau)."""
+    q8l, sq = W.quantize_rows(g.standard_normal((rows * live, 128), dtype=np.float32))
+    q8 = np.zeros((rows, heads, 128), np.uint8)
+    q8[:, :live] = q8l.reshape(rows, live, 128)
+    w = np.zeros((rows, heads), np.float32)
+    w[:, :live] = (sq.reshape(rows, live) * g.random((rows, live), dtype=np.float32)).astype(np.float32)
+    return q8, w
+
+
+def _tables(g, rows, pool_pages, shared_pages, take, private, unrelated_rows=()):
+    """Each row lists `take` of the chunk's `shared_pages` pages in its own
+    order, then `private` pages of its own; rows in `unrelated_rows` list
+    random pool pages instead.  A few rows list a page twice, a few entries
+    are -1 or past the pool."""
+    chunk = g.permutation(pool_pages)[:shared_pages]
+    blocks = take + private
+    table = np.empty((rows, blocks), np.int32)
+    for r in range(rows):
+        if r in unrelated_rows:
+            table[r] = g.integers(0, pool_pages, blocks)
+        else:
+            table[r, :take] = chunk[g.permutation(shared_pages)[:take]]
+            table[r, take:] = g.integers(0, pool_pages, private)
+    dup = g.random(rows) < 0.05
+    for r in np.nonzero(dup)[0]:
+        a, b = g.choice(blocks, 2, replace=False)
+        table[r, b] = table[r, a]
+    table[g.random((rows, blocks)) < 0.02] = -1
+    table[g.random((rows, blocks)) < 0.01] = pool_pages + 5
+    return table
+
+
+def _padded(native, table, width):
+    """The pool with an all-zero page appended, and the table with every
+    invalid entry and every slot past it (up to width) pointing there."""
+    pool_pages = native.shape[0]
+    pool = np.concatenate([native, np.zeros((1, native.shape[1]), np.uint8)])
+    tab = np.full((table.shape[0], max(-(-width // 64), table.shape[1])), pool_pages, np.int32)
+    tab[:, :table.shape[1]] = np.where((table >= 0) & (table < pool_pages), table, pool_pages)
+    return pool, tab
+
+
+def _certain_zeros(q8, w, pool, tab, lens, width):
+    """Keys whose every live head dot lies below 0 by more than the fp32
+    accumulation allowance 2^-16 * sum_d |q_d k_d|: their ReLU score is exactly
+    0 whatever the summation order (a dot at or just below 0 can come out of
+    an fp32 sum of FP8 products slightly positive, and ReLU keeps it)."""
+    qf = O.e4m3_decode(q8).astype(np.float64)
+    kk = pool[:, :8192].reshape(-1, 64, 128)
+    out = np.zeros((q8.shape[0], width), bool)
+    for r in range(q8.shape[0]):
+        n = min(int(lens[r]), width)
+        if n <= 0:
+            continue
+        j = np.arange(n)
+        k = O.e4m3_decode(kk[tab[r, j // 64], j % 64]).astype(np.float64)
+        live = w[r] != 0
+        d, a = qf[r][live] @ k.T, np.abs(qf[r][live]) @ np.abs(k).T
+        out[r, :n] = (d + 2.0 ** -16 * a <= 0).all(axis=0)
+    return out
+
+
+def _run(dev, q8, w, native, table, lens, width, relu, clean, fill=7.0):
+    rows = q8.shape[0]
+    out = torch.full((rows, width), fill, device=dev)
+    SC.fp8_paged_mqa_logits(T(q8, dev).view(torch.float8_e4m3fn), T(native, dev), T(w, dev), T(lens, dev),
+                            T(table, dev), None, width, clean_logits=clean, relu=relu, out=out)
+    return H(out).astype(np.float64)
+
+
+@pytest.mark.parametrize("rows,heads,live,relu,clean,take,private", [
+    (520, 32, 32, True, True, 44, 0),     # 65 groups sharing almost every page
+    (1031, 32, 4, True, False, 30, 4),    # last group of 7 rows, pages a wave's rows skip, unclean, zero plateau
+    (777, 48, 48, False, True, 30, 4),    # signed scores, 48 heads
+    (560, 64, 64, True, True, 44, 0),     # 64 heads: row by row (the plan takes 17 to 48 heads)
+    (600, 16, 2, True, True, 30, 4),      # one head block: row by row
+    (529, 7, 7, True, True, 30, 4),       # heads not a multiple of 16: row by row
+])
+def test_union_plan_vs_reference(dev, rows, heads, live, relu, clean, take, private):
+    g = np.random.default_rng(rows * 131 + heads)
+    pool_pages, fill = 160, 7.0
+    q8, w = _queries(g, rows, heads, live)
+    if not relu:
+        w *= np.where(g.random(w.shape) < 0.5, -1, 1).astype(np.float32)
+    k8, ks = W.quantize_rows(g.standard_normal((pool_pages * 64, 128), dtype=np.float32))
+    native = W.pack_pages(k8, ks)
+    table = _tables(g, rows, pool_pages, shared_pages=48, take=take, private=private)
+    blocks = table.shape[1]
+    lens = g.integers(1, blocks * 64 + 1, rows).astype(np.int32)
+    lens[g.random(rows) < 0.05] = 0
+    lens[g.random(rows) < 0.05] = blocks * 64 + 90  # past the table: those keys score 0
+    width = blocks * 64 + 128
+    got = _run(dev, q8, w, native, table, lens, width, relu, clean, fill)
+    pool, tab = _padded(native, table, width)
+    ref = O.paged_logits(q8, w, pool, tab, lens, width, relu=relu, clean=clean)
+    bound = O.paged_logits(q8, w, pool, tab, lens, width, magnitude=True, clean=False)
+    if not clean:
+        past = np.arange(width)[None, :] >= lens[:, None]
+        assert (got[past] == fill).all(), "a column past a row's length was written"
+        ref[past] = fill
+    fin = np.isfinite(ref)
+    assert np.array_equal(fin, np.isfinite(got))
+    if relu:
+        zero = fin & (ref == 0) & _certain_zeros(q8, w, pool, tab, lens, width)
+        assert zero.any()
+        assert (got[zero].astype(np.float32).view(np.uint32) == 0).all(), \
+            f"{int((got[zero] != 0).sum())} certain reference zeros scored other than +0.0"
+    if relu and live == heads and live >= 16:
+        assert_scores_rel(got, ref)
+    else:
+        # signed sums and lone live heads cancel: the fp32 accumulation allowance
+        assert_scores_close(got, ref, bound)
+
+
+def test_union_plan_low_sharing_groups_fall_back(dev):
+    """Groups whose rows share too little go to the per-row kernel: a batch
+    whose first 40 groups are a chunk's rows (the plan) and the rest
+    unrelated rows (row by row) gives the reference on every row."""
+    g = np.random.default_rng(77)
+    rows, heads, pool_pages = 640, 32, 400
+    q8, w = _queries(g, rows, heads, heads)
+    k8, ks = W.quantize_rows(g.standard_normal((pool_pages * 64, 128), dtype=np.float32))
+    native = W.pack_pages(k8, ks)
+    table = _tables(g, rows, pool_pages, shared_pages=40, take=28, private=2, unrelated_rows=set(range(320, rows)))
+    blocks = table.shape[1]
+    lens = g.integers(1, blocks * 64 + 1, rows).astype(np.int32)
+    width = blocks * 64
+    got = _run(dev, q8, w, native, table, lens, width, True, True)
+    pool, tab = _padded(native, table, width)
+    assert_scores_rel(got, O.paged_logits(q8, w, pool, tab, lens, width))

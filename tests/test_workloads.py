@@ -364,6 +364,13 @@ def test_config5_route_chain(dev, config5_route):
                                scores.stride(0), TOP, SINK, WIN, True, False, ft_h)
     out_h = H(out)
     assert np.array_equal(out_h, e_out) and np.array_equal(H(logical), e_lg)
+    # the same outputs from the fused Top-K for small batches (mask applied
+    # in the segment pass, map in the merge) on the unmasked fine scores
+    scores2 = SC.fp8_paged_mqa_logits(q, fine_d, d["w"], dg_lens, ft, None, WIDTH, clean_logits=True)
+    phys2, lg2, raw2 = i32(rows, TOP), i32(rows, TOP), i32(rows, TOP)
+    QF.topk_any_batch(scores2, fl, d["members"], d["rt"], d["nt"], sel, d["lens"], takes, phys2, lg2, raw2, WIN, True,
+                      torch.empty((rows, 0), device=dev, dtype=torch.int32), True, False, ft, False)
+    assert np.array_equal(H(raw2), e_raw) and np.array_equal(H(lg2), e_lg) and np.array_equal(H(phys2), e_out)
     # every selected token lies in its request's context, once
     for r in range(rows):
         lg = e_lg[r][e_lg[r] >= 0]
