@@ -59,13 +59,15 @@ __device__ __forceinline__ void step_in_thread(uint64_t (&v)[E], int e0, int k, 
     }
 }
 
+// Every aligned run of `group` (a power of two dividing n) is sorted on its
+// own; group = n sorts the whole set.
 template <int E>
-__device__ void bitonic_desc_regs(uint64_t (&v)[E], int n, uint64_t* buf0, uint64_t* buf1) {
+__device__ void bitonic_desc_regs(uint64_t (&v)[E], int n, uint64_t* buf0, uint64_t* buf1, int group) {
     const int e0 = (int)threadIdx.x * E;
     const bool live = e0 < n;
     int flip = 0;
-    for (int k = 2; k <= n; k <<= 1) {
-        const bool last = k == n;
+    for (int k = 2; k <= group; k <<= 1) {
+        const bool last = k == group;
         for (int j = k >> 1; j > 0; j >>= 1) {
             if (j < E) {
                 if (j == 1) step_in_thread<E, 1>(v, e0, k, last);
@@ -137,7 +139,7 @@ __global__ __launch_bounds__(512) void route_kernel(v1_route_args a, int n_sort)
             v[i] = ((uint64_t)score_key(best) << 32) | (uint32_t)(0xffffffffu - (uint32_t)p);
         }
     }
-    bitonic_desc_regs<E>(v, n_sort, s0, s1);
+    bitonic_desc_regs<E>(v, n_sort, s0, s1, n_sort);
     // selected takes ranks < take_stride; the fine table every rank < take
     // (v1_query.cuh:44-48), bounded by the sorted pages and the table width
     const int32_t ft_ranks = a.fill_table ? min(min(take, a.pages), a.ft_cols) : 0;
@@ -172,6 +174,36 @@ __global__ __launch_bounds__(256) void sort_f32_kernel(const int32_t* perm, int3
         const int32_t g = i / n;
         const int32_t pos = (int32_t)(0xffffffffu - (uint32_t)s[i]);
         out[base + i] = perm[base + (int64_t)g * n + pos];
+    }
+}
+
+// sort_f32_kernel for groups of at most 1024 (the reference's sizes): the
+// block's 1024 slots are held four per thread in registers, so only the steps
+// that pair elements of different waves (j >= 256) go through LDS.
+__global__ __launch_bounds__(256) void sort_f32_regs_kernel(const int32_t* perm, int32_t* out, const float* keys,
+                                                            const int32_t* flag, int32_t n, int32_t groups,
+                                                            int32_t gpb, int64_t head_stride) {
+    constexpr int E = 4;
+    __shared__ uint64_t s0[256 * E], s1[256 * E];
+    if (*flag >= 0) return;
+    const int64_t h = blockIdx.y;
+    const int32_t g0 = blockIdx.x * gpb;
+    const int32_t ng = min(gpb, groups - g0);
+    const int m = ng * n;
+    const int64_t base = h * head_stride + (int64_t)g0 * n;
+    const int e0 = (int)threadIdx.x * E;
+    uint64_t v[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const int p = e0 + i;
+        v[i] = p < m ? ((uint64_t)score_key(keys[base + p]) << 32) | (0xffffffffu - (uint32_t)(p % n)) : 0ull;
+    }
+    // (slots past m form whole groups of their own: they never mix with real ones)
+    bitonic_desc_regs<E>(v, 256 * E, s0, s1, n);
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const int p = e0 + i;
+        if (p < m) out[base + p] = perm[base + (int64_t)(p / n) * n + (int32_t)(0xffffffffu - (uint32_t)v[i])];
     }
 }
 
@@ -245,8 +277,12 @@ extern "C" int v1_sort_f32(const int32_t* perm, int32_t* out, const float* keys,
     V1_REQUIRE(flag != nullptr, "sort: flag required");
     if (groups == 0 || heads == 0) return V1_OK;
     const int gpb = max(1, min(groups, 1024 / n));
-    hipLaunchKernelGGL(sort_f32_kernel, dim3((uint32_t)cdiv(groups, gpb), heads), dim3(256), 0, as_stream(stream),
-                       perm, out, keys, flag, n, groups, gpb, head_stride);
+    if (n <= 1024)
+        hipLaunchKernelGGL(sort_f32_regs_kernel, dim3((uint32_t)cdiv(groups, gpb), heads), dim3(256), 0,
+                           as_stream(stream), perm, out, keys, flag, n, groups, gpb, head_stride);
+    else
+        hipLaunchKernelGGL(sort_f32_kernel, dim3((uint32_t)cdiv(groups, gpb), heads), dim3(256), 0, as_stream(stream),
+                           perm, out, keys, flag, n, groups, gpb, head_stride);
     return V1_LAUNCHED("sort_f32");
 }
 

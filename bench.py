@@ -25,6 +25,10 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
                -> member order, reordered pages and FP8 centers, one launch
   8            attention consumer: 4096 queries x 4 heads of one KV head, 2048 gathered bf16
                K/V slots each (1M-slot pool) -> decode attention
+  10           context timings, microseconds per call under HIP graph replay: _sort of one
+               1024-token bucket at group sizes 1024 .. 16, and the per-lease page manager
+               (fingerprint, match_pages miss / hit / collision at a 4096-page pool, publish
+               all-new / mixed / reuse), set up as the reference's own micro-benchmark
   7            shared sink+tail chunk: 64K published tokens, 4096 causal queries x 32 heads,
                sink 64 / window 2048, 40 history pages per query: one union of sink+tail
                pages -> FP8 score -> canonical order -> Top-2048 -> slots (per-row staging
@@ -109,7 +113,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9])
+    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--with", dest="with_configs", default=None, metavar="LIST",
                     help="comma-separated further configs measured after the main one and reported under "
@@ -839,6 +843,104 @@ def run(config, steps, warmup, cpu_budget, P, dev, torch, np):
     return line
 
 
+# The reference's per-kernel graph timings on H20-3e (experiments/v1_kernel_opt_20261022/
+# RESULTS.md:75-81, 105-111), reported beside this build's as context.
+REFERENCE_H20_US = {
+    "sort_1024": 10.769, "sort_512": 3.638, "sort_256": 2.548, "sort_128": 2.212, "sort_64": 1.942,
+    "sort_32": 1.738, "sort_16": 1.696, "fingerprint": 3.194, "match_miss": 2.384, "match_hit": 4.281,
+    "match_collision": 5.987, "publish_all_new": 3.484, "publish_mixed": 3.457, "publish_reuse": 1.610,
+}
+
+
+def micro_timings(P, dev, torch, reps=20, replays=50):
+    """Configuration 10: per-call times of the grouping sort and the per-lease
+    page manager under HIP graph replay, with the setups of the reference's
+    micro-benchmark (experiments/v1_kernel_opt_20261022/bench_pages.py:5-40:
+    16 temp pages, a 4096-page pool, miss / hit / collision and all-new /
+    mixed / reuse).  Each graph holds `reps` calls and is replayed `replays`
+    times; the result is microseconds per call."""
+    FG = importlib.import_module("10_20_amd.fused_grouping")
+    K = P.kernels
+    g = torch.Generator(device=dev).manual_seed(77)
+
+    def graph_us(fn):
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            graph.replay()
+        e1.record()
+        e1.synchronize()
+        return round(e0.elapsed_time(e1) * 1e3 / (replays * reps), 3)
+
+    out = {}
+    # _sort of one bucket's 1024 scores in groups of N (fused_grouping.py:64-76)
+    perm = torch.arange(1024, device=dev, dtype=torch.int32)
+    dst = torch.empty_like(perm)
+    scores = torch.randn(1024, device=dev, generator=g)
+    flag = torch.full((1,), -1, device=dev, dtype=torch.int32)
+    for n in (1024, 512, 256, 128, 64, 32, 16):
+        out[f"sort_{n}"] = graph_us(lambda n=n: FG._sort[(1024 // n, 1)](perm, dst, scores, flag, n))
+    # page manager at a 4096-page pool
+    cap = 4096
+    tmp = torch.randint(0, 256, (16, 8448), device=dev, dtype=torch.uint8, generator=g)
+    mp = torch.randint(-1, 262144, (16, 64), device=dev, dtype=torch.int32, generator=g)
+    meta = torch.tensor([4096, 1, 1], device=dev, dtype=torch.int32)
+    h = torch.empty((16, 2), device=dev, dtype=torch.int64)
+    out["fingerprint"] = graph_us(lambda: K.fingerprint[(16,)](tmp, mp, meta, h))
+    fine = torch.randint(0, 256, (cap, 8448), device=dev, dtype=torch.uint8, generator=g)
+    members = torch.zeros((cap, 64), device=dev, dtype=torch.int32)
+    hashes = torch.zeros((cap, 2), device=dev, dtype=torch.int64)
+    refs = torch.zeros(cap, device=dev, dtype=torch.int32)
+    match = torch.empty(16, device=dev, dtype=torch.int32)
+    for mode in ("miss", "hit", "collision"):
+        refs.zero_()
+        hashes.zero_()
+        if mode != "miss":
+            fine[1:17].copy_(tmp)
+            members[1:17].copy_(mp)
+            hashes[1:17].copy_(h)
+            refs[1:17] = 1
+        if mode == "collision":
+            fine[0].copy_(tmp[0])
+            fine[0, 0] ^= 1
+            members[0].copy_(mp[0])
+            hashes[0].copy_(h[0])
+            refs[0] = 1
+        out[f"match_{mode}"] = graph_us(
+            lambda: K.match_pages[(16,)](tmp, mp, h, meta, fine, members, hashes, refs, match, cap))
+        expect = [-1] * 16 if mode == "miss" else list(range(1, 17))
+        if match.tolist() != expect:
+            raise RuntimeError(f"match_pages {mode}: {match.tolist()}")
+    tc = torch.randint(0, 256, (2, 8448), device=dev, dtype=torch.uint8, generator=g)
+    tab = torch.zeros((2, 16), device=dev, dtype=torch.int32)
+    tab[1] = torch.arange(1, 17, device=dev, dtype=torch.int32)
+    new = torch.ones(16, device=dev, dtype=torch.bool)
+    f = torch.full_like(fine, 19)
+    c = torch.full((4, 8448), 19, device=dev, dtype=torch.uint8)
+    m = torch.full_like(members, -99)
+    hh = torch.full_like(hashes, -99)
+    for mode in ("all_new", "mixed", "reuse"):
+        new.fill_(mode != "reuse")
+        if mode == "mixed":
+            new[::2] = False
+        out[f"publish_{mode}"] = graph_us(
+            lambda: K.publish[(16,)](tmp, tc, tc.view(torch.float32), mp, h, meta, tab, new, f, c,
+                                     c.view(torch.float32), m, hh))
+    return out
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -856,6 +958,14 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     P = Pkg()
+    if args.config == 10:
+        us = micro_timings(P, dev, torch)
+        print(json.dumps({"metric": "microseconds per call under HIP graph replay (context timings)", "value": None,
+                          "unit": "us", "n_gpus": 1, "higher_is_better": False, "data": "synthetic (seed 77)",
+                          "config": {"workload": "one bucket's _sort at group sizes 1024..16; fingerprint, "
+                                                 "match_pages and publish of one 16-page lease at a 4096-page pool"},
+                          "timings_us": us, "reference_h20_us": REFERENCE_H20_US}), flush=True)
+        return
     rec = run(args.config, args.steps, args.warmup, args.cpu_budget, P, dev, torch, np)
     line = {"metric": rec.pop("metric"), "value": rec.pop("value"), "unit": rec.pop("unit"), "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": rec.pop("ms_per_step"),
