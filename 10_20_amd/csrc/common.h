@@ -106,6 +106,74 @@ inline uint32_t small_div_magic(uint32_t d) {
     return (uint32_t)((((uint64_t)1 << 32) + d - 1) / d);
 }
 
+// Descending bitonic network over n 64-bit composites (unique keys give a
+// strict order) held in registers: thread t holds
+// elements t*E .. t*E+E-1 (threads at or past n / E hold none and only join
+// the barriers).  Pairs (e, e ^ j) inside a thread swap registers, pairs
+// inside a wave meet through lane shuffles, and pairs across waves through
+// LDS, two buffers used in turn with one barrier per such step: of the 66
+// steps of a 2048-key network, 6 cross waves.
+__device__ __forceinline__ uint64_t bitonic_keep(uint64_t a, uint64_t b, bool keep_max) {
+    return keep_max ? (a > b ? a : b) : (a > b ? b : a);
+}
+
+template <int E, int J>
+__device__ __forceinline__ void step_in_thread(uint64_t (&v)[E], int e0, int k, bool last) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        if ((i & J) == 0) {
+            const bool desc = last || (((e0 + i) & k) == 0);
+            const uint64_t a = v[i], b = v[i + J];
+            v[i] = bitonic_keep(a, b, desc);
+            v[i + J] = bitonic_keep(a, b, !desc);
+        }
+    }
+}
+
+// Every aligned run of `group` (a power of two dividing n) is sorted on its
+// own; group = n sorts the whole set.
+template <int E>
+__device__ __forceinline__ void bitonic_desc_regs(uint64_t (&v)[E], int n, uint64_t* buf0, uint64_t* buf1, int group) {
+    const int e0 = (int)threadIdx.x * E;
+    const bool live = e0 < n;
+    int flip = 0;
+    for (int k = 2; k <= group; k <<= 1) {
+        const bool last = k == group;
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            if (j < E) {
+                if (j == 1) step_in_thread<E, 1>(v, e0, k, last);
+                if (E > 2 && j == 2) step_in_thread<E, (E > 2 ? 2 : 1)>(v, e0, k, last);
+                if (E > 4 && j == 4) step_in_thread<E, (E > 4 ? 4 : 1)>(v, e0, k, last);
+                if (E > 8 && j == 8) step_in_thread<E, (E > 8 ? 8 : 1)>(v, e0, k, last);
+            } else if (j / E < kWave) {
+                const int d = j / E;
+#pragma unroll
+                for (int i = 0; i < E; ++i) {
+                    const int e = e0 + i;
+                    const uint64_t a = v[i];
+                    const uint32_t blo = (uint32_t)__shfl_xor((int)(uint32_t)a, d, kWave);
+                    const uint32_t bhi = (uint32_t)__shfl_xor((int)(uint32_t)(a >> 32), d, kWave);
+                    const uint64_t b = ((uint64_t)bhi << 32) | blo;
+                    v[i] = bitonic_keep(a, b, ((e & j) == 0) == (last || (e & k) == 0));
+                }
+            } else {
+                uint64_t* w = flip ? buf1 : buf0;
+                flip ^= 1;
+                if (live)
+#pragma unroll
+                    for (int i = 0; i < E; ++i) w[e0 + i] = v[i];
+                __syncthreads();
+                if (live)
+#pragma unroll
+                    for (int i = 0; i < E; ++i) {
+                        const int e = e0 + i;
+                        v[i] = bitonic_keep(v[i], w[e ^ j], ((e & j) == 0) == (last || (e & k) == 0));
+                    }
+            }
+        }
+    }
+}
+
 // OCP e4m3fn byte -> float (exact; codes 0x7f / 0xff, NaN in the format, read
 // as +-480, which no encoder here produces).
 __device__ __forceinline__ float e4m3_value(uint32_t c) {

@@ -1003,13 +1003,12 @@ __global__ __launch_bounds__(256) void score_exact(ScoreParams p) {
 constexpr int kUnionEntries = 8192;  // (row, slot) pairs of a group: 8 rows x 1024 table pages
 static_assert(kUnionEntries < 0xffff, "union slots fit 16 bits");
 constexpr int kPlanThreads = 512;
-constexpr int kPlanPer = kUnionEntries / kPlanThreads;  // pairs per thread
-// LDS of the plan (dynamic, sized by the call's largest group): keys (8 B),
-// run counts (4 B) and entry masks (4 B) per pair.
-inline int64_t plan_lds_bytes(int32_t max_pairs) {
-    int64_t n = 2;
+// Pairs the plan sorts per group: the smallest power of two, at least one per
+// thread, that holds every group's pairs; its dynamic LDS is 16 bytes a pair.
+inline int32_t plan_pairs(int32_t max_pairs) {
+    int32_t n = kPlanThreads;
     while (n < max_pairs) n <<= 1;
-    return 16 * n;
+    return n;
 }
 constexpr int kUnionMinRows = 513;   // decode batches (the reference's <= 512 rows) keep score_rows
 constexpr uint32_t kNoPage = 0x7fffffffu;
@@ -1050,11 +1049,13 @@ __device__ __forceinline__ int32_t plan_scan(int32_t v, int32_t* part, int32_t& 
     return kOp == 0 ? before + wave_excl : max(before, wave_excl);
 }
 
-__global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, UnionOut u, int32_t lds_pairs) {
+// EP: pairs per thread; the call's groups have at most N = EP * kPlanThreads
+// (row, slot) pairs.  Dynamic LDS: 2N words of 8 bytes (the sort's two
+// buffers; then the run counts, entry masks and the sorted keys).
+template <int EP>
+__global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, UnionOut u) {
+    constexpr int N = EP * kPlanThreads;
     extern __shared__ __attribute__((aligned(16))) uint64_t plan_lds[];
-    uint64_t* key = plan_lds;                                        // [lds_pairs]
-    int32_t* run = reinterpret_cast<int32_t*>(plan_lds + lds_pairs);  // per page run: its entries, then its first
-    uint32_t* umask = reinterpret_cast<uint32_t*>(run + lds_pairs);   // per entry: the rows listing it
     __shared__ int32_t part[kPlanThreads / kWave];
     const int t = threadIdx.x;
     const int32_t g = blockIdx.x;
@@ -1069,93 +1070,93 @@ __global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, 
         const int32_t c = q < grows ? min(p.ctx[row0 + q], p.max_context_len) : 0;
         off[q + 1] = off[q] + (max(c, 0) + 63) / 64;
     }
-    const int32_t E = off[kQueriesPerGroup];  // <= kUnionEntries (8 * table pages of max_context_len)
-    int32_t N = 2;
-    while (N < E) N <<= 1;
-    for (int32_t e = t; e < N; e += kPlanThreads) {
-        uint64_t k = ~0ull;
+    const int32_t E = off[kQueriesPerGroup];  // <= N
+    // pair e of thread t's run: ((page + 1) << 32) | (row << 24) | slot, page
+    // kNoPage for slots past the table or out of the pool; padding is 0 and
+    // sorts last
+    uint64_t v[EP];
+#pragma unroll
+    for (int i = 0; i < EP; ++i) {
+        const int32_t e = t * EP + i;
+        v[i] = 0ull;
         if (e < E) {
             int q = 0;
 #pragma unroll
             for (int j = 1; j < kQueriesPerGroup; ++j) q += e >= off[j] ? 1 : 0;
             const int32_t slot = e - off[q];
             const int32_t page = page_of(p, row0 + q, slot);
-            k = ((uint64_t)(page >= 0 ? (uint32_t)page : kNoPage) << 32) | ((uint64_t)q << 24) | (uint32_t)slot;
-            run[e] = 0;
-            umask[e] = 0u;
+            v[i] = ((uint64_t)((page >= 0 ? (uint32_t)page : kNoPage) + 1u) << 32) | ((uint64_t)q << 24) |
+                   (uint32_t)slot;
         }
-        key[e] = k;
+    }
+    // descending sort, in registers (LDS for the steps across waves)
+    bitonic_desc_regs<EP>(v, N, plan_lds, plan_lds + N, N);
+    __syncthreads();  // the sort's buffers are free
+    int32_t* run = reinterpret_cast<int32_t*>(plan_lds);        // per page run: its entries, then its first
+    uint32_t* umask = reinterpret_cast<uint32_t*>(run + N);      // per entry: the rows listing it
+    uint64_t* sorted = plan_lds + N;                             // the sorted pairs
+#pragma unroll
+    for (int i = 0; i < EP; ++i) {
+        sorted[t * EP + i] = v[i];
+        run[t * EP + i] = 0;
+        umask[t * EP + i] = 0u;
     }
     __syncthreads();
-    // ascending bitonic sort of the N keys
-    for (int32_t k = 2; k <= N; k <<= 1) {
-        for (int32_t j = k >> 1; j > 0; j >>= 1) {
-            for (int32_t i = t; i < N / 2; i += kPlanThreads) {
-                const int32_t a = ((i & ~(j - 1)) << 1) | (i & (j - 1)), b = a + j;
-                const uint64_t x = key[a], y = key[b];
-                if ((x > y) == ((a & k) == 0)) {
-                    key[a] = y;
-                    key[b] = x;
-                }
-            }
-            __syncthreads();
-        }
-    }
-    // thread t owns pairs [t * c, t * c + c)
-    const int32_t c = (E + kPlanThreads - 1) / kPlanThreads;
-    int32_t P[kPlanPer], Q[kPlanPer], S[kPlanPer], R[kPlanPer], K[kPlanPer];
+    // runs: a page starts where the page field changes, a (page, row) run
+    // where either changes; a pair's occurrence is its distance from the
+    // start of its (page, row) run
+    int32_t P[EP], Q[EP], S[EP], R[EP], K[EP];
     int32_t nstart = 0, last = -1;
 #pragma unroll
-    for (int j = 0; j < kPlanPer; ++j) {
-        const int32_t i = t * c + j;
+    for (int j = 0; j < EP; ++j) {
+        const int32_t i = t * EP + j;
         P[j] = -1;
-        if (j < c && i < E) {
-            const uint64_t x = key[i], y = i > 0 ? key[i - 1] : ~0ull;
-            P[j] = (int32_t)(x >> 32);
+        if (i < E) {
+            const uint64_t x = v[j], y = j > 0 ? v[j - 1] : (i > 0 ? sorted[i - 1] : ~0ull);
+            P[j] = (int32_t)((uint32_t)(x >> 32) - 1u);
             Q[j] = (int32_t)((x >> 24) & 0xff);
             S[j] = (int32_t)(x & 0xffffff);
             const bool ps = i == 0 || (x >> 32) != (y >> 32);
             const bool pqs = ps || ((x >> 24) & 0xff) != ((y >> 24) & 0xff);
             nstart += ps ? 1 : 0;
-            R[j] = nstart;  // page starts up to here within the chunk
+            R[j] = nstart;  // page starts up to here within the thread's run
             if (pqs) last = i;
-            K[j] = last;    // last (page, row) start up to here within the chunk
+            K[j] = last;    // last (page, row) start up to here within the run
         }
     }
     int32_t runs, dummy;
     const int32_t run_before = plan_scan<0>(nstart, part, runs);
     const int32_t last_before = plan_scan<1>(last, part, dummy);
 #pragma unroll
-    for (int j = 0; j < kPlanPer; ++j) {
+    for (int j = 0; j < EP; ++j) {
         if (P[j] == -1) continue;
-        const int32_t i = t * c + j;
+        const int32_t i = t * EP + j;
         R[j] += run_before - 1;                        // page run of the pair
         K[j] = i - max(K[j], last_before);             // its occurrence among the row's slots of the page
         atomicMax(&run[R[j]], K[j] + 1);
     }
     __syncthreads();
     // entries per run -> first entry per run (exclusive sum over the runs)
-    int32_t cnt[kPlanPer];
+    int32_t cnt[EP];
     int32_t local = 0;
 #pragma unroll
-    for (int j = 0; j < kPlanPer; ++j) {
-        const int32_t r = t * c + j;
-        cnt[j] = (j < c && r < runs) ? run[r] : 0;
+    for (int j = 0; j < EP; ++j) {
+        const int32_t r = t * EP + j;
+        cnt[j] = r < runs ? run[r] : 0;
         local += cnt[j];
     }
     int32_t U;
     int32_t first = plan_scan<0>(local, part, U);
 #pragma unroll
-    for (int j = 0; j < kPlanPer; ++j) {
-        const int32_t r = t * c + j;
-        if (j < c && r < runs) run[r] = first;
+    for (int j = 0; j < EP; ++j) {
+        const int32_t r = t * EP + j;
+        if (r < runs) run[r] = first;
         first += cnt[j];
     }
     __syncthreads();
-    // two or more rows per union page on average
     const bool shared = 2 * U <= E;
 #pragma unroll
-    for (int j = 0; j < kPlanPer; ++j) {
+    for (int j = 0; j < EP; ++j) {
         if (P[j] == -1 || !shared) continue;
         const int32_t e = run[R[j]] + K[j];
         u.slots[(gbase + e) * kQueriesPerGroup + Q[j]] = S[j];
@@ -1545,19 +1546,30 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
                            (int32_t)kUnionLevels);
         int rc = V1_LAUNCHED("score_prep");
         if (rc != V1_OK) return rc;
-        const int32_t max_pairs = (int32_t)(kQueriesPerGroup * cdiv(a->max_context_len, 64));
-        const int32_t lds_pairs = (int32_t)(plan_lds_bytes(max_pairs) / 16);
-        // (dynamic LDS past 64 KiB is allowed once per process)
+        const int32_t npairs = plan_pairs((int32_t)(kQueriesPerGroup * cdiv(a->max_context_len, 64)));
+        // (dynamic LDS past 64 KiB is allowed once per process and instance)
         static std::once_flag lds_once;
         static hipError_t lds_err = hipSuccess;
         std::call_once(lds_once, [] {
-            lds_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&score_union_plan),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          (int)plan_lds_bytes(kUnionEntries));
+            const void* fns[] = {reinterpret_cast<const void*>(&score_union_plan<1>),
+                                 reinterpret_cast<const void*>(&score_union_plan<2>),
+                                 reinterpret_cast<const void*>(&score_union_plan<4>),
+                                 reinterpret_cast<const void*>(&score_union_plan<8>),
+                                 reinterpret_cast<const void*>(&score_union_plan<16>)};
+            for (const void* f : fns)
+                if (lds_err == hipSuccess)
+                    lds_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 16 * kUnionEntries);
         });
         if (lds_err != hipSuccess) return hip_status(lds_err, "score: hipFuncSetAttribute(score_union_plan)");
-        hipLaunchKernelGGL(score_union_plan, dim3((uint32_t)groups), dim3(kPlanThreads), plan_lds_bytes(max_pairs), st,
-                           p, u, lds_pairs);
+        const dim3 pg((uint32_t)groups), pb(kPlanThreads);
+        const size_t lds = 16 * (size_t)npairs;
+        switch (npairs / kPlanThreads) {
+            case 1: hipLaunchKernelGGL(score_union_plan<1>, pg, pb, lds, st, p, u); break;
+            case 2: hipLaunchKernelGGL(score_union_plan<2>, pg, pb, lds, st, p, u); break;
+            case 4: hipLaunchKernelGGL(score_union_plan<4>, pg, pb, lds, st, p, u); break;
+            case 8: hipLaunchKernelGGL(score_union_plan<8>, pg, pb, lds, st, p, u); break;
+            default: hipLaunchKernelGGL(score_union_plan<16>, pg, pb, lds, st, p, u); break;
+        }
         rc = V1_LAUNCHED("score_union_plan");
         if (rc != V1_OK) return rc;
         launch_hb<SharedUnion>(hb, a->relu != 0, dim3((uint32_t)(2 * (int64_t)v1::device_cus())), st, p);
