@@ -360,24 +360,39 @@ constexpr int kUnionLevels = 10;
 static_assert(kUnionRange == kWave && kUnionRange <= kMaxRangePages, "one union entry per lane");
 
 // UNION: the item's pages are union entries of per-row tables (their columns
-// come from each row's table slot; a wave skips the MFMAs of a page neither
-// of its queries lists, while the ring, the barriers and the store count go
-// on unchanged).
-template <int HB, bool RELU, bool UNION = false>
-__global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
+// come from each row's table slot; a wave skips the MFMAs of a page none of
+// its queries lists, while the ring, the barriers and the store count go on
+// unchanged).  QPW: queries per wave, 2 (4 waves per group of 8 queries) or,
+// for the union form, 1 (8 waves of 512 threads, each skipping the pages its
+// own query does not list; the linear-term row block then carries the one
+// query's pieces in rows r with r % 4 < 2 and zeros elsewhere, so every value
+// is the same as with two queries per wave).
+template <int HB, bool RELU, bool UNION = false, int QPW = kQueriesPerWave>
+__global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(ScoreParams p) {
+    static_assert(QPW == 2 || (QPW == 1 && UNION), "one query per wave: the union form");
+    constexpr int kWaves = kQueriesPerGroup / QPW;
+    constexpr int kBlock = kWave * kWaves;
+    constexpr int kKeyDma = 8 / kWaves;       // 1 KiB key chunks per wave and page
+    constexpr int kScaleLanes = 64 / kWaves;  // lanes loading the page's 256 bytes of scales
     __shared__ __attribute__((aligned(16))) uint8_t st0[V1_PAGE_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t st1[V1_PAGE_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t st2[V1_PAGE_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t st3[V1_PAGE_BYTES];
+    // One query per wave (one work-group per CU): a ring of two windows of
+    // kWin pages and one barrier per window.  The waves skip different pages
+    // (each its own row's), so a barrier per page would hold them all to the
+    // busiest SIMD at every page; over a window the loads even out.
+    constexpr int kWin = 8;
+    __shared__ __attribute__((aligned(16))) uint8_t ring[QPW == 1 ? 2 * kWin : 1][V1_PAGE_BYTES];
     __shared__ int32_t pids[kMaxRangePages];
     __shared__ int32_t item_sh;
     // ReLU path: per query of the group, a bitmap of the item's pages that
     // hold a key marked for the exact form (bit (page_begin % 32) + page);
     // all zero between items.
-    __shared__ uint32_t marks[RELU ? kQueriesPerGroup * kMarkWords : 1];
+    __shared__ uint32_t marks[RELU && !UNION ? kQueriesPerGroup * kMarkWords : 1];
     const int t = threadIdx.x, l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     if (RELU && !UNION)
-        for (int i = t; i < kQueriesPerGroup * kMarkWords; i += kThreads) marks[i] = 0u;
+        for (int i = t; i < kQueriesPerGroup * kMarkWords; i += kBlock) marks[i] = 0u;
     // union items per level (final before this kernel starts)
     int32_t lvl_n[UNION ? kUnionLevels : 1];
     int32_t total_items = p.items;
@@ -431,8 +446,8 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         const int32_t c = min(p.ctx[min(r, (int64_t)p.rows - 1)], p.max_context_len);
         lane_ctx = r < p.rows ? c : 0;
     }
-    int32_t pid[kMaxRangePages / kThreads];
-    static_assert(kMaxRangePages == kThreads, "one page id per thread");
+    int32_t pid[1];
+    static_assert(kMaxRangePages == kThreads && (kBlock == kThreads || UNION), "one page id per thread");
     // Union: lane l of every wave holds entry l's table slots for the wave's
     // two queries, packed as 16-bit halves (0xffff: not listed; slots are
     // below kUnionEntries), loaded with the prologue.
@@ -447,22 +462,22 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
 #pragma unroll
         for (int k = 0; k < kMaxRangePages / kThreads; ++k) pid[k] = -1;
     }
-    uint64_t umark[kQueriesPerWave] = {0ull, 0ull};  // union: item pages holding keys for the exact form
-    uint64_t use_mask = ~0ull;                         // union: item pages either of this wave's queries lists
+    uint64_t umark[QPW] = {};  // union: item pages holding keys for the exact form
+    uint64_t use_mask = ~0ull;  // union: item pages one of this wave's queries lists
     // Query fragments, weights and linear-term coefficients.  Rows past the
     // end read the last row (their logits are never stored).
-    v8i a[kQueriesPerWave][HB];
-    float w[kQueriesPerWave][HB][4];
+    v8i a[QPW][HB];
+    float w[QPW][HB][4];
     // Linear-term MFMA row block: row r holds piece 2*(r/4) + r%2 of query
     // (r/2)%2, so result row 4*(l/16)+i of lane l is piece 2*(l/16) + i%2 of
-    // query i/2, and coef[i] is that piece's scale.
-    static_assert(kQueriesPerWave == 2, "two queries per linear-term row block");
-    float coef[4];
-    float exact_thr[kQueriesPerWave];
+    // query i/2, and coef[i] is that piece's scale.  (One query per wave:
+    // rows with r % 4 >= 2 are zero.)
+    float coef[2 * QPW];
+    float exact_thr[QPW];
     v8i alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int q = 0; q < kQueriesPerWave; ++q) {
-        const int64_t r = row0 + wv * kQueriesPerWave + q;
+    for (int q = 0; q < QPW; ++q) {
+        const int64_t r = row0 + wv * QPW + q;
         load_q<HB>(p, r, a[q]);
         const uint8_t* rec = p.pieces + min(r, (int64_t)p.rows - 1) * kPieceRowBytes;
 #pragma unroll
@@ -480,21 +495,21 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     }
     if (RELU) {
         const int rr = l & 15;
-        const int64_t rq = min(row0 + wv * kQueriesPerWave + ((rr >> 1) & 1), (int64_t)p.rows - 1);
+        const int64_t rq = min(row0 + wv * QPW + (QPW == 2 ? (rr >> 1) & 1 : 0), (int64_t)p.rows - 1);
         const int piece = 2 * (rr >> 2) + (rr & 1);
         const u32x4* src = reinterpret_cast<const u32x4*>(p.pieces + rq * kPieceRowBytes + piece * 128 + 32 * (l >> 4));
         const u32x4 x = src[0], y = src[1];
         alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+        if (QPW == 1 && (rr & 2)) alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
     }
-#pragma unroll
-    for (int k = 0; k < kMaxRangePages / kThreads; ++k) pids[k * kThreads + t] = pid[k];
+    if (kBlock == kMaxRangePages || t < kMaxRangePages) pids[t] = pid[0];
 
-    int32_t ctx[kQueriesPerWave];
+    int32_t ctx[QPW];
     int32_t max_ctx = 0;
 #pragma unroll
     for (int q = 0; q < kQueriesPerGroup; ++q) max_ctx = max(max_ctx, __builtin_amdgcn_readlane(lane_ctx, q));
 #pragma unroll
-    for (int q = 0; q < kQueriesPerWave; ++q) ctx[q] = __builtin_amdgcn_readlane(lane_ctx, wv * kQueriesPerWave + q);
+    for (int q = 0; q < QPW; ++q) ctx[q] = __builtin_amdgcn_readlane(lane_ctx, wv * QPW + q);
     // pages of the range below the group's longest context (union: every entry)
     const int32_t npages = UNION ? ulen : max(0, min(nchunk * kChunkPages, (max_ctx + 63) / 64 - page_begin));
 
@@ -505,8 +520,8 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         if (UNION || !p.clean) return;
         for (int32_t pg = from_page; pg < nchunk * kChunkPages; ++pg) {
 #pragma unroll
-            for (int q = 0; q < kQueriesPerWave; ++q)
-                store_logit(p, row0 + wv * kQueriesPerWave + q, (page_begin + pg) * 64 + l, ctx[q], 0.f);
+            for (int q = 0; q < QPW; ++q)
+                store_logit(p, row0 + wv * QPW + q, (page_begin + pg) * 64 + l, ctx[q], 0.f);
         }
     };
     if (npages == 0) {
@@ -515,28 +530,36 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     }
     __syncthreads();  // page ids in LDS
 
-    // per-lane load offsets (into the page) of this wave's three loads
-    int32_t voff[2];
+    // per-lane load offsets (into the page) of this wave's loads
+    int32_t voff[kKeyDma];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int s = (2 * wv + i) * 64 + l;  // 16-byte LDS slot
+    for (int i = 0; i < kKeyDma; ++i) {
+        const int s = (kKeyDma * wv + i) * 64 + l;  // 16-byte LDS slot
         const int key = s >> 3;
         voff[i] = key * 128 + (((s & 7) ^ key_swizzle(key & 15)) << 4);
     }
-    const int32_t soff = 8192 + 64 * wv + 4 * l;
+    const int32_t soff = 8192 + 4 * kScaleLanes * wv + 4 * l;
     auto issue = [&](uint8_t* buf, int32_t page) {
         const i32x4 rs = page_rsrc(p.kv, page);
         const uint32_t base = lds_addr(buf);
-        dma16(rs, voff[0], base + (2 * wv) * 1024);
-        dma16(rs, voff[1], base + (2 * wv + 1) * 1024);
-        if (l < 16) dma4(rs, soff, base + 8192 + 64 * wv);
+#pragma unroll
+        for (int i = 0; i < kKeyDma; ++i) dma16(rs, voff[i], base + (kKeyDma * wv + i) * 1024);
+        if (l < kScaleLanes) dma4(rs, soff, base + 8192 + 4 * kScaleLanes * wv);
     };
-    issue(st0, __builtin_amdgcn_readfirstlane(pids[0]));
-    issue(st1, 1 < npages ? __builtin_amdgcn_readfirstlane(pids[1]) : -1);
-    issue(st2, 2 < npages ? __builtin_amdgcn_readfirstlane(pids[2]) : -1);
-    issue(st3, 3 < npages ? __builtin_amdgcn_readfirstlane(pids[3]) : -1);
-    // page id of the next page to load, read from LDS one step ahead
-    int32_t pid_next = pids[kStages];
+    int32_t pid_next = 0;
+    if constexpr (QPW == 2) {
+        issue(st0, __builtin_amdgcn_readfirstlane(pids[0]));
+        issue(st1, 1 < npages ? __builtin_amdgcn_readfirstlane(pids[1]) : -1);
+        issue(st2, 2 < npages ? __builtin_amdgcn_readfirstlane(pids[2]) : -1);
+        issue(st3, 3 < npages ? __builtin_amdgcn_readfirstlane(pids[3]) : -1);
+        // page id of the next page to load, read from LDS one step ahead
+        pid_next = pids[kStages];
+    } else {
+        // the first two windows
+#pragma unroll
+        for (int j = 0; j < 2 * kWin; ++j)
+            issue(ring[j], j < npages ? __builtin_amdgcn_readfirstlane(pids[j]) : -1);
+    }
 
     // B fragment of key block kb: key kb*16 + l%16, chunks 2*(l/16) and +1;
     // plus the scale of key l
@@ -563,7 +586,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // pipe keeps working while the VALU folds older results; the stream runs
     // on across pages, the first kLag slots of a page finishing the previous
     // page's partials.
-    constexpr int kPer = (RELU ? 1 : 0) + kQueriesPerWave * HB;
+    constexpr int kPer = (RELU ? 1 : 0) + QPW * HB;
     constexpr int kTotal = 4 * kPer;
     constexpr int kLag = 3;
     static_assert(kTotal % (kLag + 1) == 0 && kTotal > kLag + 4, "result ring continues across pages");
@@ -579,12 +602,12 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         const int rr = RELU ? max(r - 1, 0) : r;  // head block (r == 0 is the linear-term block)
         d[idx % (kLag + 1)] = (RELU && r == 0) ? mfma_fp8(alin, f.b[kb]) : mfma_fp8(a[rr / HB][rr % HB], f.b[kb]);
     };
-    auto consume = [&](int jj, float (&part)[kQueriesPerWave][4]) __attribute__((always_inline)) {
+    auto consume = [&](int jj, float (&part)[QPW][4]) __attribute__((always_inline)) {
         const int kb = jj / kPer, r = jj % kPer;
         const v4f x = d[jj % (kLag + 1)];
         if (RELU && r == 0) {
 #pragma unroll
-            for (int q = 0; q < kQueriesPerWave; ++q) part[q][kb] = fmaf(coef[2 * q + 1], x[2 * q + 1], coef[2 * q] * x[2 * q]);
+            for (int q = 0; q < QPW; ++q) part[q][kb] = fmaf(coef[2 * q + 1], x[2 * q + 1], coef[2 * q] * x[2 * q]);
         } else {
             const int rr = RELU ? r - 1 : r;
             const int q = rr / HB, hb = rr % HB;
@@ -595,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
             }
         }
     };
-    // Every step issues exactly kQueriesPerWave logit stores, each through a
+    // Every step issues exactly QPW logit stores, each through a
     // buffer descriptor over the columns of the page that the query writes:
     // lanes with nothing to write (no page, a row past the end, a column past
     // max_context_len, or past the context without clean_logits) lie past the
@@ -606,11 +629,11 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // of zero only mark their page here (a bit per query and page in LDS, set
     // in a rarely taken scalar branch with no vector memory operation); the
     // item's end hands the marks to score_exact.
-    auto store = [&](int32_t pg, bool live, const float (&part)[kQueriesPerWave][4], float scale) {
+    auto store = [&](int32_t pg, bool live, const float (&part)[QPW][4], float scale) {
 #pragma unroll
-        for (int q = 0; q < kQueriesPerWave; ++q) {
+        for (int q = 0; q < QPW; ++q) {
             const float v = reduce_scatter4(part[q]);
-            const int32_t qr = wv * kQueriesPerWave + q;  // row within the group
+            const int32_t qr = wv * QPW + q;  // row within the group
             // this page's first column in the query's row (union: from the
             // row's table slot; a page the row does not list stores nothing)
             int32_t col = (page_begin + pg) * 64;
@@ -645,22 +668,31 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
                         int32_t bit = (page_begin & 31) + pg;
                         asm volatile("" : "+s"(bit));
                         if (l == 0)
-                            atomicOr(&marks[(wv * kQueriesPerWave + q) * kMarkWords + (bit >> 5)], 1u << (bit & 31));
+                            atomicOr(&marks[(wv * QPW + q) * kMarkWords + (bit >> 5)], 1u << (bit & 31));
                     }
                 }
             }
         }
     };
 
+    // The store of a step with nothing to store: a descriptor of length 0
+    // drops it, and the step's count of memory operations stays fixed.
+    auto no_store = [&]() __attribute__((always_inline)) {
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(p.logits, 0, 0, kRawDword);
+        __builtin_amdgcn_raw_buffer_store_b32(0u, rs, l * 4, 0, 0);
+    };
+
     // The page wait.  A wave's vector memory operations complete in issue
     // order (loads and stores alike share vmcnt and retire in order), and per
-    // step a wave issues kQueriesPerWave stores and then kDmaPerPage loads.
-    // At step i the loads of page i+1 were issued at step i-3; after them came
-    // the stores and loads of steps i-2 and i-1 and the stores of step i, so
-    // `vmcnt <= kWaitCount` holds only once page i+1 has landed.  (The first
-    // pages are covered by the full wait before the loop.)
-    constexpr int kWaitCount = (kDmaPerPage + kQueriesPerWave) * (kStages - 2) + kQueriesPerWave;
-    static_assert(kStages == 4 && kWaitCount == 12, "barrier wait count");
+    // step a wave issues QPW stores and then kDmaPerPage loads (kKeyDma key
+    // chunks and the scales).  At step i the loads of page i+1 were issued at
+    // step i-3; after them came the stores and loads of steps i-2 and i-1 and
+    // the stores of step i, so `vmcnt <= kWaitCount` holds only once page i+1
+    // has landed.  (The first pages are covered by the full wait before the
+    // loop.)
+    constexpr int kDmaPerPage = kKeyDma + 1;
+    constexpr int kWaitCount = (kDmaPerPage + QPW) * (kStages - 2) + QPW;
+    static_assert(kStages == 4 && (QPW == 1 || kWaitCount == 12), "barrier wait count (per page: two queries per wave)");
     // After the barrier every wave has read page i out of LDS (its fragments
     // were read at step i-1), so its buffer receives page i+4.
     auto sync = [&](int32_t i, uint8_t* cur) __attribute__((always_inline)) {
@@ -668,14 +700,14 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         issue(cur, i + kStages < npages ? __builtin_amdgcn_readfirstlane(pid_next) : -1);
         pid_next = pids[min(i + kStages + 1, kMaxRangePages - 1)];
     };
-    auto drain = [&](float (&part)[kQueriesPerWave][4]) __attribute__((always_inline)) {
+    auto drain = [&](float (&part)[QPW][4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = kTotal - kLag; j < kTotal; ++j) consume(j, part);
     };
     // Page j is computed: it lies in the item and (union) one of this wave's
-    // queries lists it.  (The union form runs up to 48 heads: with 64 the
-    // branch around the stream costs the register allocator ~30 VGPRs past
-    // the 256 of two waves per SIMD.)
+    // queries lists it.  (With 64 heads and two queries per wave the branch
+    // around the stream costs the register allocator ~30 VGPRs past the 256
+    // of two waves per SIMD: 64 heads take one query per wave.)
     constexpr bool kSkip = UNION;
     auto used = [&](int32_t j) __attribute__((always_inline)) {
         return j >= 0 && j < npages && (!kSkip || ((use_mask >> (j & 63)) & 1ull) != 0);
@@ -683,7 +715,7 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // Step i: page i's fragments are in fc; fn holds page i-1's until page
     // i+1's are read into it.
     auto step = [&](int32_t i, uint8_t* cur, const uint8_t* next, const Frag& fc, Frag& fn,
-                    float (&pc)[kQueriesPerWave][4], float (&pp)[kQueriesPerWave][4]) {
+                    float (&pc)[QPW][4], float (&pp)[QPW][4]) {
         if (used(i)) {
 #pragma unroll
             for (int idx = 0; idx < kTotal; ++idx) {
@@ -711,10 +743,62 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
             load_frag(next, fn);
         }
     };
-    Frag fa, fb;
-    float pa[kQueriesPerWave][4], pb[kQueriesPerWave][4];
+    // One query per wave, step i at position k of the ring: page i's
+    // fragments are in fc (read during the previous step, or after the
+    // barrier that opened its window); the previous page is stored (or, when
+    // this wave did not compute it, a store through an empty descriptor is
+    // issued, so every step issues exactly one); the next page's fragments
+    // are read during the step unless it opens the next window.  At a
+    // window's end the next window's loads were followed by exactly kWin
+    // stores, every wave has read this window's pages, and its buffers
+    // receive the window after next.
+    auto wstep = [&](int32_t i, int k, const Frag& fc, Frag& fn, float (&pc)[QPW][4],
+                     float (&pp)[QPW][4]) __attribute__((always_inline)) {
+        const bool wend = k % kWin == kWin - 1;  // (k is a constant of the unrolled loop)
+        uint8_t* next = ring[(k + 1) % (2 * kWin)];
+        if (used(i)) {
 #pragma unroll
-    for (int q = 0; q < kQueriesPerWave; ++q)
+            for (int idx = 0; idx < kTotal; ++idx) {
+                mfma_at(idx, fc);
+                __builtin_amdgcn_sched_barrier(0);
+                if (idx >= kLag)
+                    consume(idx - kLag, pc);
+                else
+                    consume(kTotal + idx - kLag, pp);
+                if (idx == kStoreAt) {
+                    if (used(i - 1))
+                        store(i - 1, true, pp, fn.scale);
+                    else
+                        no_store();
+                }
+                if (idx == kFragAt && !wend) load_frag(next, fn);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            if (used(i - 1)) {
+                drain(pp);
+                store(i - 1, true, pp, fn.scale);
+            } else {
+                no_store();
+            }
+            if (!wend) load_frag(next, fn);
+        }
+        if (wend) {
+            static_assert(kWin == 8, "window wait count");
+            V1_PAGE_BARRIER(8);  // kWin
+#pragma unroll
+            for (int j = 0; j < kWin; ++j) {
+                const int32_t pg = i + 1 + kWin + j;
+                issue(ring[(k + 1 + kWin + j) % (2 * kWin)],
+                      pg < npages ? __builtin_amdgcn_readfirstlane(pids[min(pg, kMaxRangePages - 1)]) : -1);
+            }
+            load_frag(next, fn);
+        }
+    };
+    Frag fa, fb;
+    float pa[QPW][4], pb[QPW][4];
+#pragma unroll
+    for (int q = 0; q < QPW; ++q)
 #pragma unroll
         for (int k = 0; k < 4; ++k) pa[q][k] = pb[q][k] = 0.f;
     // Compiler-visible full wait: the query fragments, weights and records
@@ -723,28 +807,51 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     __builtin_amdgcn_s_waitcnt(0);
     V1_PAGE_BARRIER(0);
 #pragma unroll
-    for (int q = 0; q < kQueriesPerWave; ++q)
+    for (int q = 0; q < QPW; ++q)
         exact_thr[q] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, exact_thr[q])));
     if constexpr (UNION) {
         // (loaded after the prologue's wait: kept out of its register peak)
         const int64_t e = ubase + min(l, ulen - 1);
         const uint32_t umask = p.u_mask[e];
-        const int2 uslot2 = *reinterpret_cast<const int2*>(p.u_slots + e * kQueriesPerGroup + wv * kQueriesPerWave);
-        const bool in0 = l < ulen && ((umask >> (wv * kQueriesPerWave)) & 1u);
-        const bool in1 = l < ulen && ((umask >> (wv * kQueriesPerWave + 1)) & 1u);
-        uslots = (in0 ? (uint32_t)uslot2.x & 0xffffu : 0xffffu) | ((in1 ? (uint32_t)uslot2.y & 0xffffu : 0xffffu) << 16);
-        use_mask = __builtin_amdgcn_ballot_w64(in0 | in1);
+        if constexpr (QPW == 2) {
+            const int2 uslot2 = *reinterpret_cast<const int2*>(p.u_slots + e * kQueriesPerGroup + wv * QPW);
+            const bool in0 = l < ulen && ((umask >> (wv * QPW)) & 1u);
+            const bool in1 = l < ulen && ((umask >> (wv * QPW + 1)) & 1u);
+            uslots = (in0 ? (uint32_t)uslot2.x & 0xffffu : 0xffffu) |
+                     ((in1 ? (uint32_t)uslot2.y & 0xffffu : 0xffffu) << 16);
+            use_mask = __builtin_amdgcn_ballot_w64(in0 | in1);
+        } else {
+            const int32_t uslot = p.u_slots[e * kQueriesPerGroup + wv];
+            const bool in0 = l < ulen && ((umask >> wv) & 1u);
+            uslots = (in0 ? (uint32_t)uslot & 0xffffu : 0xffffu) | 0xffff0000u;
+            use_mask = __builtin_amdgcn_ballot_w64(in0);
+        }
     }
-    load_frag(st0, fa);
-    for (int32_t i = 0; i < npages; i += kStages) {
-        step(i, st0, st1, fa, fb, pa, pb);
-        step(i + 1, st1, st2, fb, fa, pb, pa);
-        step(i + 2, st2, st3, fa, fb, pa, pb);
-        step(i + 3, st3, st0, fb, fa, pb, pa);
-    }
-    if (npages % kStages == 0 && used(npages - 1)) {
-        drain(pb);
-        store(npages - 1, true, pb, fb.scale);
+    if constexpr (QPW == 2) {
+        load_frag(st0, fa);
+        for (int32_t i = 0; i < npages; i += kStages) {
+            step(i, st0, st1, fa, fb, pa, pb);
+            step(i + 1, st1, st2, fb, fa, pb, pa);
+            step(i + 2, st2, st3, fa, fb, pa, pb);
+            step(i + 3, st3, st0, fb, fa, pb, pa);
+        }
+        if (npages % kStages == 0 && used(npages - 1)) {
+            drain(pb);
+            store(npages - 1, true, pb, fb.scale);
+        }
+    } else {
+        load_frag(ring[0], fa);
+        for (int32_t i0 = 0; i0 < npages; i0 += 2 * kWin) {
+#pragma unroll
+            for (int k = 0; k < 2 * kWin; k += 2) {
+                wstep(i0 + k, k, fa, fb, pa, pb);
+                wstep(i0 + k + 1, k + 1, fb, fa, pb, pa);
+            }
+        }
+        if (npages % (2 * kWin) == 0 && used(npages - 1)) {
+            drain(pb);
+            store(npages - 1, true, pb, fb.scale);
+        }
     }
     V1_PAGE_BARRIER(0);  // the page buffers are reused by the next item
     fill_rest(npages);
@@ -753,15 +860,14 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
         if (RELU) {
             const int32_t words = (((p.max_context_len + 63) >> 6) + 31) >> 5;
 #pragma unroll
-            for (int q = 0; q < kQueriesPerWave; ++q) {
+            for (int q = 0; q < QPW; ++q) {
                 uint64_t m = umark[q];
                 while (m != 0ull) {
                     const int32_t pg = __builtin_ctzll(m);
                     m &= m - 1;
                     const int32_t slot = (int32_t)(((uint32_t)__builtin_amdgcn_readlane((int)uslots, pg) >> (16 * q)) & 0xffffu);
                     if (l == 0)
-                        atomicOr(p.exact_pages + (row0 + wv * kQueriesPerWave + q) * words + (slot >> 5),
-                                 1u << (slot & 31));
+                        atomicOr(p.exact_pages + (row0 + wv * QPW + q) * words + (slot >> 5), 1u << (slot & 31));
                 }
             }
         }
@@ -772,13 +878,13 @@ __global__ __launch_bounds__(kThreads) void score_shared(ScoreParams p) {
     // (The bitmaps' row length follows from max_context_len.)
     int lane = l;
     asm volatile("" : "+v"(lane));  // keeps the lane arithmetic below inside the loop
-    if (RELU && lane < kQueriesPerWave * kMarkWords) {
+    if (RELU && lane < QPW * kMarkWords) {
         const int q = lane / kMarkWords, k = lane % kMarkWords;
-        const uint32_t bits = marks[(wv * kQueriesPerWave + q) * kMarkWords + k];
+        const uint32_t bits = marks[(wv * QPW + q) * kMarkWords + k];
         if (bits != 0u) {
             const int32_t words = (((p.max_context_len + 63) >> 6) + 31) >> 5;
-            atomicOr(p.exact_pages + (row0 + wv * kQueriesPerWave + q) * words + (page_begin >> 5) + k, bits);
-            marks[(wv * kQueriesPerWave + q) * kMarkWords + k] = 0u;
+            atomicOr(p.exact_pages + (row0 + wv * QPW + q) * words + (page_begin >> 5) + k, bits);
+            marks[(wv * QPW + q) * kMarkWords + k] = 0u;
         }
     }
   }
@@ -988,30 +1094,37 @@ __global__ __launch_bounds__(256) void score_exact(ScoreParams p) {
 
 // ---------------------------------------------------------- union plan
 // Per-row tables of a batch whose rows share most of their pages (the rows
-// of one prefill chunk) go through the shared-table kernel's page ring: per
-// group of 8 rows, the (row, slot) pairs of the rows' live table slots are
-// sorted by (page, row, slot); every distinct page becomes a union entry,
-// and a row that lists a page k times puts its k-th slot in the page's k-th
-// entry.  Entries hold the pool page (-1 for slots past the table or out of
-// the pool: their keys read as zeros and score 0, as in score_rows), a
-// mask of the rows that list it and each such row's slot.  The group's
+// of one prefill chunk) go through the shared-table kernel's page ring.  Per
+// group of 8 rows, the valid pages of the rows' live table slots go into a
+// hash set in LDS (open addressing, linear probing); every distinct page
+// becomes a union entry holding the pool page, a mask of the rows that list
+// it and each such row's slot.  A row that lists a page again puts that slot
+// in an entry of its own.  Slots past the table or out of the pool get no
+// entry: their columns are written here, 0 below the row's context and -inf
+// from there to max_context_len with clean_logits (the values of a page of
+// zeros in score_rows).  Entries follow the order of the hash slots, which
+// depends on the order of insertion; no value depends on it.  The group's
 // entries are cut into items of at most kUnionRange entries, full ranges
 // first (level 0), then a halving tail (levels 1 ..), appended to per-level
-// lists; groups whose rows share too little (fewer than two rows per page
-// on average) are flagged for score_rows instead.  One work-group per group;
-// with clean_logits it also fills the columns past each row's last page.
+// lists.  Groups whose rows share too little (fewer than two listed pairs
+// per entry on average), or where a page probes more than kPlanProbes
+// slots, are flagged for score_rows, whose values are the same bit for bit.
+// One work-group per group; with clean_logits it also fills the columns past
+// each row's last page.
 constexpr int kUnionEntries = 8192;  // (row, slot) pairs of a group: 8 rows x 1024 table pages
 static_assert(kUnionEntries < 0xffff, "union slots fit 16 bits");
 constexpr int kPlanThreads = 512;
-// Pairs the plan sorts per group: the smallest power of two, at least one per
-// thread, that holds every group's pairs; its dynamic LDS is 16 bytes a pair.
-inline int32_t plan_pairs(int32_t max_pairs) {
+constexpr int kPlanPairs = kUnionEntries / kPlanThreads;  // pairs per thread
+constexpr int kPlanProbes = 64;
+// Hash slots per group: the smallest power of two, at least one per thread,
+// that holds every pair of a group (load <= 1/2 wherever the group is shared);
+// 8 bytes of dynamic LDS each.
+inline int32_t plan_slots(int32_t max_pairs) {
     int32_t n = kPlanThreads;
     while (n < max_pairs) n <<= 1;
     return n;
 }
 constexpr int kUnionMinRows = 513;   // decode batches (the reference's <= 512 rows) keep score_rows
-constexpr uint32_t kNoPage = 0x7fffffffu;
 
 struct UnionOut {
     int32_t* pages;
@@ -1022,42 +1135,39 @@ struct UnionOut {
     int32_t* fallback;  // [rows] 1: the row is scored by score_rows
 };
 
-// Exclusive prefix sum (kOp 0) or exclusive running max (kOp 1, identity -1)
-// of one value per thread over the work-group; `total` is the sum / max of all.
-template <int kOp>
+// Exclusive prefix sum of one value per thread over the work-group; `total`
+// is the sum of all.
 __device__ __forceinline__ int32_t plan_scan(int32_t v, int32_t* part, int32_t& total) {
     const int w = threadIdx.x / kWave, l = __lane_id();
     int32_t inc = v;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
         const int32_t o = __shfl_up(inc, off, kWave);
-        if (l >= off) inc = kOp == 0 ? inc + o : max(inc, o);
+        if (l >= off) inc += o;
     }
     if (l == kWave - 1) part[w] = inc;
     __syncthreads();
-    int32_t before = kOp == 0 ? 0 : -1;
-    total = kOp == 0 ? 0 : -1;
+    int32_t before = 0;
+    total = 0;
 #pragma unroll
     for (int k = 0; k < kPlanThreads / kWave; ++k) {
         const int32_t x = part[k];
-        if (k < w) before = kOp == 0 ? before + x : max(before, x);
-        total = kOp == 0 ? total + x : max(total, x);
+        if (k < w) before += x;
+        total += x;
     }
     __syncthreads();  // part is free again
-    const int32_t excl_in_wave = __shfl_up(inc, 1, kWave);
-    const int32_t wave_excl = l == 0 ? (kOp == 0 ? 0 : -1) : excl_in_wave;
-    return kOp == 0 ? before + wave_excl : max(before, wave_excl);
+    return before + inc - v;
 }
 
-// EP: pairs per thread; the call's groups have at most N = EP * kPlanThreads
-// (row, slot) pairs.  Dynamic LDS: 2N words of 8 bytes (the sort's two
-// buffers; then the run counts, entry masks and the sorted keys).
-template <int EP>
-__global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, UnionOut u) {
-    constexpr int N = EP * kPlanThreads;
-    extern __shared__ __attribute__((aligned(16))) uint64_t plan_lds[];
+// Dynamic LDS: hslots page keys (-1: empty) and hslots row masks (after the
+// count, the slot's entry).
+__global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, UnionOut u, int32_t hslots) {
+    extern __shared__ __attribute__((aligned(16))) int32_t plan_lds[];
+    int32_t* hkey = plan_lds;
+    uint32_t* hbits = reinterpret_cast<uint32_t*>(plan_lds + hslots);
     __shared__ int32_t part[kPlanThreads / kWave];
-    const int t = threadIdx.x;
+    __shared__ int32_t overflow;
+    const int t = threadIdx.x, l = __lane_id(), wv = threadIdx.x / kWave;
     const int32_t g = blockIdx.x;
     const int64_t row0 = (int64_t)g * kQueriesPerGroup;
     const int32_t grows = (int32_t)min<int64_t>(kQueriesPerGroup, (int64_t)p.rows - row0);
@@ -1070,102 +1180,113 @@ __global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, 
         const int32_t c = q < grows ? min(p.ctx[row0 + q], p.max_context_len) : 0;
         off[q + 1] = off[q] + (max(c, 0) + 63) / 64;
     }
-    const int32_t E = off[kQueriesPerGroup];  // <= N
-    // pair e of thread t's run: ((page + 1) << 32) | (row << 24) | slot, page
-    // kNoPage for slots past the table or out of the pool; padding is 0 and
-    // sorts last
-    uint64_t v[EP];
+    const int32_t E = off[kQueriesPerGroup];  // <= hslots
+    auto row_of = [&](int32_t e) __attribute__((always_inline)) {
+        int q = 0;
 #pragma unroll
-    for (int i = 0; i < EP; ++i) {
-        const int32_t e = t * EP + i;
-        v[i] = 0ull;
+        for (int j = 1; j < kQueriesPerGroup; ++j) q += e >= off[j] ? 1 : 0;
+        return q;
+    };
+    for (int32_t h = t; h < hslots; h += kPlanThreads) {
+        hkey[h] = -1;
+        hbits[h] = 0u;
+    }
+    if (t == 0) overflow = 0;
+    __syncthreads();
+    // pair e = t + k * kPlanThreads: res[k] = its hash slot (plus 0x10000 when
+    // its row listed the page at another slot first), -1 for a slot without
+    // a valid page, -2 past the pairs
+    const int shift = 32 - __builtin_ctz((uint32_t)hslots);
+    int32_t res[kPlanPairs];
+    int32_t nvalid = 0, nrep = 0;
+#pragma unroll
+    for (int k = 0; k < kPlanPairs; ++k) {
+        const int32_t e = t + k * kPlanThreads;
+        res[k] = -2;
         if (e < E) {
-            int q = 0;
-#pragma unroll
-            for (int j = 1; j < kQueriesPerGroup; ++j) q += e >= off[j] ? 1 : 0;
-            const int32_t slot = e - off[q];
-            const int32_t page = page_of(p, row0 + q, slot);
-            v[i] = ((uint64_t)((page >= 0 ? (uint32_t)page : kNoPage) + 1u) << 32) | ((uint64_t)q << 24) |
-                   (uint32_t)slot;
+            const int q = row_of(e);
+            const int32_t page = page_of(p, row0 + q, e - off[q]);
+            res[k] = -1;
+            if (page >= 0) {
+                ++nvalid;
+                uint32_t h = ((uint32_t)page * 0x9e3779b1u) >> shift;
+                int32_t found = -1;
+                for (int i = 0; i < kPlanProbes; ++i) {
+                    const int32_t old = atomicCAS(&hkey[h], -1, page);
+                    if (old == -1 || old == page) {
+                        found = (int32_t)h;
+                        break;
+                    }
+                    h = (h + 1) & (uint32_t)(hslots - 1);
+                }
+                if (found < 0) {
+                    overflow = 1;
+                } else {
+                    const uint32_t rep = (atomicOr(&hbits[found], 1u << q) >> q) & 1u;
+                    nrep += (int32_t)rep;
+                    res[k] = found | (int32_t)(rep << 16);
+                }
+            }
         }
     }
-    // descending sort, in registers (LDS for the steps across waves)
-    bitonic_desc_regs<EP>(v, N, plan_lds, plan_lds + N, N);
-    __syncthreads();  // the sort's buffers are free
-    int32_t* run = reinterpret_cast<int32_t*>(plan_lds);        // per page run: its entries, then its first
-    uint32_t* umask = reinterpret_cast<uint32_t*>(run + N);      // per entry: the rows listing it
-    uint64_t* sorted = plan_lds + N;                             // the sorted pairs
-#pragma unroll
-    for (int i = 0; i < EP; ++i) {
-        sorted[t * EP + i] = v[i];
-        run[t * EP + i] = 0;
-        umask[t * EP + i] = 0u;
-    }
     __syncthreads();
-    // runs: a page starts where the page field changes, a (page, row) run
-    // where either changes; a pair's occurrence is its distance from the
-    // start of its (page, row) run
-    int32_t P[EP], Q[EP], S[EP], R[EP], K[EP];
-    int32_t nstart = 0, last = -1;
-#pragma unroll
-    for (int j = 0; j < EP; ++j) {
-        const int32_t i = t * EP + j;
-        P[j] = -1;
-        if (i < E) {
-            const uint64_t x = v[j], y = j > 0 ? v[j - 1] : (i > 0 ? sorted[i - 1] : ~0ull);
-            P[j] = (int32_t)((uint32_t)(x >> 32) - 1u);
-            Q[j] = (int32_t)((x >> 24) & 0xff);
-            S[j] = (int32_t)(x & 0xffffff);
-            const bool ps = i == 0 || (x >> 32) != (y >> 32);
-            const bool pqs = ps || ((x >> 24) & 0xff) != ((y >> 24) & 0xff);
-            nstart += ps ? 1 : 0;
-            R[j] = nstart;  // page starts up to here within the thread's run
-            if (pqs) last = i;
-            K[j] = last;    // last (page, row) start up to here within the run
+    // thread t's run of hash slots: [t * per, (t + 1) * per)
+    const int32_t per = hslots / kPlanThreads;
+    int32_t occ = 0;
+    for (int32_t h = t * per; h < (t + 1) * per; ++h) occ += hkey[h] != -1 ? 1 : 0;
+    int32_t Umain, D, V;
+    const int32_t first_main = plan_scan(occ, part, Umain);
+    const int32_t first_rep = Umain + plan_scan(nrep, part, D);
+    plan_scan(nvalid, part, V);
+    const int32_t U = Umain + D;
+    const bool shared = overflow == 0 && 2 * U <= V;
+    if (shared) {
+        int32_t e = first_main;
+        for (int32_t h = t * per; h < (t + 1) * per; ++h) {
+            const int32_t key = hkey[h];
+            if (key == -1) continue;
+            u.pages[gbase + e] = key;
+            u.mask[gbase + e] = hbits[h];
+            hbits[h] = (uint32_t)e;
+            ++e;
         }
     }
-    int32_t runs, dummy;
-    const int32_t run_before = plan_scan<0>(nstart, part, runs);
-    const int32_t last_before = plan_scan<1>(last, part, dummy);
-#pragma unroll
-    for (int j = 0; j < EP; ++j) {
-        if (P[j] == -1) continue;
-        const int32_t i = t * EP + j;
-        R[j] += run_before - 1;                        // page run of the pair
-        K[j] = i - max(K[j], last_before);             // its occurrence among the row's slots of the page
-        atomicMax(&run[R[j]], K[j] + 1);
-    }
     __syncthreads();
-    // entries per run -> first entry per run (exclusive sum over the runs)
-    int32_t cnt[EP];
-    int32_t local = 0;
+    if (shared) {
+        int32_t r = first_rep;
 #pragma unroll
-    for (int j = 0; j < EP; ++j) {
-        const int32_t r = t * EP + j;
-        cnt[j] = r < runs ? run[r] : 0;
-        local += cnt[j];
-    }
-    int32_t U;
-    int32_t first = plan_scan<0>(local, part, U);
+        for (int k = 0; k < kPlanPairs; ++k) {
+            if (res[k] < 0) continue;
+            const int32_t e = t + k * kPlanThreads;
+            const int q = row_of(e);
+            const int32_t slot = e - off[q], h = res[k] & 0xffff;
+            int32_t ent = (int32_t)hbits[h];
+            if (res[k] >> 16) {
+                ent = r++;
+                u.pages[gbase + ent] = hkey[h];
+                u.mask[gbase + ent] = 1u << q;
+            }
+            u.slots[(gbase + ent) * kQueriesPerGroup + q] = slot;
+        }
+        // slots without a valid page: the whole wave writes each one's 64 columns
 #pragma unroll
-    for (int j = 0; j < EP; ++j) {
-        const int32_t r = t * EP + j;
-        if (r < runs) run[r] = first;
-        first += cnt[j];
+        for (int k = 0; k < kPlanPairs; ++k) {
+            uint64_t inv = __builtin_amdgcn_ballot_w64(res[k] == -1);
+            while (inv != 0ull) {
+                const int32_t lane = __builtin_ctzll(inv);
+                inv &= inv - 1;
+                const int32_t e = wv * kWave + lane + k * kPlanThreads;
+                const int q = row_of(e);
+                const int32_t c = min(p.ctx[row0 + q], p.max_context_len);
+                const int32_t j = (e - off[q]) * 64 + l;
+                float* rp = p.logits + (row0 + q) * p.logits_stride;
+                if (j < c)
+                    rp[j] = 0.f;
+                else if (p.clean && j < p.max_context_len)
+                    rp[j] = -__builtin_huge_valf();
+            }
+        }
     }
-    __syncthreads();
-    const bool shared = 2 * U <= E;
-#pragma unroll
-    for (int j = 0; j < EP; ++j) {
-        if (P[j] == -1 || !shared) continue;
-        const int32_t e = run[R[j]] + K[j];
-        u.slots[(gbase + e) * kQueriesPerGroup + Q[j]] = S[j];
-        u.pages[gbase + e] = P[j] == (int32_t)kNoPage ? -1 : P[j];  // (every pair of the entry writes the same page)
-        atomicOr(&umask[e], 1u << Q[j]);
-    }
-    __syncthreads();
-    if (shared)
-        for (int32_t e = t; e < U; e += kPlanThreads) u.mask[gbase + e] = umask[e];
     if (t < grows) u.fallback[row0 + t] = shared ? 0 : 1;
     if (shared && p.clean) {
         // columns past each row's last live page (score_rows fills them for flagged rows)
@@ -1350,10 +1471,15 @@ struct Shared {
         hipLaunchKernelGGL((score_shared<HB, RELU>), g, dim3(kThreads), 0, st, p);
     }
 };
-struct SharedUnion {  // (v1_score takes the union form from 17 to 48 heads only)
+// The union form (v1_score takes it from 17 heads): two queries per wave up
+// to 48 heads, one with 64 (one 512-thread work-group per CU).
+struct SharedUnion {
     template <int HB, bool RELU>
     static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
-        if constexpr (HB == 2 || HB == 3) hipLaunchKernelGGL((score_shared<HB, RELU, true>), g, dim3(kThreads), 0, st, p);
+        if constexpr (HB == 2 || HB == 3)
+            hipLaunchKernelGGL((score_shared<HB, RELU, true>), g, dim3(kThreads), 0, st, p);
+        else if constexpr (HB == 4)
+            hipLaunchKernelGGL((score_shared<HB, RELU, true, 1>), g, dim3(2 * kThreads), 0, st, p);
     }
 };
 struct Rows {
@@ -1362,10 +1488,10 @@ struct Rows {
         hipLaunchKernelGGL((score_rows<HB, RELU>), g, dim3(kThreads), 0, st, p);
     }
 };
-struct RowsFast {  // (the flagged rows of the union form: 17 to 48 heads)
+struct RowsFast {  // (the flagged rows of the union form: 17 heads and more)
     template <int HB, bool RELU>
     static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
-        if constexpr (HB == 2 || HB == 3) hipLaunchKernelGGL((score_rows<HB, RELU, true>), g, dim3(kThreads), 0, st, p);
+        if constexpr (HB >= 2) hipLaunchKernelGGL((score_rows<HB, RELU, true>), g, dim3(kThreads), 0, st, p);
     }
 };
 
@@ -1513,13 +1639,10 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
     // the union plan, the shared-table kernel over each group's union, and
     // score_rows for the rows of groups that share too little.
     // Measured: with one head block score_rows' cost per page (a few MFMAs)
-    // is below the ring's, and with 64 heads, where every union page is
-    // computed for all 8 rows, the plan lost to score_rows at the reference's
-    // page_fraction 0.5 (1024 rows x 545 pages: 0.545 against 0.514 ms); from
-    // 17 to 48 heads the waves skip the pages their rows do not list (4096
-    // rows x 32 heads, 40 routed pages: 0.31 -> 0.23 ms).
+    // is below the ring's; from 17 heads the waves skip the pages their rows
+    // do not list (4096 rows x 32 heads, 40 routed pages: 0.31 -> 0.18 ms).
     const int64_t plan_need = v1_score_tables_workspace(a->rows, a->max_context_len);
-    const bool plan = plan_need > 0 && a->heads > 16 && a->heads <= 48 && a->workspace != nullptr &&
+    const bool plan = plan_need > 0 && a->heads > 16 && a->workspace != nullptr &&
                       a->workspace_bytes >= plan_need && (reinterpret_cast<uintptr_t>(a->workspace) & 255) == 0;
     if (plan) {
         const UnionLayout L = union_layout(a->rows, a->max_context_len);
@@ -1546,33 +1669,21 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
                            (int32_t)kUnionLevels);
         int rc = V1_LAUNCHED("score_prep");
         if (rc != V1_OK) return rc;
-        const int32_t npairs = plan_pairs((int32_t)(kQueriesPerGroup * cdiv(a->max_context_len, 64)));
-        // (dynamic LDS past 64 KiB is allowed once per process and instance)
+        const int32_t hslots = plan_slots((int32_t)(kQueriesPerGroup * cdiv(a->max_context_len, 64)));
+        // (dynamic LDS past 64 KiB needs the attribute, set once per process)
         static std::once_flag lds_once;
         static hipError_t lds_err = hipSuccess;
         std::call_once(lds_once, [] {
-            const void* fns[] = {reinterpret_cast<const void*>(&score_union_plan<1>),
-                                 reinterpret_cast<const void*>(&score_union_plan<2>),
-                                 reinterpret_cast<const void*>(&score_union_plan<4>),
-                                 reinterpret_cast<const void*>(&score_union_plan<8>),
-                                 reinterpret_cast<const void*>(&score_union_plan<16>)};
-            for (const void* f : fns)
-                if (lds_err == hipSuccess)
-                    lds_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 16 * kUnionEntries);
+            lds_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&score_union_plan),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 8 * kUnionEntries);
         });
         if (lds_err != hipSuccess) return hip_status(lds_err, "score: hipFuncSetAttribute(score_union_plan)");
-        const dim3 pg((uint32_t)groups), pb(kPlanThreads);
-        const size_t lds = 16 * (size_t)npairs;
-        switch (npairs / kPlanThreads) {
-            case 1: hipLaunchKernelGGL(score_union_plan<1>, pg, pb, lds, st, p, u); break;
-            case 2: hipLaunchKernelGGL(score_union_plan<2>, pg, pb, lds, st, p, u); break;
-            case 4: hipLaunchKernelGGL(score_union_plan<4>, pg, pb, lds, st, p, u); break;
-            case 8: hipLaunchKernelGGL(score_union_plan<8>, pg, pb, lds, st, p, u); break;
-            default: hipLaunchKernelGGL(score_union_plan<16>, pg, pb, lds, st, p, u); break;
-        }
+        hipLaunchKernelGGL(score_union_plan, dim3((uint32_t)groups), dim3(kPlanThreads), 8 * (size_t)hslots, st, p, u,
+                           hslots);
         rc = V1_LAUNCHED("score_union_plan");
         if (rc != V1_OK) return rc;
-        launch_hb<SharedUnion>(hb, a->relu != 0, dim3((uint32_t)(2 * (int64_t)v1::device_cus())), st, p);
+        // (two 256-thread work-groups per CU; one of 512 threads with 64 heads)
+        launch_hb<SharedUnion>(hb, a->relu != 0, dim3((uint32_t)((hb == 4 ? 1 : 2) * (int64_t)v1::device_cus())), st, p);
         rc = V1_LAUNCHED("score_shared (union)");
         if (rc != V1_OK) return rc;
         // flagged rows with the plan's arithmetic (every row of the call gets

@@ -3,7 +3,8 @@
 Batches of more than 512 rows with per-row tables (the fine tables of a
 prefill chunk, sglang/srt/layers/attention/v1_deepseek/runtime.py:538-548)
 are scored per group of 8 rows over the union of the rows' table pages (17
-to 48 heads, when the rows share enough of their pages).  The
+heads and more, when the rows share enough of their pages; two queries per
+wave up to 48 heads, one with 64).  The
 result must be the formula of kernels.py:310-313 through each row's own table,
 whatever the tables hold: partly overlapping page sets in each row's own
 order, unequal lengths (empty rows, rows past their table), a page listed
@@ -101,7 +102,9 @@ def _run(dev, q8, w, native, table, lens, width, relu, clean, fill=7.0):
     (520, 32, 32, True, True, 44, 0),     # 65 groups sharing almost every page
     (1031, 32, 4, True, False, 30, 4),    # last group of 7 rows, pages a wave's rows skip, unclean, zero plateau
     (777, 48, 48, False, True, 30, 4),    # signed scores, 48 heads
-    (560, 64, 64, True, True, 44, 0),     # 64 heads: row by row (the plan takes 17 to 48 heads)
+    (560, 64, 64, True, True, 44, 0),     # 64 heads: one query per wave
+    (1031, 64, 4, True, False, 30, 4),    # 64 heads, few live ones, unclean, partial last group
+    (777, 64, 64, False, True, 30, 4),    # 64 heads, signed scores
     (600, 16, 2, True, True, 30, 4),      # one head block: row by row
     (529, 7, 7, True, True, 30, 4),       # heads not a multiple of 16: row by row
 ])
@@ -157,3 +160,25 @@ def test_union_plan_low_sharing_groups_fall_back(dev):
     got = _run(dev, q8, w, native, table, lens, width, True, True)
     pool, tab = _padded(native, table, width)
     assert_scores_rel(got, O.paged_logits(q8, w, pool, tab, lens, width))
+
+
+@pytest.mark.parametrize("heads", [32, 64])
+def test_union_plan_rows_bitwise_across_kernels(dev, heads):
+    """A row gets the same bits whichever kernel scores it: row 8 repeats
+    row 0 (query, weights, table, length) inside a group of otherwise
+    unrelated rows, which the plan hands to the per-row kernel, while row 0's
+    group is scored over its union."""
+    g = np.random.default_rng(heads)
+    rows, pool_pages = 528, 300
+    q8, w = _queries(g, rows, heads, heads)
+    k8, ks = W.quantize_rows(g.standard_normal((pool_pages * 64, 128), dtype=np.float32))
+    native = W.pack_pages(k8, ks)
+    table = _tables(g, rows, pool_pages, shared_pages=40, take=30, private=2, unrelated_rows=set(range(9, 16)))
+    blocks = table.shape[1]
+    lens = g.integers(blocks * 32, blocks * 64 + 1, rows).astype(np.int32)
+    q8[8], w[8], table[8], lens[8] = q8[0], w[0], table[0], lens[0]
+    width = blocks * 64
+    got = _run(dev, q8, w, native, table, lens, width, True, True).astype(np.float32)
+    assert np.array_equal(got[8].view(np.uint32), got[0].view(np.uint32))
+    pool, tab = _padded(native, table, width)
+    assert_scores_rel(got.astype(np.float64), O.paged_logits(q8, w, pool, tab, lens, width))
