@@ -175,8 +175,9 @@ typedef struct {
  * fast value is within rounding of zero get the direct ReLU sum, so keys with
  * no positive head dot score exactly 0, as kernels.py:310-313 gives). */
 int64_t v1_score_workspace(int32_t rows, int32_t max_context_len);
-/* Per-row block tables (block_table_stride != 0) of more than 512 rows with
- * max_context_len <= 65536: given a 256-byte aligned workspace of at least
+/* Per-row block tables (block_table_stride != 0) of more than 512 rows and
+ * more than 16 heads with max_context_len <= 65536: given a 256-byte aligned
+ * workspace of at least
  * this many bytes (0 when the shape does not qualify), v1_score plans each
  * group of 8 rows over the union of their table pages and stages every page
  * once for the group (the rows of one prefill chunk share most pages, as the
