@@ -752,11 +752,12 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
     // window's end the next window's loads were followed by exactly kWin
     // stores, every wave has read this window's pages, and its buffers
     // receive the window after next.
-    auto wstep = [&](int32_t i, int k, const Frag& fc, Frag& fn, float (&pc)[QPW][4],
+    // (ucur, uprev: this wave computes page i, computed page i - 1)
+    auto wstep = [&](int32_t i, int k, bool ucur, bool uprev, const Frag& fc, Frag& fn, float (&pc)[QPW][4],
                      float (&pp)[QPW][4]) __attribute__((always_inline)) {
         const bool wend = k % kWin == kWin - 1;  // (k is a constant of the unrolled loop)
         uint8_t* next = ring[(k + 1) % (2 * kWin)];
-        if (used(i)) {
+        if (ucur) {
 #pragma unroll
             for (int idx = 0; idx < kTotal; ++idx) {
                 mfma_at(idx, fc);
@@ -766,7 +767,7 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
                 else
                     consume(kTotal + idx - kLag, pp);
                 if (idx == kStoreAt) {
-                    if (used(i - 1))
+                    if (uprev)
                         store(i - 1, true, pp, fn.scale);
                     else
                         no_store();
@@ -775,7 +776,7 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
-            if (used(i - 1)) {
+            if (uprev) {
                 drain(pp);
                 store(i - 1, true, pp, fn.scale);
             } else {
@@ -840,15 +841,23 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
             store(npages - 1, true, pb, fb.scale);
         }
     } else {
+        // this wave's pages of the item as one mask (npages <= 64), read
+        // per step with constant shifts
+        static_assert(kUnionRange == 64 && 64 % (2 * kWin) == 0, "item pages in one 64-bit mask");
+        const uint64_t vmask = use_mask & (npages >= 64 ? ~0ull : (1ull << npages) - 1ull);
+        bool uprev = false;
         load_frag(ring[0], fa);
         for (int32_t i0 = 0; i0 < npages; i0 += 2 * kWin) {
+            const uint64_t wm = vmask >> i0;
 #pragma unroll
             for (int k = 0; k < 2 * kWin; k += 2) {
-                wstep(i0 + k, k, fa, fb, pa, pb);
-                wstep(i0 + k + 1, k + 1, fb, fa, pb, pa);
+                const bool u0 = (wm >> k) & 1ull, u1 = (wm >> (k + 1)) & 1ull;
+                wstep(i0 + k, k, u0, uprev, fa, fb, pa, pb);
+                wstep(i0 + k + 1, k + 1, u1, u0, fb, fa, pb, pa);
+                uprev = u1;
             }
         }
-        if (npages % (2 * kWin) == 0 && used(npages - 1)) {
+        if (uprev) {  // (the item ended at a ring boundary on a computed page)
             drain(pb);
             store(npages - 1, true, pb, fb.scale);
         }
@@ -1167,6 +1176,7 @@ __global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, 
     uint32_t* hbits = reinterpret_cast<uint32_t*>(plan_lds + hslots);
     __shared__ int32_t part[kPlanThreads / kWave];
     __shared__ int32_t overflow;
+    __shared__ int32_t by_mask[256];
     const int t = threadIdx.x, l = __lane_id(), wv = threadIdx.x / kWave;
     const int32_t g = blockIdx.x;
     const int64_t row0 = (int64_t)g * kQueriesPerGroup;
@@ -1235,20 +1245,43 @@ __global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, 
     int32_t occ = 0;
     for (int32_t h = t * per; h < (t + 1) * per; ++h) occ += hkey[h] != -1 ? 1 : 0;
     int32_t Umain, D, V;
-    const int32_t first_main = plan_scan(occ, part, Umain);
+    plan_scan(occ, part, Umain);
     const int32_t first_rep = Umain + plan_scan(nrep, part, D);
     plan_scan(nvalid, part, V);
     const int32_t U = Umain + D;
     const bool shared = overflow == 0 && 2 * U <= V;
+    // Entries of distinct pages, counted by their mask of rows, then dealt
+    // so that every 8 consecutive entries take a like share of each mask:
+    // the one-row-per-wave union form computes a window of 8 entries per
+    // barrier, each wave its own row's, and the busiest SIMD sets the
+    // window's time.  Rank r < 8W (W = Umain / 8 windows) goes to
+    // (r % W) * 8 + r / W, the rest stay in place.
+    for (int i = t; i < 256; i += kPlanThreads) by_mask[i] = 0;
+    __syncthreads();
+    int32_t rk[kPlanPairs];
+#pragma unroll
+    for (int i = 0; i < kPlanPairs; ++i) {
+        const int32_t h = t * per + i;
+        rk[i] = 0;
+        if (i < per && hkey[h] != -1) rk[i] = atomicAdd(&by_mask[hbits[h] & 0xffu], 1);
+    }
+    __syncthreads();
+    int32_t counted;
+    const int32_t mask_start = plan_scan(t < 256 ? by_mask[t] : 0, part, counted);
+    if (t < 256) by_mask[t] = mask_start;
+    __syncthreads();
     if (shared) {
-        int32_t e = first_main;
-        for (int32_t h = t * per; h < (t + 1) * per; ++h) {
-            const int32_t key = hkey[h];
-            if (key == -1) continue;
-            u.pages[gbase + e] = key;
-            u.mask[gbase + e] = hbits[h];
+        const int32_t W = Umain / 8;
+#pragma unroll
+        for (int i = 0; i < kPlanPairs; ++i) {
+            const int32_t h = t * per + i;
+            if (i >= per || hkey[h] == -1) continue;
+            const uint32_t m = hbits[h];
+            const int32_t r = by_mask[m & 0xffu] + rk[i];
+            const int32_t e = r < 8 * W ? (r % W) * 8 + r / W : r;
+            u.pages[gbase + e] = hkey[h];
+            u.mask[gbase + e] = m;
             hbits[h] = (uint32_t)e;
-            ++e;
         }
     }
     __syncthreads();
