@@ -182,3 +182,32 @@ def test_union_plan_rows_bitwise_across_kernels(dev, heads):
     assert np.array_equal(got[8].view(np.uint32), got[0].view(np.uint32))
     pool, tab = _padded(native, table, width)
     assert_scores_rel(got.astype(np.float64), O.paged_logits(q8, w, pool, tab, lens, width))
+
+
+def test_union_plan_probe_overflow_falls_back(dev):
+    """A group whose pages all land on one slot of the plan's hash set (68
+    pages of a 34000-page pool with the same multiplicative hash into 512
+    slots) probes past the plan's limit and is scored row by row; every row
+    still gives the reference."""
+    g = np.random.default_rng(5)
+    rows, heads, slots, pool_pages = 520, 32, 64, 34000
+    width = slots * 64  # 8 x 64 pairs per group: a 512-slot hash set
+    p = np.arange(pool_pages, dtype=np.uint64)
+    h = ((p * np.uint64(0x9E3779B1)) & np.uint64(0xFFFFFFFF)) >> np.uint64(23)
+    vals, counts = np.unique(h, return_counts=True)
+    colliding = p[h == vals[np.argmax(counts)]].astype(np.int32)
+    assert len(colliding) >= 66
+    others = np.setdiff1d(np.arange(1024, dtype=np.int32), colliding)[:90]
+    used = np.union1d(colliding, others)
+    native = np.zeros((pool_pages, 8448), np.uint8)
+    k8, ks = W.quantize_rows(g.standard_normal((len(used) * 64, 128), dtype=np.float32))
+    native[used] = W.pack_pages(k8, ks)
+    q8, w = _queries(g, rows, heads, heads)
+    table = np.empty((rows, slots), np.int32)
+    for r in range(rows):
+        table[r] = g.permutation(colliding)[:slots] if r < 8 else g.choice(others, slots)
+    lens = g.integers(width // 2, width + 1, rows).astype(np.int32)
+    lens[:8] = width  # the first group lists every colliding page
+    got = _run(dev, q8, w, native, table, lens, width, True, True)
+    pool, tab = _padded(native, table, width)
+    assert_scores_rel(got, O.paged_logits(q8, w, pool, tab, lens, width))
