@@ -19,10 +19,11 @@
 // key row swizzled so that the 16-byte fragment reads are bank-conflict free)
 // and reused by 8 queries x 64 heads.  Rows with their own tables run one
 // query per work-group, each wave streaming whole pages straight from HBM
-// (decode batches), or, for more than 512 rows (a prefill chunk's rows share
-// most of their pages), through the same LDS page ring over the union of each
-// 8-row group's table pages (score_union_plan + the union form of
-// score_shared), each wave skipping the pages neither of its queries lists.
+// (decode batches), or, for more than 512 rows of more than 16 heads (a
+// prefill chunk's rows share most of their pages), through the same LDS page
+// ring over the union of each 8-row group's table pages (score_union_plan +
+// the union form of score_shared), each wave skipping the pages none of its
+// queries lists.
 #include <algorithm>
 #include <mutex>
 

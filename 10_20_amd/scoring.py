@@ -8,8 +8,9 @@ k / s_k come from 8448-byte native pages ([64, 1, 132] byte view: 64x128 FP8
 then 64 fp32 scales) through block_table[r, j // 64].  A block table with row
 stride 0 (e.g. `table[None].expand(rows, -1)`) marks rows that share one
 table; they are tiled together so each key page is staged once per 8 rows.
-Per-row tables of more than 512 rows (a prefill chunk's fine tables) are
-planned per 8-row group over the union of their pages, staged the same way.
+Per-row tables of more than 512 rows with more than 16 heads (a prefill
+chunk's fine tables) are planned per 8-row group over the union of their
+pages, staged the same way.
 """
 import ctypes
 

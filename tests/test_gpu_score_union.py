@@ -105,6 +105,8 @@ def _run(dev, q8, w, native, table, lens, width, relu, clean, fill=7.0):
     (560, 64, 64, True, True, 44, 0),     # 64 heads: one query per wave
     (1031, 64, 4, True, False, 30, 4),    # 64 heads, few live ones, unclean, partial last group
     (777, 64, 64, False, True, 30, 4),    # 64 heads, signed scores
+    (545, 50, 50, True, True, 40, 2),     # 50 heads: the one-row form with a partial head block
+    (530, 17, 17, True, False, 30, 4),    # 17 heads: two rows per wave, a partial head block
     (600, 16, 2, True, True, 30, 4),      # one head block: row by row
     (529, 7, 7, True, True, 30, 4),       # heads not a multiple of 16: row by row
 ])
