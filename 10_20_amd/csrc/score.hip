@@ -1231,7 +1231,7 @@ __global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, 
                     h = (h + 1) & (uint32_t)(hslots - 1);
                 }
                 if (found < 0) {
-                    overflow = 1;
+                    atomicOr(&overflow, 1);
                 } else {
                     const uint32_t rep = (atomicOr(&hbits[found], 1u << q) >> q) & 1u;
                     nrep += (int32_t)rep;
