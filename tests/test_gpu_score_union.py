@@ -213,3 +213,31 @@ def test_union_plan_probe_overflow_falls_back(dev):
     got = _run(dev, q8, w, native, table, lens, width, True, True)
     pool, tab = _padded(native, table, width)
     assert_scores_rel(got, O.paged_logits(q8, w, pool, tab, lens, width))
+
+
+@pytest.mark.parametrize("heads", [32, 64])
+def test_union_plan_repeats_and_empty_groups(dev, heads):
+    """Rows that list one page three times (each later slot in an entry of its
+    own), a group whose rows list no valid page at all (every live column
+    scores 0, nothing is staged), and a group of empty rows, beside ordinary
+    chunk rows."""
+    g = np.random.default_rng(heads + 3)
+    rows, pool_pages = 528, 200
+    q8, w = _queries(g, rows, heads, heads)
+    k8, ks = W.quantize_rows(g.standard_normal((pool_pages * 64, 128), dtype=np.float32))
+    native = W.pack_pages(k8, ks)
+    table = _tables(g, rows, pool_pages, shared_pages=40, take=30, private=2)
+    blocks = table.shape[1]
+    table[0, 3] = table[0, 9] = table[0, 17] = table[0, 1]       # three repeats in row 0
+    table[5, :6] = table[5, 10]                                   # a page six times in row 5
+    table[8:16] = -1                                              # group 1: no valid page
+    table[16:24, ::2] = pool_pages + 7                            # group 2: every other slot out of the pool
+    lens = g.integers(blocks * 32, blocks * 64 + 1, rows).astype(np.int32)
+    lens[24:32] = 0                                               # group 3: empty rows
+    width = blocks * 64 + 64
+    got = _run(dev, q8, w, native, table, lens, width, True, True)
+    pool, tab = _padded(native, table, width)
+    ref = O.paged_logits(q8, w, pool, tab, lens, width)
+    assert (got[8:16][np.isfinite(ref[8:16])] == 0).all()
+    assert np.isneginf(got[24:32]).all()
+    assert_scores_rel(got, ref)
