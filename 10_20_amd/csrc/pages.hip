@@ -287,55 +287,74 @@ __global__ void fine_table_kernel(const int32_t* rt, const void* selected, int32
 }
 
 // kernels.py:518-564 (tail_rows == NULL: every row owns its scratch, :407-441).
-// Block (row, p): copies tail-candidate page p of an owner row, 64 tokens x
-// (128 FP8 bytes + fp32 scale); slots past the candidate count become zero.
-// With indexed_end, the tail starts at the published index end instead of the
-// last whole 1024-token bucket (experiments/tail_union_lab_20261021/
+// Block (row, g): copies tail-candidate pages kPages*g .. +kPages-1 of an
+// owner row, 64 tokens x (128 FP8 bytes + fp32 scale) each; slots past the
+// candidate count become zero, pages past it (other than page 0) are left
+// untouched.  Every thread issues its page-table reads, then its 2*kPages
+// 16-byte loads and its scale load, then the stores.  With indexed_end, the
+// tail starts at the published index end instead of the last whole
+// 1024-token bucket (experiments/tail_union_lab_20261021/
 // baseline_published.py:21-61).
+// Measured: four pages per work-group for prefill-sized batches (1024 rows of
+// 2 or 34 candidate pages: 18.9 -> 8.4 and 18.7 -> 13.3 us, most of the
+// one-page grid's work-groups having nothing to copy), one page for a decode
+// batch (128 rows of up to 34 pages: 19.2 us, 20.9 with four).
+template <int kPages>
 __global__ __launch_bounds__(256) void stage_tail_kernel(const uint8_t* native, const int32_t* nt, const int32_t* lens,
                                                          const int32_t* indexed_end, uint8_t* fine,
                                                          const int32_t* tail_rows, int32_t capacity, int32_t np,
                                                          int32_t scratch, int32_t sink_cap, int32_t window,
                                                          int64_t native_pages, int64_t fine_pages) {
     const int64_t row = blockIdx.x;
-    const int32_t p = blockIdx.y;
+    constexpr int kChunks = kPages * 64 * 8 / 256;  // 16-byte chunks per thread
+    static_assert(kPages >= 1 && kPages <= 4, "one scale slot per thread of the first 64 * kPages");
+    const int32_t p0 = blockIdx.y * kPages;
     if (tail_rows != nullptr && tail_rows[row] != row) return;
     const int32_t n = lens[row];
     const int32_t sink = min(n, sink_cap);
     const int32_t indexed = indexed_end ? min(max(*indexed_end, 0), n) : max(n - 1, 0) / 1024 * 1024;
     const int32_t tail = max(sink, min(indexed, max(sink, n - window)));
     const int32_t count = sink + n - tail;
-    if (!(p * 64 < count || p == 0)) return;
-    const int64_t dst = capacity + row * scratch + p;
-    if (dst >= fine_pages) return;
-    uint8_t* out = fine + dst * V1_PAGE_BYTES;
-    // 64 tokens x 8 chunks of 16 bytes
-    for (int c = threadIdx.x; c < 64 * 8; c += 256) {
-        const int slot = c / 8, part = c % 8;
-        const int32_t i = p * 64 + slot;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (i < count) {
-            const int32_t logical = i < sink ? i : tail + i - sink;
-            const int32_t e = logical / 64;
-            const int64_t page = e < np ? nt[row * np + e] : -1;
-            if (page >= 0 && page < native_pages)
-                v = reinterpret_cast<const u32x4*>(native + page * V1_PAGE_BYTES + (logical % 64) * 128)[part];
-        }
-        reinterpret_cast<u32x4*>(out + slot * 128)[part] = v;
-    }
-    if (threadIdx.x < 64) {
-        const int slot = threadIdx.x;
-        const int32_t i = p * 64 + slot;
-        float s = 0.f;
-        if (i < count) {
-            const int32_t logical = i < sink ? i : tail + i - sink;
-            const int32_t e = logical / 64;
-            const int64_t page = e < np ? nt[row * np + e] : -1;
-            if (page >= 0 && page < native_pages)
-                s = reinterpret_cast<const float*>(native + page * V1_PAGE_BYTES + 8192)[logical % 64];
-        }
-        reinterpret_cast<float*>(out + 8192)[slot] = s;
-    }
+    if (!(p0 * 64 < count || p0 == 0)) return;
+    // page p of the row's scratch is written: inside the scratch and the pool,
+    // and holding candidates (page 0 always)
+    const int64_t dst0 = capacity + row * scratch + p0;
+    auto written = [&](int j) {
+        const int32_t p = p0 + j;
+        return p < scratch && (p * 64 < count || p == 0) && dst0 + j < fine_pages;
+    };
+    // the 128 key bytes of candidate slot i in the native pool (nullptr: a
+    // zero slot: past the count, or its page outside the table or the pool)
+    auto key_row = [&](int32_t i) -> const uint8_t* {
+        if (i >= count) return nullptr;
+        const int32_t logical = i < sink ? i : tail + i - sink;
+        const int32_t e = logical / 64;
+        const int64_t page = e < np ? nt[row * np + e] : -1;
+        if (page < 0 || page >= native_pages) return nullptr;
+        return native + page * V1_PAGE_BYTES + (logical % 64) * 128;
+    };
+    // chunk k of this thread: page p0 + c / 512, slot (c % 512) / 8, part c % 8
+    // with c = threadIdx.x + 256 k; the thread's scale is slot threadIdx.x % 64
+    // of page p0 + threadIdx.x / 64
+    const int t = (int)threadIdx.x;
+    const uint8_t* src[kChunks];
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k) src[k] = key_row((p0 + k / 2) * 64 + (t + 256 * (k % 2)) / 8);
+    const bool has_scale = t < 64 * kPages;
+    const uint8_t* ssrc = has_scale ? key_row((p0 + t / 64) * 64 + t % 64) : nullptr;
+    u32x4 v[kChunks];
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k)
+        v[k] = src[k] ? reinterpret_cast<const u32x4*>(src[k])[t % 8] : u32x4{0u, 0u, 0u, 0u};
+    // (the scale of the key row at token j of a page lies at byte 8192 + 4 j)
+    const int32_t si = (p0 + t / 64) * 64 + t % 64;
+    const int32_t sj = (si < sink ? si : tail + si - sink) % 64;
+    const float sc = ssrc ? reinterpret_cast<const float*>(ssrc - sj * 128 + 8192)[sj] : 0.f;
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k)
+        if (written(k / 2))
+            reinterpret_cast<u32x4*>(fine + (dst0 + k / 2) * V1_PAGE_BYTES + ((t + 256 * (k % 2)) / 8) * 128)[t % 8] = v[k];
+    if (has_scale && written(t / 64)) reinterpret_cast<float*>(fine + (dst0 + t / 64) * V1_PAGE_BYTES + 8192)[t % 64] = sc;
 }
 
 // stage_tail over pages of 64 rows of row_bytes each (MLA latent rows of 656
@@ -460,16 +479,31 @@ extern "C" int v1_fine_table(const int32_t* rt, const void* selected, int32_t se
     return V1_LAUNCHED("fine_table");
 }
 
+// Four pages per work-group from 512 rows on (prefill-sized batches), one
+// below (decode batches: more, shorter work-groups keep more of the rows'
+// pages in flight at once).
+static void launch_stage_tail(const uint8_t* native, const int32_t* nt, const int32_t* lens,
+                              const int32_t* indexed_end, uint8_t* fine, const int32_t* tail_rows, int32_t rows,
+                              int32_t capacity, int32_t np, int32_t scratch, int32_t sink, int32_t window,
+                              int64_t native_pages, int64_t fine_pages, hipStream_t st) {
+    if (rows >= 512)
+        hipLaunchKernelGGL(stage_tail_kernel<4>, dim3(rows, (uint32_t)cdiv(scratch, 4)), dim3(256), 0, st, native, nt,
+                           lens, indexed_end, fine, tail_rows, capacity, np, scratch, sink, window, native_pages,
+                           fine_pages);
+    else
+        hipLaunchKernelGGL(stage_tail_kernel<1>, dim3(rows, scratch), dim3(256), 0, st, native, nt, lens, indexed_end,
+                           fine, tail_rows, capacity, np, scratch, sink, window, native_pages, fine_pages);
+}
+
 extern "C" int v1_stage_tail(const uint8_t* native, const int32_t* nt, const int32_t* lens, uint8_t* fine,
                              const int32_t* tail_rows, int32_t rows, int32_t capacity, int32_t np, int32_t scratch,
                              int32_t sink, int32_t window, int64_t native_pages, int64_t fine_pages, void* stream) {
-    V1_REQUIRE(rows >= 0 && np > 0 && scratch > 0, "stage_tail: bad shape");
+    V1_REQUIRE(rows >= 0 && np > 0 && scratch > 0 && capacity >= 0, "stage_tail: bad shape");
     V1_REQUIRE((reinterpret_cast<uintptr_t>(native) & 15) == 0 && (reinterpret_cast<uintptr_t>(fine) & 15) == 0,
                "stage_tail: pools must be 16-byte aligned");
     if (rows == 0) return V1_OK;
-    hipLaunchKernelGGL(stage_tail_kernel, dim3(rows, scratch), dim3(256), 0, as_stream(stream), native, nt, lens,
-                       static_cast<const int32_t*>(nullptr), fine, tail_rows, capacity, np, scratch, sink, window,
-                       native_pages, fine_pages);
+    launch_stage_tail(native, nt, lens, nullptr, fine, tail_rows, rows, capacity, np, scratch, sink, window,
+                      native_pages, fine_pages, as_stream(stream));
     return V1_LAUNCHED("stage_tail");
 }
 
@@ -477,13 +511,13 @@ extern "C" int v1_stage_tail_published(const uint8_t* native, const int32_t* nt,
                                        const int32_t* indexed_end, uint8_t* fine, const int32_t* tail_rows,
                                        int32_t rows, int32_t capacity, int32_t np, int32_t scratch, int32_t sink,
                                        int32_t window, int64_t native_pages, int64_t fine_pages, void* stream) {
-    V1_REQUIRE(rows >= 0 && np > 0 && scratch > 0, "stage_tail_published: bad shape");
+    V1_REQUIRE(rows >= 0 && np > 0 && scratch > 0 && capacity >= 0, "stage_tail_published: bad shape");
     V1_REQUIRE(indexed_end != nullptr, "stage_tail_published: indexed_end is required");
     V1_REQUIRE((reinterpret_cast<uintptr_t>(native) & 15) == 0 && (reinterpret_cast<uintptr_t>(fine) & 15) == 0,
                "stage_tail_published: pools must be 16-byte aligned");
     if (rows == 0) return V1_OK;
-    hipLaunchKernelGGL(stage_tail_kernel, dim3(rows, scratch), dim3(256), 0, as_stream(stream), native, nt, lens,
-                       indexed_end, fine, tail_rows, capacity, np, scratch, sink, window, native_pages, fine_pages);
+    launch_stage_tail(native, nt, lens, indexed_end, fine, tail_rows, rows, capacity, np, scratch, sink, window,
+                      native_pages, fine_pages, as_stream(stream));
     return V1_LAUNCHED("stage_tail_published");
 }
 

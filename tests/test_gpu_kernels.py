@@ -575,6 +575,34 @@ def test_stage_tail_and_tables_random_vs_oracle(dev):
         assert np.array_equal(H(ft), exp)
 
 
+@pytest.mark.parametrize("rows", [9, 520])
+def test_stage_tail_page_groups_and_pool_edges(dev, rows):
+    """Both work-group shapes of the staging kernel (one page per work-group
+    below 512 rows, four from 512 on): scratch widths that are not a multiple
+    of four pages, candidate counts that end inside a group or past the
+    scratch, table entries past the native pool (their slots read as zeros)
+    and a fine pool that ends inside the last row's scratch (pages past it are
+    not written)."""
+    g = np.random.default_rng(21 + rows)
+    np_, cap, native_pages, extra = 12, 7, 50, 6
+    cases = ((6, 300), (5, 200), (9, 520), (1, 100)) if rows < 512 else ((6, 300), (9, 520))
+    for scratch, window in cases:
+        native = g.integers(0, 256, (native_pages, 8448), dtype=np.uint8)
+        nt = g.integers(0, native_pages + extra, (rows, np_)).astype(np.int32)
+        lens = g.integers(1, np_ * 64 + 1, rows).astype(np.int32)
+        full = cap + rows * scratch
+        fine_pages = full - 3
+        out = T(np.full((fine_pages, 8448), 5, np.uint8), dev)
+        K.stage_tail[(rows, scratch)](T(native, dev), None, T(nt, dev), T(lens, dev), out, None, cap, np_, scratch,
+                                      64, window)
+        # the oracle over a pool padded with zero pages: a table entry past the
+        # kernel's pool then reads zeros, as the kernel's range check gives
+        padded = np.concatenate([native, np.zeros((extra, 8448), np.uint8)])
+        exp = np.full((full, 8448), 5, np.uint8)
+        O.stage_tail(padded, nt, lens, exp, cap, scratch, 64, window)
+        assert np.array_equal(H(out), exp[:fine_pages]), (scratch, window)
+
+
 def test_query_metadata_vs_oracle(dev):
     g = np.random.default_rng(9)
     rows, NP = 50, 256
