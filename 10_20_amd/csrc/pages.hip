@@ -380,19 +380,34 @@ __global__ __launch_bounds__(256) void stage_tail_rows_kernel(const uint8_t* nat
     if (dst >= fine_pages) return;
     const int64_t page_bytes = (int64_t)row_bytes * 64;
     const int32_t parts = row_bytes / 16;
+    const int32_t total = 64 * parts;
     u32x4* out = reinterpret_cast<u32x4*>(fine + dst * page_bytes);
-    for (int32_t c = threadIdx.x; c < 64 * parts; c += 256) {
-        const int32_t slot = c / parts, part = c - slot * parts;
-        const int32_t i = p * 64 + slot;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (i < count) {
-            const int32_t logical = i < sink ? i : tail + i - sink;
-            const int32_t e = logical / 64;
-            const int64_t page = e < np ? nt[row * np + e] : -1;
-            if (page >= 0 && page < native_pages)
-                v = reinterpret_cast<const u32x4*>(native + page * page_bytes + (int64_t)(logical % 64) * row_bytes)[part];
+    // kBatch chunks per thread at a time: their sources first (page-table
+    // reads), then all their loads, then the stores
+    constexpr int kBatch = 8;
+    for (int32_t c0 = threadIdx.x; c0 < total; c0 += 256 * kBatch) {
+        const u32x4* src[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int32_t c = c0 + 256 * k;
+            const int32_t slot = c / parts, part = c - slot * parts;
+            const int32_t i = p * 64 + slot;
+            src[k] = nullptr;
+            if (c < total && i < count) {
+                const int32_t logical = i < sink ? i : tail + i - sink;
+                const int32_t e = logical / 64;
+                const int64_t page = e < np ? nt[row * np + e] : -1;
+                if (page >= 0 && page < native_pages)
+                    src[k] = reinterpret_cast<const u32x4*>(native + page * page_bytes +
+                                                            (int64_t)(logical % 64) * row_bytes) + part;
+            }
         }
-        out[c] = v;
+        u32x4 v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) v[k] = src[k] ? *src[k] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k)
+            if (c0 + 256 * k < total) out[c0 + 256 * k] = v[k];
     }
 }
 
