@@ -8,7 +8,7 @@
 // candidates take every candidate (sglang/kernels/jit/csrc/deepseek_v4/
 // topk_v2.cuh:136-143).
 //
-// Design: one 512-thread work-group selects over up to 32768 positions with
+// Design: one 512-thread work-group selects over up to 40960 positions with
 // under 40 KiB of LDS, so four work-groups (rows) share a CU and the HBM
 // streams of some rows overlap the LDS selection of others.
 //  1. 2048 keys sampled in 64 runs of 32 (one 128-byte line each: 8 KB of a
@@ -27,8 +27,10 @@
 // it) a second pivot, aimed by the observed count, is streamed once more; a
 // second miss runs the same steps exactly on the whole row (statistics, radix
 // passes), streamed again.
-// Rows longer than 32768 columns are cut into 32768-column segments whose
-// Top-T land in a workspace; a merge work-group selects from their union.
+// Rows longer than 40960 columns (32768 in batches of fewer than 512 rows,
+// where more, shorter segments keep more of the GPU busy) are cut into
+// segments whose Top-T land in a workspace; a merge work-group selects from
+// their union.
 #include <algorithm>
 #include <cstddef>
 
@@ -39,10 +41,11 @@ namespace {
 
 constexpr int kBlock = 512;
 constexpr int kWaves = kBlock / kWave;  // 8
-constexpr int kSpan = 32768;            // positions one work-group selects over
+constexpr int kSpan = 40960;            // positions one work-group selects over
 constexpr int kWords = kSpan / 32;      // position bitmap words
-constexpr int kDigitBits = 11;          // radix digit width
-constexpr int kHist = 1 << kDigitBits;  // histogram bins, 4 per thread
+constexpr int kDigitBits = 10;          // radix digit width
+constexpr int kHist = 1 << kDigitBits;  // histogram bins, 2 per thread
+constexpr int kHistWords = kHist > kWords ? kHist : kWords;  // histograms; bitmap word prefixes
 constexpr int kCandMax = 3584;
 constexpr int kCandPerThread = kCandMax / kBlock;  // 7
 constexpr int kSampleRuns = 64;                    // pivot sample: runs of 32 keys (128 bytes)
@@ -54,11 +57,11 @@ constexpr uint32_t kNegInfBits = 0xff800000u;  // float bits of -inf
 // offsets at or past the descriptor's length return zeros.
 constexpr int32_t kRawDword = 0x00020000;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-static_assert(kHist == 4 * kBlock && kWords % kBlock == 0 && kCandMax % kBlock == 0, "work split");
+static_assert(kHist % kBlock == 0 && kWords % 256 == 0 && kCandMax % kBlock == 0, "work split");
 static_assert(kSampleRuns * 32 == 4 * kBlock, "eight threads per sample run");
 
 struct alignas(16) SelSmem {  // (arrays at 16-byte offsets: read as 16-byte words)
-    uint32_t hist[kHist];      // radix histograms; bitmap word prefixes
+    uint32_t hist[kHistWords];  // radix histograms; bitmap word prefixes
     uint32_t cand_key[kCandMax];  // (after the ranks of a transform row: its selected positions in slot order)
     uint16_t cand_pos[kCandMax];
     uint32_t gt_bits[kWords];  // positions with key > tau
@@ -140,10 +143,11 @@ __device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& b
                                          uint32_t& inbin) {
     if (threadIdx.x < kWave) {
         const int lane = threadIdx.x;
-        uint4* h4 = reinterpret_cast<uint4*>(sm.hist + kHist - 32 * (lane + 1));
+        constexpr int kPer = kHist / kWave;  // bins per lane
+        uint4* h4 = reinterpret_cast<uint4*>(sm.hist + kHist - kPer * (lane + 1));
         uint32_t local = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < kPer / 4; ++i) {
             const uint4 v = h4[i];
             local += v.x + v.y + v.z + v.w;
         }
@@ -152,10 +156,10 @@ __device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& b
         if (own != 0) {
             const int L = (int)__builtin_ctzll(own);
             const uint32_t excl = readlane(incl - local, L);
-            const uint32_t top = (uint32_t)(kHist - 1 - 32 * L);
-            const uint32_t c = lane < 32 ? sm.hist[top - lane] : 0u;
+            const uint32_t top = (uint32_t)(kHist - 1 - kPer * L);
+            const uint32_t c = lane < kPer ? sm.hist[top - lane] : 0u;
             const uint32_t ci = wave_inclusive_sum(c);
-            const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < 32 && excl + ci >= rank);
+            const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < kPer && excl + ci >= rank);
             if (lane == (int)__builtin_ctzll(hit)) {
                 sm.bc[0] = top - lane;
                 sm.bc[1] = excl + ci - c;
@@ -164,7 +168,7 @@ __device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& b
         }
         // (after the reads above: one wave's LDS accesses complete in order)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) h4[i] = make_uint4(0u, 0u, 0u, 0u);
+        for (int i = 0; i < kPer / 4; ++i) h4[i] = make_uint4(0u, 0u, 0u, 0u);
         if (threadIdx.x == 0) sm.bc[3] = 0;  // append counter of small_bin_select
     }
     __syncthreads();
@@ -175,7 +179,7 @@ __device__ __forceinline__ void find_bin(uint32_t rank, SelSmem& sm, uint32_t& b
 
 __device__ __forceinline__ void clear_hist(SelSmem& sm) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sm.hist[threadIdx.x + i * kBlock] = 0;
+    for (int i = 0; i < kHist / kBlock; ++i) sm.hist[threadIdx.x + i * kBlock] = 0;
 }
 
 // Digit window of a pass: bits [shift, shift+bits) under the fixed prefix.
@@ -215,10 +219,9 @@ struct Radix {
 // then visits each marked item again and writes it to its slot.
 struct Ranker {
     __device__ __forceinline__ static void clear(SelSmem& sm) {
-#pragma unroll
-        for (int i = 0; i < kWords / kBlock; ++i) {
-            sm.gt_bits[threadIdx.x + i * kBlock] = 0;
-            sm.eq_bits[threadIdx.x + i * kBlock] = 0;
+        for (int i = threadIdx.x; i < kWords; i += kBlock) {
+            sm.gt_bits[i] = 0;
+            sm.eq_bits[i] = 0;
         }
     }
     __device__ __forceinline__ static void mark(SelSmem& sm, uint32_t pos, bool gt, bool eq) {
@@ -226,17 +229,19 @@ struct Ranker {
         if (eq) atomicOr(&sm.eq_bits[pos >> 5], 1u << (pos & 31));
     }
     // word prefixes: hist[w] = packed (gt | eq << 16) count before word w;
-    // wave 0 scans the 1024 words, 16 per lane
+    // wave 0 scans the kWords words, kWords / 64 per lane
     __device__ __forceinline__ static void scan(SelSmem& sm) {
         if (threadIdx.x < kWave) {
             const int lane = threadIdx.x;
-            // (16-byte LDS accesses: words 16 lane .. 16 lane + 15)
-            const uint4* g4 = reinterpret_cast<const uint4*>(sm.gt_bits + 16 * lane);
-            const uint4* e4 = reinterpret_cast<const uint4*>(sm.eq_bits + 16 * lane);
-            uint32_t c[16];
+            constexpr int kWpl = kWords / kWave;  // words per lane
+            static_assert(kWpl % 4 == 0, "16-byte LDS words");
+            // (16-byte LDS accesses: words kWpl lane .. kWpl lane + kWpl - 1)
+            const uint4* g4 = reinterpret_cast<const uint4*>(sm.gt_bits + kWpl * lane);
+            const uint4* e4 = reinterpret_cast<const uint4*>(sm.eq_bits + kWpl * lane);
+            uint32_t c[kWpl];
             uint32_t local = 0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < kWpl / 4; ++q) {
                 const uint4 g = g4[q], e = e4[q];
                 c[4 * q + 0] = (uint32_t)__popc(g.x) | ((uint32_t)__popc(e.x) << 16);
                 c[4 * q + 1] = (uint32_t)__popc(g.y) | ((uint32_t)__popc(e.y) << 16);
@@ -245,9 +250,9 @@ struct Ranker {
                 local += c[4 * q] + c[4 * q + 1] + c[4 * q + 2] + c[4 * q + 3];
             }
             uint32_t run = wave_inclusive_sum(local) - local;
-            uint4* h4 = reinterpret_cast<uint4*>(sm.hist + 16 * lane);
+            uint4* h4 = reinterpret_cast<uint4*>(sm.hist + kWpl * lane);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < kWpl / 4; ++q) {
                 uint4 o;
                 o.x = run;
                 run += c[4 * q];
@@ -1190,12 +1195,14 @@ __global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
     int32_t* out = p.page_indices + row * p.topk;
     int32_t* raws = p.raw_indices ? p.raw_indices + row * p.topk : nullptr;
     // Pages of at least 64 positions: the row's page table (at most
-    // kSpan / 64 = kBlock entries) is staged in LDS (the mask-page array,
+    // kSpan / 64 <= 2 kBlock entries) is staged in LDS (the mask-page array,
     // unused by plain rows), its loads issued with the pivot sample's.
     const int bits = p.page_bits;
     const bool staged = bits >= kTableBits;
     const int32_t entries = staged ? min(p.page_table_cols, kSpan >> bits) : 0;
     const int32_t entry = (int32_t)threadIdx.x < entries ? table[threadIdx.x] : 0;
+    const int32_t entry2 = (int32_t)threadIdx.x + kBlock < entries ? table[threadIdx.x + kBlock] : 0;
+    static_assert(kSpan / 64 <= 2 * kBlock, "two table entries per thread");
     auto emit = [&](const auto& at, const auto& pos, const auto&) {
         constexpr int N = sizeof(at) / sizeof(at[0]);
         int32_t raw[N];
@@ -1213,12 +1220,18 @@ __global__ __launch_bounds__(kBlock, 8) void transform_rows(TransformParams p) {
         }
     };
     if constexpr (kShortRows) {
-        if (staged) sm.maskpage[threadIdx.x] = entry;  // read after select_short's first barrier
+        if (staged) {  // read after select_short's first barrier
+            sm.maskpage[threadIdx.x] = entry;
+            if ((int32_t)threadIdx.x + kBlock < kSpan / 64) sm.maskpage[threadIdx.x + kBlock] = entry2;
+        }
         select_short(src, (uint32_t)T, sm, emit);
     } else {
         uint32_t sk[4];
         src.load4(sample_pos(L), sk);
-        if (staged) sm.maskpage[threadIdx.x] = entry;  // read after select_sampled's first barrier
+        if (staged) {  // read after select_sampled's first barrier
+            sm.maskpage[threadIdx.x] = entry;
+            if ((int32_t)threadIdx.x + kBlock < kSpan / 64) sm.maskpage[threadIdx.x + kBlock] = entry2;
+        }
         select_sampled(src, sk, (uint32_t)T, sm, emit);
     }
     if (!staged) return;
@@ -1261,16 +1274,21 @@ struct Workspace {
     __device__ __forceinline__ int64_t at(int64_t row, int32_t s) const { return (row * nseg + s) * (int64_t)T; }
 };
 
-// Segments of a row: the fewest that keep each within kSpan columns (more
-// segments make the merge, which selects over nseg * topk candidates, cost as
-// much as they save).  One segment means the single-pass kernel.
+// Segments of a row: the fewest that keep each within segment_span columns
+// (more segments make the merge, which selects over nseg * topk candidates,
+// cost as much as they save).  One segment means the single-pass kernel.
 struct SegPlan {
     int32_t nseg, seg;
 };
+// Longest segment: the work-group's whole span for batches of 512 rows or
+// more; 32768 columns below, where more, shorter segments keep more of the
+// GPU busy.  Measured: 1024 rows of 34880 columns in one pass 57 us against
+// 108 us as two segments and a merge; 128 rows of up to 67K columns 48 us as
+// three segments of at most 32768 columns against 51 us as two.
+inline int64_t segment_span(int32_t batch) { return batch >= 512 ? kSpan : 32768; }
 inline SegPlan plan_segments(int32_t batch, int32_t cols, int32_t topk) {
-    (void)batch;
     (void)topk;
-    const int64_t nseg = cdiv(cols, kSpan);
+    const int64_t nseg = cdiv(cols, segment_span(batch));
     if (nseg <= 1) return SegPlan{1, cols};
     const int64_t seg = cdiv(cdiv(cols, nseg), 64) * 64;
     return SegPlan{(int32_t)cdiv(cols, seg), (int32_t)seg};
@@ -1582,7 +1600,7 @@ int launch_topk(void (*single)(P), void (*single_short)(P), void (*seg)(P, Works
     V1_REQUIRE((reinterpret_cast<uintptr_t>(wsp) & 15) == 0, "%s: the workspace must be 16-byte aligned", name);
     const Workspace ws = make_workspace(wsp, batch, plan, topk);
     V1_REQUIRE((int64_t)ws.nseg * topk <= kSpan, "%s: %d columns exceed the %lld supported at topk %d", name, cols,
-               (long long)(kSpan / topk) * kSpan, topk);
+               (long long)(kSpan / topk) * segment_span(batch), topk);
     hipLaunchKernelGGL(seg, dim3(ws.nseg, batch), dim3(kBlock), 0, st, p, ws);
     int rc = V1_LAUNCHED(name);
     if (rc != V1_OK) return rc;

@@ -104,7 +104,7 @@ typedef struct {
     const int32_t* fine_table; /* [batch, fine_table_cols] */
     int32_t fine_table_cols;
     int32_t direct_fine;
-    void* workspace;           /* rows longer than 32768 columns: >= v1_topk_workspace() bytes */
+    void* workspace;           /* split rows: >= v1_topk_workspace() bytes (0 when no row is split) */
     int64_t workspace_bytes;
 } v1_topk_args;
 int64_t v1_topk_workspace(int32_t batch, int32_t cols, int32_t topk);
@@ -116,9 +116,10 @@ int v1_topk(const v1_topk_args* a, void* stream);
  * Replaces TopKKernel::transform / topk_transform_512_v2
  *   sglang/kernels/jit/csrc/deepseek_v4/topk_v2.cuh:352-460,
  *   sglang/kernels/jit/include/sgl_kernel/deepseek_v4/topk_impl.cuh:156-190.
- * Rows longer than one work-group's register tile are split over several
- * work-groups; `workspace` (device memory, >= v1_topk_workspace() bytes)
- * then holds the per-segment candidates.
+ * A work-group selects over up to 40960 columns; longer rows (and, in
+ * batches of fewer than 512 rows, rows over 32768 columns) are split over
+ * several work-groups, and `workspace` (device memory, >= v1_topk_workspace()
+ * bytes) then holds the per-segment candidates.
  * ---------------------------------------------------------------------- */
 typedef struct {
     const float* scores;        /* [batch, cols], row stride score_stride */

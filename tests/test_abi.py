@@ -82,6 +82,9 @@ def test_workspace_sizes_are_host_arithmetic(lib):
     assert h.v1_topk_workspace(4096, 32768, 2048) == 0       # large batch: one work-group per row
     assert h.v1_topk_workspace(4096, 65536, 2048) == 4096 * 2 * (2048 * 8 + 4)
     assert h.v1_topk_workspace(128, 131072, 2048) == 128 * 4 * (2048 * 8 + 4)
+    # rows up to 40960 columns: one pass from 512 rows on, segments of at most 32768 columns below
+    assert h.v1_topk_workspace(1024, 34880, 2048) == 0
+    assert h.v1_topk_workspace(128, 34880, 2048) == 128 * 2 * (2048 * 8 + 4)
     assert h.v1_score_workspace(4096, 32768) >= 4096 * (8 * 128 + 8 * 4 + 16 * 4)
     # per-row tables: the page-union plan only for more than 512 rows of at most 65536 columns
     assert h.v1_score_tables_workspace(512, 34880) == 0

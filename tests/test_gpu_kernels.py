@@ -299,9 +299,10 @@ def _v1_case(g, B, cols, take_max, ties):
                                              (20000, 2048, True), (32768, 2048, False), (70000, 2048, True),
                                              (40000, 512, False), (200000, 2048, True)])
 def test_fused_topk_random_vs_oracle(dev, cols, topk, ties):
-    """Register-resident rows (<= 8192 columns), streamed rows, and segmented
-    rows whose merge holds the candidates in registers (<= 4 segments at
-    T = 2048) or streams them (7 segments at 200000 columns)."""
+    """Register-resident rows (<= 8192 columns), streamed rows (one pass up to
+    40960 columns in a batch of 513 rows), and segmented rows whose merge
+    holds the candidates in registers (<= 4 segments at T = 2048) or streams
+    them (5 segments at 200000 columns)."""
     g = np.random.default_rng(cols + topk)
     B = 513
     c = _v1_case(g, B, cols, 40, ties)
@@ -793,12 +794,13 @@ def test_topk_adversarial_rows(dev, kind, cols):
     assert np.array_equal(H(raw), e_raw) and np.array_equal(H(out), e_out)
 
 
-@pytest.mark.parametrize("cols", [2100, 9000, 32768])
+@pytest.mark.parametrize("cols", [2100, 9000, 32768, 40960])
 def test_topk_large_batch_vs_oracle(dev, cols):
     """1100 rows (more than four per CU) of varying lengths with every
     adversarial row kind mixed in (their pivot misses take the re-aimed pivot
     or the exact passes), rows of at most T candidates and a padded row
-    stride; every row compared with the oracle."""
+    stride, up to the 40960 columns one work-group selects over (a 640-entry
+    page table); every row compared with the oracle."""
     g = np.random.default_rng(cols + 7)
     B = 1100
     stride = -(-cols // 4) * 4 + 4
@@ -824,7 +826,7 @@ def test_topk_large_batch_vs_oracle(dev, cols):
 
 @pytest.mark.parametrize("page_size", [16, 64, 128, 1024])
 @pytest.mark.parametrize("short_table", [False, True])
-@pytest.mark.parametrize("cols", [32768, 6000])
+@pytest.mark.parametrize("cols", [32768, 6000, 40000])
 def test_topk_transform_page_sizes(dev, page_size, short_table, cols):
     """Page sizes either side of 64 tokens (the register-resident rows take
     tables of at most 512 entries, smaller pages stream), a page table that
