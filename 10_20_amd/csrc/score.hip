@@ -145,7 +145,9 @@ __device__ __forceinline__ float wave_all(float v, Op op) {
 }
 
 // One wave per query row: q' = sum_h w_h q_h split into its pieces, and the
-// record described above.
+// record described above.  relu: 1 the fold (halved weights, pieces, the
+// exact-path threshold); 0 (no ReLU) or 2 (ReLU taken directly, one head
+// block) the weights alone.
 __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float* w, int32_t rows, int32_t heads,
                                                   int32_t relu, uint8_t* out, uint32_t* work, uint32_t* exact_pages,
                                                   int32_t exact_words, uint32_t* clear, int32_t nclear) {
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float*
     }
     bound = wave_all(bound, [](float x, float y) { return x + y; });
     uint8_t* dst = out + row * kPieceRowBytes;
-    for (int pc = 0; pc < kPieces; ++pc) {
+    for (int pc = 0; pc < (relu == 1 ? kPieces : 0); ++pc) {
         const float m = wave_all(fmaxf(fabsf(a0), fabsf(a1)), [](float x, float y) { return fmaxf(x, y); });
         // scale: smallest power of two >= m / 448 (1 when the residual is zero)
         float sc = 1.f;
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(256) void score_prep(const uint8_t* q, const float*
         a0 -= sc * e4m3_value(c0);
         a1 -= sc * e4m3_value(c1);
     }
-    reinterpret_cast<float*>(dst + kRecWeights)[l] = l < heads ? (relu ? 0.5f : 1.f) * w[row * heads + l] : 0.f;
+    reinterpret_cast<float*>(dst + kRecWeights)[l] = l < heads ? (relu == 1 ? 0.5f : 1.f) * w[row * heads + l] : 0.f;
     if (l < 4) reinterpret_cast<float*>(dst + kRecBound)[l] = l == 0 ? kExactFrac * 448.f * bound : 0.f;
 }
 
@@ -371,6 +373,12 @@ static_assert(kUnionRange == kWave && kUnionRange <= kMaxRangePages, "one union 
 template <int HB, bool RELU, bool UNION = false, int QPW = kQueriesPerWave>
 __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(ScoreParams p) {
     static_assert(QPW == 2 || (QPW == 1 && UNION), "one query per wave: the union form");
+    // ReLU through the linear term + |x| fold (and score_exact for exact
+    // zeros) from two head blocks on; with one head block each result is
+    // taken as w * max(x, 0) directly (exactly 0 when no head dot is
+    // positive): its VALU cost is that of the fold's, and it saves the
+    // linear-term MFMA (a third of the block's) and the exact pass.
+    constexpr bool kFold = RELU && HB > 1;
     constexpr int kWaves = kQueriesPerGroup / QPW;
     constexpr int kBlock = kWave * kWaves;
     constexpr int kKeyDma = 8 / kWaves;       // 1 KiB key chunks per wave and page
@@ -390,9 +398,9 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
     // ReLU path: per query of the group, a bitmap of the item's pages that
     // hold a key marked for the exact form (bit (page_begin % 32) + page);
     // all zero between items.
-    __shared__ uint32_t marks[RELU && !UNION ? kQueriesPerGroup * kMarkWords : 1];
+    __shared__ uint32_t marks[kFold && !UNION ? kQueriesPerGroup * kMarkWords : 1];
     const int t = threadIdx.x, l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    if (RELU && !UNION)
+    if (kFold && !UNION)
         for (int i = t; i < kQueriesPerGroup * kMarkWords; i += kBlock) marks[i] = 0u;
     // union items per level (final before this kernel starts)
     int32_t lvl_n[UNION ? kUnionLevels : 1];
@@ -487,14 +495,14 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
 #pragma unroll
             for (int i = 0; i < 4; ++i) w[q][hb][i] = x[i];
         }
-        if (RELU) {
+        if (kFold) {
             const float2 x = *reinterpret_cast<const float2*>(rec + kRecScales + 8 * (l >> 4));
             coef[2 * q] = x.x;
             coef[2 * q + 1] = x.y;
             exact_thr[q] = *reinterpret_cast<const float*>(rec + kRecBound);  // the same for every lane
         }
     }
-    if (RELU) {
+    if (kFold) {
         const int rr = l & 15;
         const int64_t rq = min(row0 + wv * QPW + (QPW == 2 ? (rr >> 1) & 1 : 0), (int64_t)p.rows - 1);
         const int piece = 2 * (rr >> 2) + (rr & 1);
@@ -587,7 +595,7 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
     // pipe keeps working while the VALU folds older results; the stream runs
     // on across pages, the first kLag slots of a page finishing the previous
     // page's partials.
-    constexpr int kPer = (RELU ? 1 : 0) + QPW * HB;
+    constexpr int kPer = (kFold ? 1 : 0) + QPW * HB;
     constexpr int kTotal = 4 * kPer;
     constexpr int kLag = 3;
     static_assert(kTotal % (kLag + 1) == 0 && kTotal > kLag + 4, "result ring continues across pages");
@@ -600,22 +608,22 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
     for (int k = 0; k <= kLag; ++k) d[k] = v4f{0.f, 0.f, 0.f, 0.f};
     auto mfma_at = [&](int idx, const Frag& f) __attribute__((always_inline)) {
         const int kb = idx / kPer, r = idx % kPer;
-        const int rr = RELU ? max(r - 1, 0) : r;  // head block (r == 0 is the linear-term block)
-        d[idx % (kLag + 1)] = (RELU && r == 0) ? mfma_fp8(alin, f.b[kb]) : mfma_fp8(a[rr / HB][rr % HB], f.b[kb]);
+        const int rr = kFold ? max(r - 1, 0) : r;  // head block (r == 0 is the linear-term block)
+        d[idx % (kLag + 1)] = (kFold && r == 0) ? mfma_fp8(alin, f.b[kb]) : mfma_fp8(a[rr / HB][rr % HB], f.b[kb]);
     };
     auto consume = [&](int jj, float (&part)[QPW][4]) __attribute__((always_inline)) {
         const int kb = jj / kPer, r = jj % kPer;
         const v4f x = d[jj % (kLag + 1)];
-        if (RELU && r == 0) {
+        if (kFold && r == 0) {
 #pragma unroll
             for (int q = 0; q < QPW; ++q) part[q][kb] = fmaf(coef[2 * q + 1], x[2 * q + 1], coef[2 * q] * x[2 * q]);
         } else {
-            const int rr = RELU ? r - 1 : r;
+            const int rr = kFold ? r - 1 : r;
             const int q = rr / HB, hb = rr % HB;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float prev = (!RELU && hb == 0 && i == 0) ? 0.f : part[q][kb];
-                part[q][kb] = fmaf(w[q][hb][i], RELU ? fabsf(x[i]) : x[i], prev);
+                const float prev = (!kFold && hb == 0 && i == 0) ? 0.f : part[q][kb];
+                part[q][kb] = fmaf(w[q][hb][i], kFold ? fabsf(x[i]) : RELU ? relu(x[i]) : x[i], prev);
             }
         }
     };
@@ -654,7 +662,7 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
                                                               lim * 4, kRawDword);
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l < valid ? v * scale : -__builtin_huge_valf()), rs,
                                                   l * 4, 0, 0);
-            if (RELU) {
+            if (kFold) {
                 // (ballots of the bare compares stay scalar masks; the
                 // uniform conditions join on the scalar side)
                 const uint64_t near = __builtin_amdgcn_ballot_w64(fabsf(v) <= exact_thr[q]) &
@@ -867,7 +875,7 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
     fill_rest(npages);
     if constexpr (UNION) {
         // marked pages to the rows' page bitmaps, at each row's table slot
-        if (RELU) {
+        if (kFold) {
             const int32_t words = (((p.max_context_len + 63) >> 6) + 31) >> 5;
 #pragma unroll
             for (int q = 0; q < QPW; ++q) {
@@ -888,7 +896,7 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
     // (The bitmaps' row length follows from max_context_len.)
     int lane = l;
     asm volatile("" : "+v"(lane));  // keeps the lane arithmetic below inside the loop
-    if (RELU && lane < QPW * kMarkWords) {
+    if (kFold && lane < QPW * kMarkWords) {
         const int q = lane / kMarkWords, k = lane % kMarkWords;
         const uint32_t bits = marks[(wv * QPW + q) * kMarkWords + k];
         if (bits != 0u) {
@@ -1652,17 +1660,19 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         p.pieces = ws;
         p.work = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes);
         p.exact_pages = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes + 256);
-        p.exact_words = a->relu ? exact_words(a->max_context_len) : 0;
+        // ReLU: the linear term + |x| fold and score_exact from 17 heads on,
+        // ReLU taken directly with one head block (score_shared's kFold)
+        const bool fold = a->relu && hb > 1;
+        p.exact_words = fold ? exact_words(a->max_context_len) : 0;
         const dim3 row_waves((uint32_t)cdiv(a->rows, 4));
-        hipLaunchKernelGGL(score_prep, row_waves, dim3(256), 0, st, a->q, a->weights, a->rows, a->heads, a->relu, ws,
-                           p.work, p.exact_pages, p.exact_words, nullptr, 0);
+        hipLaunchKernelGGL(score_prep, row_waves, dim3(256), 0, st, a->q, a->weights, a->rows, a->heads,
+                           fold ? 1 : a->relu ? 2 : 0, ws, p.work, p.exact_pages, p.exact_words, nullptr, 0);
         int rc = V1_LAUNCHED("score_prep");
         if (rc != V1_OK) return rc;
         launch_hb<Shared>(hb, a->relu != 0, dim3((uint32_t)std::min<int64_t>(items, wgs)), st, p);
         rc = V1_LAUNCHED("score_shared");
-        if (rc != V1_OK || !a->relu) return rc;
+        if (rc != V1_OK || !fold) return rc;
         switch (hb) {
-            case 1: hipLaunchKernelGGL(score_exact<1>, row_waves, dim3(256), 0, st, p); break;
             case 2: hipLaunchKernelGGL(score_exact<2>, row_waves, dim3(256), 0, st, p); break;
             case 3: hipLaunchKernelGGL(score_exact<3>, row_waves, dim3(256), 0, st, p); break;
             default: hipLaunchKernelGGL(score_exact<4>, row_waves, dim3(256), 0, st, p); break;

@@ -640,7 +640,8 @@ def _score_case(g, rows, heads, ctx_max, shared, pool_pages):
 
 
 @pytest.mark.parametrize("rows,heads,ctx,shared", [(37, 64, 3000, True), (24, 64, 5000, False), (19, 1, 2688, False),
-                                                   (20, 32, 1100, True), (9, 16, 700, False)])
+                                                   (20, 32, 1100, True), (9, 16, 700, False), (33, 16, 2688, True),
+                                                   (25, 1, 2688, True)])
 def test_score_vs_dequantised_reference(dev, rows, heads, ctx, shared):
     g = np.random.default_rng(rows * heads + ctx)
     q8, w, native, table, lens = _score_case(g, rows, heads, ctx, shared, 200)
