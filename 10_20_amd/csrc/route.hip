@@ -73,14 +73,20 @@ __global__ __launch_bounds__(512) void route_kernel(v1_route_args a, int n_sort)
             v[i] = ((uint64_t)score_key(best) << 32) | (uint32_t)(0xffffffffu - (uint32_t)p);
         }
     }
-    bitonic_desc_regs<E>(v, n_sort, s0, s1, n_sort);
+    // Only the first n = pow2(active) slots are sorted: every slot past them
+    // holds a page at or past `active` (a -inf score) or padding, which the
+    // whole sort would leave in place (-inf pages in ascending order after
+    // every active page), so rank r >= n is page r.  (The network's steps
+    // pair slots below n only with each other.)
+    const int n = min(n_sort, active <= 2 ? 2 : 1 << (32 - __builtin_clz((uint32_t)(active - 1))));
+    bitonic_desc_regs<E>(v, n, s0, s1, n);
     // selected takes ranks < take_stride; the fine table every rank < take
     // (v1_query.cuh:44-48), bounded by the sorted pages and the table width
     const int32_t ft_ranks = a.fill_table ? min(min(take, a.pages), a.ft_cols) : 0;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
         const int r = e0 + i;
-        const int32_t p = (int32_t)(0xffffffffu - (uint32_t)v[i]);
+        const int32_t p = r < n ? (int32_t)(0xffffffffu - (uint32_t)v[i]) : r;
         if (r < a.take_stride) selected[r] = (Index)p;
         if (r < ft_ranks) ft[r] = rt[p];
     }

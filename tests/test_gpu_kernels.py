@@ -216,6 +216,28 @@ def test_route_random_vs_oracle(dev, pages, bits):
     assert np.array_equal(H(s_d), sel) and np.array_equal(H(f_d), ft)
 
 
+@pytest.mark.parametrize("pages", [256, 2048])
+def test_route_sorts_only_active_prefix(dev, pages):
+    """The route kernel sorts only the first power of two of slots that holds
+    a row's active pages; a selected array as wide as the table checks the
+    ranks past that prefix (pages at or past `active`, in ascending order)."""
+    g = np.random.default_rng(pages + 5)
+    actives = [16, 48, 80, 128, 144, pages // 2 + 16, pages]
+    B = len(actives)
+    scores = np.round(g.standard_normal((B, pages * 8)) * 3).astype(np.float32)
+    scores[g.random(scores.shape) < 0.02] = -np.inf
+    lens = (np.int32(actives) // 16 * 1024 + 1 + g.integers(0, 1024, B)).astype(np.int32)
+    takes = (np.int32(actives) // 2).astype(np.int32)
+    rt = g.integers(0, 10000, (B, pages)).astype(np.int32)
+    tail = np.arange(B, dtype=np.int32)
+    sel, ft = np.full((B, pages), -7, np.int32), np.full((B, pages + 68), -7, np.int32)
+    s_d, f_d = T(sel, dev), T(ft, dev)
+    O.route(scores, lens, takes, sel, pages, rt, ft, tail, 1000, True)
+    QF.module().route(T(scores, dev), T(lens, dev), T(takes, dev), s_d, pages, T(rt, dev), f_d, T(tail, dev), 1000,
+                      True)
+    assert np.array_equal(H(s_d), sel) and np.array_equal(H(f_d), ft)
+
+
 def test_route_rejects_like_reference(dev):
     m = QF.module()
     B = 4
