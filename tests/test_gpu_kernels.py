@@ -743,7 +743,7 @@ def assert_scores_close(got, ref, bound):
 
 
 def assert_scores_rel(got, ref):
-    """The north star's bound where every head weight is >= 0 (so every
+    """The score tolerance where every head weight is >= 0 (so every
     reference score is >= 0): each finite score within 1e-2 relative of the
     fp64 reference, exactly +0.0 (bit for bit) where the reference is 0, and
     the same -inf pattern."""
