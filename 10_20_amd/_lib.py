@@ -92,6 +92,8 @@ _SIGNATURES = {
     "v1_fine": (_c_i32, [ctypes.POINTER(FineArgs), _vp]),
     "v1_score_workspace": (_c_i64, [_c_i32, _c_i32]),
     "v1_score_tables_workspace": (_c_i64, [_c_i32, _c_i32]),
+    "v1_score_pages_workspace": (_c_i64, [_c_i32, _c_i32, _c_i64]),
+    "v1_score_page_major": (_c_i32, [_c_i32, ctypes.POINTER(_c_i32)]),
     "v1_score_noalloc": (_c_i32, [ctypes.POINTER(ScoreArgs), _vp]),
     "v1_score_noalloc_capacity": (_c_i64, []),
     "v1_gather_slots": (_c_i32, [_vp, _vp, _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32,

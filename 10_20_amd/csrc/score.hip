@@ -257,6 +257,34 @@ __device__ __forceinline__ void page_partials(const v8i (&a)[HB], const v8i (&b)
     }
 }
 
+// page_partials as one stream: MFMA idx (key block idx / HB, head block
+// idx % HB) goes to a ring of kLag + 1 result sets and is folded kLag MFMAs
+// after issue, so the MFMA pipe works while the VALU folds older results
+// (left alone, the compiler folds each result right after its MFMA and
+// waits for it).  The same products in the same order as page_partials:
+// the values are equal bit for bit.
+template <int HB, bool RELU>
+__device__ __forceinline__ void page_partials_lag(const v8i (&a)[HB], const v8i (&b)[4], const float (&w)[HB][4],
+                                                  float (&s)[4]) {
+    constexpr int kN = 4 * HB, kLag = 3;
+    v4f d[kLag + 1];
+#pragma unroll
+    for (int idx = 0; idx < kN + kLag; ++idx) {
+        if (idx < kN) d[idx % (kLag + 1)] = mfma_fp8(a[idx % HB], b[idx / HB]);
+        const int j = idx - kLag;
+        if (j >= 0) {
+            const v4f x = d[j % (kLag + 1)];
+            const int kb = j / HB, hb = j % HB;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float prev = (hb == 0 && i == 0) ? 0.f : s[kb];
+                s[kb] = fmaf(w[hb][i], RELU ? relu(x[i]) : x[i], prev);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // Reduce-scatter over the four 16-lane groups: lane g*16+c returns
 // sum over groups of s[g] at column c, i.e. the full head sum of key g*16+c.
 // permlane32_swap(x, y) exchanges the upper half of x with the lower half of
@@ -1021,7 +1049,7 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
                         part[kb] = acc;
                     }
                 } else {
-                    page_partials<HB, RELU>(a, b, w, part);
+                    page_partials_lag<HB, RELU>(a, b, w, part);
                 }
                 out = reduce_scatter4(part);
                 if (FAST && RELU) {
@@ -1372,6 +1400,261 @@ __global__ __launch_bounds__(kPlanThreads) void score_union_plan(ScoreParams p, 
     }
 }
 
+// ------------------------------------------- page-major per-row tables
+// Per-row tables of a large batch over a small pool (a prefill chunk's fine
+// tables over one request's pages).  A work item is (chunk c of kPmPages
+// consecutive pool pages, block of kPmRows rows): it stages the chunk's pages
+// in LDS once and computes every (row, listed page) pair of its rows from
+// them, so every MFMA serves a row that lists the page and a key page is read
+// from memory once per row block rather than once per row.  ReLU is taken
+// directly (w * max(x, 0), as score_rows does), so a key with no positive
+// head dot scores exactly 0 and no exact pass follows.
+//   score_pages_clear  empties the dense pair table and the overflow count;
+//   score_pages_place  one thread per (row, table slot): a listed pool page's
+//                      slot goes to table[chunk][row][page % kPmPages]; a
+//                      second slot of the same row and page goes to the
+//                      overflow list; columns no pair covers are written
+//                      (0 below the context: a slot past the table or out of
+//                      the pool reads as zeros; -inf past it with clean_logits);
+//   score_pages        the work items, plus one extra grid row that scores the
+//                      overflow pairs one wave per pair.
+constexpr int kPmPages = 8;
+constexpr int kPmWaves = 4;                // waves per work-group
+constexpr bool kPmPrefetch = true;         // the next row's loads issued before the current row
+constexpr int kPmRows = 16 * kPmWaves;     // rows per work item
+constexpr uint32_t kPmNone = 0xffffffffu;
+constexpr int64_t kPmMaxTableBytes = 64ll << 20;
+
+struct PmTables {
+    uint32_t* table;     // [chunks][rows][kPmPages] table slot of (row, pool page), kPmNone: not listed
+    uint32_t* overflow;  // (row << 16 | slot) of the pairs the table has no room for
+    uint32_t* count;     // overflow entries
+    int64_t table_words;  // 16-byte words of the table
+    int32_t chunks;
+};
+
+struct PmLayout {
+    int64_t count, overflow, table, total, table_words;
+    int32_t chunks;
+};
+PmLayout pm_layout(int32_t rows, int32_t max_context_len, int64_t kv_blocks) {
+    PmLayout L{};
+    L.chunks = (int32_t)cdiv(kv_blocks, kPmPages);
+    L.count = 0;
+    L.overflow = 256;
+    L.table = (L.overflow + (int64_t)rows * cdiv(max_context_len, 64) * 4 + 255) & ~int64_t(255);
+    const int64_t table_bytes = (int64_t)L.chunks * rows * kPmPages * 4;
+    L.table_words = table_bytes / 16;
+    L.total = L.table + table_bytes;
+    return L;
+}
+
+__global__ __launch_bounds__(256) void score_pages_clear(PmTables m) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    uint4* s = reinterpret_cast<uint4*>(m.table);
+    for (int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x; k < m.table_words; k += stride)
+        s[k] = make_uint4(kPmNone, kPmNone, kPmNone, kPmNone);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *m.count = 0;
+}
+
+__global__ __launch_bounds__(256) void score_pages_place(ScoreParams p, PmTables m) {
+    const int64_t row = blockIdx.y;
+    const int32_t j = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+    const int32_t all_pages = (p.max_context_len + 63) / 64;
+    if (j >= all_pages) return;
+    const int32_t ctx = min(p.ctx[row], p.max_context_len);
+    const int32_t row_pages = (ctx + 63) / 64;
+    const int32_t page = j < row_pages ? page_of(p, row, j) : -1;
+    if (page >= 0) {
+        uint32_t* at = m.table + (((int64_t)(page / kPmPages) * p.rows + row) * kPmPages + page % kPmPages);
+        if (atomicCAS(at, kPmNone, (uint32_t)j) != kPmNone) m.overflow[atomicAdd(m.count, 1u)] = (uint32_t)(row << 16) | (uint32_t)j;
+        return;
+    }
+    if (j >= row_pages && !p.clean) return;
+    for (int i = 0; i < 64; ++i) store_logit(p, row, j * 64 + i, ctx, 0.f);
+}
+
+template <int HB, bool RELU>
+__global__ __launch_bounds__(kWave * kPmWaves) void score_pages(ScoreParams p, PmTables m) {
+    __shared__ __attribute__((aligned(16))) uint8_t pages[kPmPages][V1_PAGE_BYTES];
+    __shared__ uint32_t used_sh;
+    constexpr int kBlock = kWave * kPmWaves;
+    const int t = threadIdx.x, l = __lane_id(), wv = __builtin_amdgcn_readfirstlane(t / kWave);
+    // B fragment of key block kb of a staged page: key kb*16 + l%16, chunks
+    // 2*(l/16) and +1 (stored swizzled, as score_shared stages them)
+    const int swz = key_swizzle(l & 15);
+    const int boff0 = (l & 15) * 128 + (((2 * (l >> 4)) ^ swz) << 4);
+    const int boff1 = (l & 15) * 128 + (((2 * (l >> 4) + 1) ^ swz) << 4);
+    if ((int32_t)blockIdx.y == m.chunks) {
+        // overflow pairs: one wave per pair, the page read straight from memory
+        const uint32_t n = *m.count;
+        for (uint32_t e = blockIdx.x * kPmWaves + wv; e < n; e += gridDim.x * kPmWaves) {
+            const uint32_t pr = m.overflow[e];
+            const int64_t row = pr >> 16;
+            const int32_t slot = (int32_t)(pr & 0xffffu);
+            const int32_t page = page_of(p, row, slot);
+            v8i a[HB], b[4];
+            float w[HB][4];
+            load_q<HB>(p, row, a);
+            load_w<HB>(p, row, w);
+            const uint8_t* base = p.kv + (int64_t)max(page, 0) * V1_PAGE_BYTES;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(base + (kb * 16 + (l & 15)) * 128 + 32 * (l >> 4));
+                const u32x4 x = src[0], y = src[1];
+                b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+            }
+            const float scale = reinterpret_cast<const float*>(base + 8192)[l];
+            float part[4];
+            page_partials_lag<HB, RELU>(a, b, w, part);
+            store_logit(p, row, slot * 64 + l, min(p.ctx[row], p.max_context_len), reduce_scatter4(part) * scale);
+        }
+        return;
+    }
+    const int32_t c = blockIdx.y;
+    const int64_t r0 = (int64_t)blockIdx.x * kPmRows;
+    const uint32_t* tab = m.table + (int64_t)c * p.rows * kPmPages;
+    // pages of the chunk that the block's rows list
+    if (t == 0) used_sh = 0;
+    __syncthreads();
+    uint32_t used = 0;
+    for (int e = t; e < kPmRows * kPmPages; e += kBlock) {
+        const int64_t r = r0 + e / kPmPages;
+        if (r < p.rows && tab[r * kPmPages + e % kPmPages] != kPmNone) used |= 1u << (e % kPmPages);
+    }
+    if (used) atomicOr(&used_sh, used);
+    __syncthreads();
+    used = __builtin_amdgcn_readfirstlane(used_sh);
+    if (used == 0) return;
+    // stage the listed pages: per page eight 1 KiB key chunks and 256 bytes
+    // of scales, the 72 loads dealt to the waves in turn
+    for (int o = wv; o < kPmPages * 9; o += kPmWaves) {
+        const int k = o / 9, part = o % 9;
+        const int64_t pg = (int64_t)c * kPmPages + k;
+        const int32_t page = ((used >> k) & 1u) && pg < p.kv_blocks ? (int32_t)pg : -1;
+        const i32x4 rs = page_rsrc(p.kv, page);
+        const uint32_t base = lds_addr(pages[k]);
+        if (part < 8) {
+            const int s = part * 64 + l;  // 16-byte LDS slot
+            const int key = s >> 3;
+            dma16(rs, key * 128 + (((s & 7) ^ key_swizzle(key & 15)) << 4), base + part * 1024);
+        } else {
+            dma4(rs, 8192 + 4 * l, base + 8192);
+        }
+    }
+    V1_PAGE_BARRIER(0);
+    // Rows of this wave: r0 + wv, r0 + wv + 4, ...  The next row's table
+    // slots, query fragments, weights and length are loaded before the
+    // current row is computed (two register sets, used in turn); every load
+    // is issued from a clamped index and every row issues exactly kPmPages
+    // logit stores (range-checked buffer stores: a page the row does not list
+    // gets a descriptor of length 0), so the wait for a row's data is an
+    // exact count and never drains the next row's loads.
+    const auto tab_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(tab), 0,
+                                                          (int32_t)(p.rows * kPmPages * 4), kRawDword);
+    const auto ctx_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(p.ctx), 0, p.rows * 4, kRawDword);
+    const auto none_rs = __builtin_amdgcn_make_buffer_rsrc(p.logits, 0, 0, kRawDword);
+    struct RowData {
+        u32x4 s[kPmPages / 4];
+        v8i a[HB];
+        float w[HB][4];
+        int32_t ctx;
+    };
+    // Whole head blocks (heads a multiple of 16): the query fragments and
+    // weights load without the per-lane range selects (a row past the end
+    // reads the last row, whose logits it never stores).
+    const bool whole = (p.heads & 15) == 0;
+    auto fetch = [&](int64_t row, RowData& d) __attribute__((always_inline)) {
+        const int32_t rc = (int32_t)min(row, (int64_t)p.rows - 1);
+#pragma unroll
+        for (int i = 0; i < kPmPages / 4; ++i)
+            d.s[i] = __builtin_amdgcn_raw_buffer_load_b128(tab_rs, rc * kPmPages * 4 + 16 * i, 0, 0);
+        if (whole) {
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb) {
+                const int h = hb * 16 + (l & 15);
+                const u32x4* src = reinterpret_cast<const u32x4*>(p.q + ((int64_t)rc * p.heads + h) * 128 + 32 * (l >> 4));
+                const u32x4 x = src[0], y = src[1];
+                d.a[hb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+                const v4f wv4 = *reinterpret_cast<const v4f*>(p.w + (int64_t)rc * p.heads + hb * 16 + 4 * (l >> 4));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d.w[hb][i] = wv4[i];
+            }
+        } else {
+            load_q<HB>(p, row, d.a);
+            load_w<HB>(p, row, d.w);
+        }
+        d.ctx = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(ctx_rs, rc * 4, 0, 0);
+    };
+    auto run = [&](int64_t row, const RowData& d) __attribute__((always_inline)) {
+        uint32_t slot[kPmPages];
+#pragma unroll
+        for (int k = 0; k < kPmPages; ++k) slot[k] = d.s[k / 4][k % 4];
+        const int32_t ctx = min(__builtin_amdgcn_readfirstlane(d.ctx), p.max_context_len);
+        const bool live_row = row < p.rows;
+#pragma unroll
+        for (int k = 0; k < kPmPages; ++k) {
+            const uint32_t sk = __builtin_amdgcn_readfirstlane(slot[k]);
+            const bool live = live_row && sk != kPmNone;
+            if (!live) {
+                // (the store count stays fixed: a zero-length descriptor drops it)
+                __builtin_amdgcn_raw_buffer_store_b32(0u, none_rs, 0, 0, 0);
+                continue;
+            }
+            float v = 0.f;
+            {
+                v8i b[4];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    const u32x4 x = *reinterpret_cast<const u32x4*>(pages[k] + kb * 2048 + boff0);
+                    const u32x4 y = *reinterpret_cast<const u32x4*>(pages[k] + kb * 2048 + boff1);
+                    b[kb] = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+                }
+                float part[4];
+                page_partials_lag<HB, RELU>(d.a, b, d.w, part);
+                v = reduce_scatter4(part) * reinterpret_cast<const float*>(pages[k] + 8192)[l];
+            }
+            // columns [col, col + 64) of the row: logits below its context,
+            // -inf from there to max_context_len with clean_logits
+            const int32_t col = (int32_t)sk * 64;
+            const int32_t end = (p.clean ? p.max_context_len : ctx) - col;
+            const int32_t lim = __builtin_amdgcn_readfirstlane(end > 0 ? (end < 64 ? end : 64) : 0);
+            // (the row's address made scalar explicitly: the descriptor must be)
+            const uint64_t at = reinterpret_cast<uint64_t>(p.logits + min(row, (int64_t)p.rows - 1) * p.logits_stride + col);
+            const uint64_t at_s = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(at >> 32)) << 32) |
+                                  (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)at);
+            const auto rs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<float*>(at_s), 0, lim * 4, kRawDword);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l < ctx - col ? v : -__builtin_huge_valf()), rs, l * 4,
+                                                  0, 0);
+        }
+    };
+    constexpr int kSteps = kPmRows / kPmWaves;
+    static_assert(kSteps % 2 == 0, "rows taken in pairs");
+    if constexpr (kPmPrefetch) {
+        RowData d0, d1;
+        fetch(r0 + wv, d0);
+#pragma unroll 1
+        for (int i = 0; i < kSteps; i += 2) {
+            const int64_t ra = r0 + wv + kPmWaves * i;
+            if (ra >= p.rows) break;
+            fetch(ra + kPmWaves, d1);
+            run(ra, d0);
+            if (ra + kPmWaves >= p.rows) break;
+            fetch(ra + 2 * kPmWaves, d0);
+            run(ra + kPmWaves, d1);
+        }
+    } else {
+#pragma unroll 1
+        for (int i = 0; i < kSteps; ++i) {
+            const int64_t ra = r0 + wv + kPmWaves * i;
+            if (ra >= p.rows) break;
+            RowData d0;
+            fetch(ra, d0);
+            run(ra, d0);
+        }
+    }
+}
+
 // -------------------------------------------- scoring without DeepGEMM
 // The reference's Triton fallbacks for hosts without DeepGEMM or with the
 // query optimisations off (runtime.py:450-466, 565-590).
@@ -1530,6 +1813,12 @@ struct Rows {
         hipLaunchKernelGGL((score_rows<HB, RELU>), g, dim3(kThreads), 0, st, p);
     }
 };
+struct Pages {
+    template <int HB, bool RELU>
+    static void launch(dim3 g, hipStream_t st, const ScoreParams& p, const PmTables& m) {
+        hipLaunchKernelGGL((score_pages<HB, RELU>), g, dim3(kWave * kPmWaves), 0, st, p, m);
+    }
+};
 struct RowsFast {  // (the flagged rows of the union form: 17 heads and more)
     template <int HB, bool RELU>
     static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
@@ -1607,6 +1896,26 @@ extern "C" int64_t v1_score_tables_workspace(int32_t rows, int32_t max_context_l
     return union_layout(rows, max_context_len).total;
 }
 
+namespace {
+int g_page_major = 1;
+}
+
+extern "C" int v1_score_page_major(int32_t enable, int32_t* previous) {
+    V1_REQUIRE(enable == 0 || enable == 1, "score_page_major: enable must be 0 or 1 (got %d)", enable);
+    if (previous) *previous = g_page_major;
+    g_page_major = enable;
+    return V1_OK;
+}
+
+extern "C" int64_t v1_score_pages_workspace(int32_t rows, int32_t max_context_len, int64_t kv_blocks) {
+    // (overflow entries pack the row and the slot in 16 bits each)
+    if (rows < kUnionMinRows || rows > 65535 || max_context_len <= 0 || cdiv(max_context_len, 64) > 65535 ||
+        kv_blocks <= 0)
+        return 0;
+    const PmLayout L = pm_layout(rows, max_context_len, kv_blocks);
+    return L.total - L.table > kPmMaxTableBytes ? 0 : L.total;
+}
+
 extern "C" int v1_score(const v1_score_args* a, void* stream) {
     V1_REQUIRE(a != nullptr, "score: null args");
     V1_REQUIRE(a->heads >= 1 && a->heads <= 64, "score: heads must be in [1, 64]");
@@ -1678,6 +1987,30 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
             default: hipLaunchKernelGGL(score_exact<4>, row_waves, dim3(256), 0, st, p); break;
         }
         return V1_LAUNCHED("score_exact");
+    }
+    // Per-row tables of more than 512 rows with at most 32 heads over a pool
+    // small enough for the dense pair table (one request's pages): the
+    // page-major kernels.  Measured against the page-union plan: 4096 rows x
+    // 32 heads (40 history pages + the shared tail union) 0.153 against
+    // 0.182 ms; at 64 heads (1024 rows of 545 of 1057 pages) 0.493 against
+    // 0.463-0.475 ms, so more heads keep the plan.
+    const int64_t pm_need = v1_score_pages_workspace(a->rows, a->max_context_len, a->kv_blocks);
+    if (g_page_major && hb <= 2 && pm_need > 0 && a->workspace != nullptr && a->workspace_bytes >= pm_need &&
+        (reinterpret_cast<uintptr_t>(a->workspace) & 255) == 0) {
+        const PmLayout L = pm_layout(a->rows, a->max_context_len, a->kv_blocks);
+        uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+        const PmTables m{reinterpret_cast<uint32_t*>(ws + L.table), reinterpret_cast<uint32_t*>(ws + L.overflow),
+                         reinterpret_cast<uint32_t*>(ws + L.count), L.table_words, L.chunks};
+        const int64_t clear_wgs = std::max<int64_t>(1, std::min<int64_t>(cdiv(L.table_words, 256), 4 * (int64_t)v1::device_cus()));
+        hipLaunchKernelGGL(score_pages_clear, dim3((uint32_t)clear_wgs), dim3(256), 0, st, m);
+        int rc = V1_LAUNCHED("score_pages_clear");
+        if (rc != V1_OK) return rc;
+        hipLaunchKernelGGL(score_pages_place, dim3((uint32_t)cdiv(cdiv(a->max_context_len, 64), 256), (uint32_t)a->rows),
+                           dim3(256), 0, st, p, m);
+        rc = V1_LAUNCHED("score_pages_place");
+        if (rc != V1_OK) return rc;
+        launch_hb<Pages>(hb, a->relu != 0, dim3((uint32_t)cdiv(a->rows, kPmRows), (uint32_t)L.chunks + 1), st, p, m);
+        return V1_LAUNCHED("score_pages");
     }
     // Per-row tables of more than 512 rows with a large enough workspace:
     // the union plan, the shared-table kernel over each group's union, and

@@ -8,9 +8,11 @@ k / s_k come from 8448-byte native pages ([64, 1, 132] byte view: 64x128 FP8
 then 64 fp32 scales) through block_table[r, j // 64].  A block table with row
 stride 0 (e.g. `table[None].expand(rows, -1)`) marks rows that share one
 table; they are tiled together so each key page is staged once per 8 rows.
-Per-row tables of more than 512 rows with more than 16 heads (a prefill
-chunk's fine tables) are planned per 8-row group over the union of their
-pages, staged the same way.
+Per-row tables of more than 512 rows (a prefill chunk's fine tables) over a
+pool small enough for a dense (row, pool page) table are scored page-major:
+each work-group stages 8 pool pages once for every row of a 64-row block that
+lists them.  Over larger pools, rows with more than 16 heads are planned per
+8-row group over the union of their pages, staged the same way.
 """
 import ctypes
 
@@ -57,15 +59,29 @@ def fp8_paged_mqa_logits(q, kv_cache, weights, context_lens, block_table, schedu
     elif out.dtype != torch.float32 or out.shape[0] != rows or out.shape[1] < max_context_len or out.stride(1) != 1:
         raise ValueError("out must be float32 [rows, >= max_context_len]")
     # shared tables need the workspace; per-row tables of large batches use
-    # it for the page-union plan (0 bytes: each row on its own)
-    need = (_lib.lib().v1_score_workspace(rows, int(max_context_len)) if block_table.stride(0) == 0
-            else _lib.lib().v1_score_tables_workspace(rows, int(max_context_len)))
+    # it for the page-major pair table over a small pool, else for the
+    # page-union plan (0 bytes: each row on its own)
+    kv_blocks = kv.numel() // PAGE_BYTES
+    if block_table.stride(0) == 0:
+        need = _lib.lib().v1_score_workspace(rows, int(max_context_len))
+    else:
+        need = max(_lib.lib().v1_score_pages_workspace(rows, int(max_context_len), kv_blocks),
+                   _lib.lib().v1_score_tables_workspace(rows, int(max_context_len)))
     ws, ws_bytes = workspace(q.device, need, "score")
-    a = _lib.ScoreArgs(_lib.ptr(q), _lib.ptr(kv), kv.numel() // PAGE_BYTES, _lib.ptr(weights), _lib.ptr(lens),
+    a = _lib.ScoreArgs(_lib.ptr(q), _lib.ptr(kv), kv_blocks, _lib.ptr(weights), _lib.ptr(lens),
                        _lib.ptr(block_table), block_table.stride(0), block_table.shape[1], _lib.ptr(out), out.stride(0),
                        int(max_context_len), rows, heads, int(bool(relu)), int(bool(clean_logits)), ws, ws_bytes)
     _lib.check(_lib.lib().v1_score(ctypes.byref(a), _lib.stream_of(q)), "fp8_paged_mqa_logits")
     return out
+
+
+def page_major(enable):
+    """Allow (True, the default) or forbid the page-major form for per-row
+    tables of large batches over a small pool; returns the previous setting.
+    A switch for tests and measurements."""
+    prev = ctypes.c_int32(0)
+    _lib.check(_lib.lib().v1_score_page_major(int(bool(enable)), ctypes.byref(prev)), "score_page_major")
+    return bool(prev.value)
 
 
 def get_paged_mqa_logits_metadata(context_lens, block_size, num_sms):

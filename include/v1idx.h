@@ -185,6 +185,21 @@ int64_t v1_score_workspace(int32_t rows, int32_t max_context_len);
  * fine tables of runtime.py:538-548 do); groups sharing less than two rows
  * per page, and calls without the workspace, score each row on its own. */
 int64_t v1_score_tables_workspace(int32_t rows, int32_t max_context_len);
+/* Workspace bytes for per-row tables scored page-major (0: not taken).  For
+ * more than 512 rows over a pool of kv_blocks pages whose dense pair table
+ * (rows x kv_blocks x 4 bytes) fits 64 MiB, e.g. a prefill chunk's fine tables
+ * over one request's pages: each work-group stages 8 pool pages in LDS once
+ * and scores every row of a 64-row block that lists them.  v1_score takes
+ * this form when its workspace holds this many bytes (checked before the
+ * page-union plan of v1_score_tables_workspace); the values are those of the
+ * row-by-row kernel, bit for bit.  No counterpart in the reference, which
+ * scores each row's table on its own (runtime.py:538-548). */
+int64_t v1_score_pages_workspace(int32_t rows, int32_t max_context_len, int64_t kv_blocks);
+/* 0 keeps v1_score off the page-major form (then the page-union plan takes
+ * per-row tables of large batches), 1 (the default) allows it; process-wide,
+ * the previous setting goes to *previous (if not NULL).  No counterpart in the
+ * reference: a switch for tests and measurements. */
+int v1_score_page_major(int32_t enable, int32_t* previous);
 int v1_score(const v1_score_args* a, void* stream);
 /* v1_score without a caller workspace and without any allocation: the
  * shared-table path's scratch is a static 16 MiB device array per GPU

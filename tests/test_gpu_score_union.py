@@ -1,10 +1,12 @@
-"""Per-row block tables of large batches through the page-union plan.
+"""Per-row block tables of large batches: page-major and the page-union plan.
 
 Batches of more than 512 rows with per-row tables (the fine tables of a
 prefill chunk, sglang/srt/layers/attention/v1_deepseek/runtime.py:538-548)
-are scored per group of 8 rows over the union of the rows' table pages (17
-heads and more, when the rows share enough of their pages; two queries per
-wave up to 48 heads, one with 64).  The
+are scored page-major over a small pool (each work-group stages 8 pool pages
+once for every row of a 64-row block that lists them), or per group of 8 rows
+over the union of the rows' table pages (17 heads and more, when the rows
+share enough of their pages; two queries per wave up to 48 heads, one with
+64).  Every test runs in both forms (`form`).  The
 result must be the formula of kernels.py:310-313 through each row's own table,
 whatever the tables hold: partly overlapping page sets in each row's own
 order, unequal lengths (empty rows, rows past their table), a page listed
@@ -24,6 +26,14 @@ pytestmark = pytest.mark.gpu
 
 SC = pkg("scoring")
 W = pkg("workloads")
+
+
+@pytest.fixture(params=["pages", "union"])
+def form(request):
+    """page-major allowed (it takes every batch here over a small pool) or off"""
+    prev = SC.page_major(request.param == "pages")
+    yield request.param
+    SC.page_major(prev)
 
 
 def _queries(g, rows, heads, live):
@@ -110,7 +120,7 @@ def _run(dev, q8, w, native, table, lens, width, relu, clean, fill=7.0):
     (600, 16, 2, True, True, 30, 4),      # one head block: row by row
     (529, 7, 7, True, True, 30, 4),       # heads not a multiple of 16: row by row
 ])
-def test_union_plan_vs_reference(dev, rows, heads, live, relu, clean, take, private):
+def test_union_plan_vs_reference(dev, form, rows, heads, live, relu, clean, take, private):
     g = np.random.default_rng(rows * 131 + heads)
     pool_pages, fill = 160, 7.0
     q8, w = _queries(g, rows, heads, live)
@@ -146,7 +156,7 @@ def test_union_plan_vs_reference(dev, rows, heads, live, relu, clean, take, priv
         assert_scores_close(got, ref, bound)
 
 
-def test_union_plan_low_sharing_groups_fall_back(dev):
+def test_union_plan_low_sharing_groups_fall_back(dev, form):
     """Groups whose rows share too little go to the per-row kernel: a batch
     whose first 40 groups are a chunk's rows (the plan) and the rest
     unrelated rows (row by row) gives the reference on every row."""
@@ -165,7 +175,7 @@ def test_union_plan_low_sharing_groups_fall_back(dev):
 
 
 @pytest.mark.parametrize("heads", [32, 64])
-def test_union_plan_rows_bitwise_across_kernels(dev, heads):
+def test_union_plan_rows_bitwise_across_kernels(dev, form, heads):
     """A row gets the same bits whichever kernel scores it: row 8 repeats
     row 0 (query, weights, table, length) inside a group of otherwise
     unrelated rows, which the plan hands to the per-row kernel, while row 0's
@@ -186,7 +196,7 @@ def test_union_plan_rows_bitwise_across_kernels(dev, heads):
     assert_scores_rel(got.astype(np.float64), O.paged_logits(q8, w, pool, tab, lens, width))
 
 
-def test_union_plan_probe_overflow_falls_back(dev):
+def test_union_plan_probe_overflow_falls_back(dev, form):
     """A group whose pages all land on one slot of the plan's hash set (68
     pages of a 34000-page pool with the same multiplicative hash into 512
     slots) probes past the plan's limit and is scored row by row; every row
@@ -216,7 +226,7 @@ def test_union_plan_probe_overflow_falls_back(dev):
 
 
 @pytest.mark.parametrize("heads", [32, 64])
-def test_union_plan_repeats_and_empty_groups(dev, heads):
+def test_union_plan_repeats_and_empty_groups(dev, form, heads):
     """Rows that list one page three times (each later slot in an entry of its
     own), a group whose rows list no valid page at all (every live column
     scores 0, nothing is staged), and a group of empty rows, beside ordinary
@@ -241,3 +251,33 @@ def test_union_plan_repeats_and_empty_groups(dev, heads):
     assert (got[8:16][np.isfinite(ref[8:16])] == 0).all()
     assert np.isneginf(got[24:32]).all()
     assert_scores_rel(got, ref)
+
+
+@pytest.mark.parametrize("heads,relu", [(32, True), (32, False), (20, True), (16, True)])
+def test_page_major_bitwise_equals_row_kernel(dev, heads, relu):
+    """The page-major form (taken for at most 32 heads) gives every row the
+    bits of the row-by-row kernel (the same products in the same order):
+    600 rows scored page-major, then their first 300 alone (a batch of at
+    most 512 rows goes row by row); 20 heads load through the partial head
+    block's range checks."""
+    g = np.random.default_rng(heads * 3 + relu)
+    rows, pool_pages = 600, 120
+    q8, w = _queries(g, rows, heads, heads)
+    if not relu:
+        w *= np.where(g.random(w.shape) < 0.5, -1, 1).astype(np.float32)
+    k8, ks = W.quantize_rows(g.standard_normal((pool_pages * 64, 128), dtype=np.float32))
+    native = W.pack_pages(k8, ks)
+    table = _tables(g, rows, pool_pages, shared_pages=50, take=36, private=3)
+    blocks = table.shape[1]
+    lens = g.integers(1, blocks * 64 + 1, rows).astype(np.int32)
+    width = blocks * 64 + 64
+    prev = SC.page_major(True)
+    try:
+        both = _run(dev, q8, w, native, table, lens, width, relu, True).astype(np.float32)
+    finally:
+        SC.page_major(prev)
+    alone = _run(dev, q8[:300], w[:300], native, table[:300], lens[:300], width, relu, True).astype(np.float32)
+    assert np.array_equal(both[:300].view(np.uint32), alone.view(np.uint32))
+    pool, tab = _padded(native, table, width)
+    if relu:
+        assert_scores_rel(both.astype(np.float64), O.paged_logits(q8, w, pool, tab, lens, width))
