@@ -405,8 +405,11 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
     // zeros) from two head blocks on; with one head block each result is
     // taken as w * max(x, 0) directly (exactly 0 when no head dot is
     // positive): its VALU cost is that of the fold's, and it saves the
-    // linear-term MFMA (a third of the block's) and the exact pass.
-    constexpr bool kFold = RELU && HB > 1;
+    // linear-term MFMA (a third of the block's) and the exact pass.  The
+    // union form (per-row tables) takes ReLU directly at every head count:
+    // its values are then those of score_rows and the page-major kernels,
+    // bit for bit, whichever of them scores a row.
+    constexpr bool kFold = RELU && HB > 1 && !UNION;
     constexpr int kWaves = kQueriesPerGroup / QPW;
     constexpr int kBlock = kWave * kWaves;
     constexpr int kKeyDma = 8 / kWaves;       // 1 KiB key chunks per wave and page
@@ -946,13 +949,7 @@ __global__ __launch_bounds__(kWave * kQueriesPerGroup / QPW) void score_shared(S
 // (up to kRowPids), so a page's key loads never wait on its table entry.
 constexpr int kRowPids = 2048;
 
-// FAST: the values of score_shared, bit for bit: the ReLU path takes the
-// linear-term pieces plus the |x| sum with the halved weights of the query's
-// record, and marks pages with a key near zero for score_exact; the signed
-// path takes the record's weights.  (The rows of a batch scored through the
-// union plan that score_rows takes instead then get the same values as the
-// plan's rows; otherwise ReLU is applied directly.)
-template <int HB, bool RELU, bool FAST = false>
+template <int HB, bool RELU>
 __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
     __shared__ int32_t pid_s[kRowPids];
     const int l = __lane_id(), wv = threadIdx.x / kWave;
@@ -983,33 +980,7 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
         v8i a[HB];
         float w[HB][4];
         load_q<HB>(p, row, a);
-        // FAST: the record's weights, linear-term pieces (both queries of
-        // score_shared's row block are this row: its result rows of the
-        // first query are the ones kept) and exact-path threshold
-        v8i alin = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-        float coef[2] = {0.f, 0.f}, exact_thr = 0.f;
-        if constexpr (FAST) {
-            const uint8_t* rec = p.pieces + row * kPieceRowBytes;
-#pragma unroll
-            for (int hb = 0; hb < HB; ++hb) {
-                const v4f x = *reinterpret_cast<const v4f*>(rec + kRecWeights + (hb * 16 + 4 * (l >> 4)) * 4);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) w[hb][i] = x[i];
-            }
-            if (RELU) {
-                const float2 c2 = *reinterpret_cast<const float2*>(rec + kRecScales + 8 * (l >> 4));
-                coef[0] = c2.x;
-                coef[1] = c2.y;
-                exact_thr = *reinterpret_cast<const float*>(rec + kRecBound);
-                const int rr = l & 15;
-                const int piece = 2 * (rr >> 2) + (rr & 1);
-                const u32x4* src = reinterpret_cast<const u32x4*>(rec + piece * 128 + 32 * (l >> 4));
-                const u32x4 x = src[0], y = src[1];
-                alin = v8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
-            }
-        } else {
-            load_w<HB>(p, row, w);
-        }
+        load_w<HB>(p, row, w);
         auto fetch = [&](int32_t s, int32_t pg, v8i (&b)[4], float& scale) __attribute__((always_inline)) {
             const int32_t page = pool_page(s, pg);
             if (page < 0) return false;
@@ -1027,38 +998,8 @@ __global__ __launch_bounds__(kThreads) void score_rows(ScoreParams p) {
             float out = 0.f;
             if (ok) {
                 float part[4];
-                if constexpr (FAST) {
-                    // score_shared's consume order: the linear block sets the
-                    // partial, then every head block's four results in order
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) {
-                        float acc = 0.f;
-                        if (RELU) {
-                            const v4f x = mfma_fp8(alin, b[kb]);
-                            acc = fmaf(coef[1], x[1], coef[0] * x[0]);
-                        }
-#pragma unroll
-                        for (int hb = 0; hb < HB; ++hb) {
-                            const v4f d = mfma_fp8(a[hb], b[kb]);
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const float prev = (!RELU && hb == 0 && i == 0) ? 0.f : acc;
-                                acc = fmaf(w[hb][i], RELU ? fabsf(d[i]) : d[i], prev);
-                            }
-                        }
-                        part[kb] = acc;
-                    }
-                } else {
-                    page_partials_lag<HB, RELU>(a, b, w, part);
-                }
+                page_partials_lag<HB, RELU>(a, b, w, part);
                 out = reduce_scatter4(part);
-                if (FAST && RELU) {
-                    const uint64_t near = __builtin_amdgcn_ballot_w64(fabsf(out) <= exact_thr && pg * 64 + l < ctx);
-                    if (near != 0ull && l == 0) {
-                        const int32_t words = (((p.max_context_len + 63) >> 6) + 31) >> 5;
-                        atomicOr(p.exact_pages + row * words + (pg >> 5), 1u << (pg & 31));
-                    }
-                }
             } else {
                 scale = 0.f;
             }
@@ -1425,24 +1366,42 @@ constexpr int kPmRows = 16 * kPmWaves;     // rows per work item
 constexpr uint32_t kPmNone = 0xffffffffu;
 constexpr int64_t kPmMaxTableBytes = 64ll << 20;
 
+// Chunks are cut from the pool pages the batch lists, in pool order (a
+// bitmap of listed pages and each page's rank among them), so a chunk's
+// pages are all live even where the listed pages are spread over a larger
+// pool (a fine pool of 2048 page slots holding 1024 built pages).
+constexpr int kPmMaxPool = 32768;          // pool pages (a 1024-word bitmap)
+constexpr int kPmReplicas = 16;            // copies of the bitmap the marks are spread over
+constexpr int kPmRankThreads = 1024;
+
 struct PmTables {
-    uint32_t* table;     // [chunks][rows][kPmPages] table slot of (row, pool page), kPmNone: not listed
-    uint32_t* overflow;  // (row << 16 | slot) of the pairs the table has no room for
-    uint32_t* count;     // overflow entries
+    uint32_t* table;      // [chunks][rows][kPmPages] table slot of (row, listed page), kPmNone: not listed
+    uint32_t* overflow;   // (row << 16 | slot) of the pairs the table has no room for
+    uint32_t* count;      // [0] overflow entries, [1] listed pool pages
+    uint32_t* bits;       // [kPmReplicas][words] pool pages some row lists (replica 0: all, after the ranks)
+    uint32_t* word_base;  // [words] listed pages before each bitmap word
+    int32_t* listed;      // listed pool pages in pool order (the rank's page)
     int64_t table_words;  // 16-byte words of the table
     int32_t chunks;
+    int32_t words;
+    int32_t compact;      // chunks of listed pages (else of consecutive pool pages)
 };
 
 struct PmLayout {
-    int64_t count, overflow, table, total, table_words;
-    int32_t chunks;
+    int64_t count, overflow, bits, word_base, listed, table, total, table_words;
+    int32_t chunks, words;
 };
 PmLayout pm_layout(int32_t rows, int32_t max_context_len, int64_t kv_blocks) {
     PmLayout L{};
+    auto up = [](int64_t x) { return (x + 255) & ~int64_t(255); };
     L.chunks = (int32_t)cdiv(kv_blocks, kPmPages);
+    L.words = (int32_t)cdiv(kv_blocks, 32);
     L.count = 0;
     L.overflow = 256;
-    L.table = (L.overflow + (int64_t)rows * cdiv(max_context_len, 64) * 4 + 255) & ~int64_t(255);
+    L.bits = up(L.overflow + (int64_t)rows * cdiv(max_context_len, 64) * 4);
+    L.word_base = up(L.bits + (int64_t)kPmReplicas * L.words * 4);
+    L.listed = up(L.word_base + (int64_t)L.words * 4);
+    L.table = up(L.listed + kv_blocks * 4);
     const int64_t table_bytes = (int64_t)L.chunks * rows * kPmPages * 4;
     L.table_words = table_bytes / 16;
     L.total = L.table + table_bytes;
@@ -1451,10 +1410,64 @@ PmLayout pm_layout(int32_t rows, int32_t max_context_len, int64_t kv_blocks) {
 
 __global__ __launch_bounds__(256) void score_pages_clear(PmTables m) {
     const int64_t stride = (int64_t)gridDim.x * 256;
+    const int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
     uint4* s = reinterpret_cast<uint4*>(m.table);
-    for (int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x; k < m.table_words; k += stride)
-        s[k] = make_uint4(kPmNone, kPmNone, kPmNone, kPmNone);
-    if (blockIdx.x == 0 && threadIdx.x == 0) *m.count = 0;
+    for (int64_t k = i0; k < m.table_words; k += stride) s[k] = make_uint4(kPmNone, kPmNone, kPmNone, kPmNone);
+    for (int64_t k = i0; k < (int64_t)kPmReplicas * m.words; k += stride) m.bits[k] = 0u;
+    if (i0 < 2) m.count[i0] = 0u;
+}
+
+// The listed-page bitmap: each work-group ORs the valid pages of 16 rows'
+// tables into an LDS bitmap, then its non-zero words into replica b % 16 of
+// the global bitmap (a small pool's few words would otherwise take a global
+// atomic from every work-group on one address); the rank kernel ORs the
+// replicas.
+__global__ __launch_bounds__(256) void score_pages_mark(ScoreParams p, PmTables m) {
+    __shared__ uint32_t lb[kPmMaxPool / 32];
+    const int t = threadIdx.x;
+    for (int k = t; k < m.words; k += 256) lb[k] = 0u;
+    __syncthreads();
+    for (int rr = 0; rr < 16; ++rr) {
+        const int64_t row = (int64_t)blockIdx.x * 16 + rr;
+        if (row >= p.rows) break;
+        const int32_t row_pages = (min(p.ctx[row], p.max_context_len) + 63) / 64;
+        for (int32_t j = t; j < row_pages; j += 256) {
+            const int32_t page = page_of(p, row, j);
+            if (page >= 0) atomicOr(&lb[page >> 5], 1u << (page & 31));
+        }
+    }
+    __syncthreads();
+    uint32_t* rep = m.bits + (int64_t)(blockIdx.x % kPmReplicas) * m.words;
+    for (int k = t; k < m.words; k += 256)
+        if (lb[k]) atomicOr(&rep[k], lb[k]);
+}
+
+// Ranks: one work-group, one bitmap word per thread (words <= 1024).
+__global__ __launch_bounds__(kPmRankThreads) void score_pages_rank(PmTables m) {
+    __shared__ uint32_t part[kPmRankThreads / kWave];
+    const int t = threadIdx.x, w = t / kWave, l = __lane_id();
+    uint32_t bits = 0u;
+    if (t < m.words) {
+#pragma unroll
+        for (int r = 0; r < kPmReplicas; ++r) bits |= m.bits[(int64_t)r * m.words + t];
+    }
+    const uint32_t c = (uint32_t)__popc(bits);
+    const uint32_t incl = wave_inclusive_sum(c);
+    if (l == kWave - 1) part[w] = incl;
+    __syncthreads();
+    uint32_t base = incl - c;
+    for (int k = 0; k < w; ++k) base += part[k];
+    if (t < m.words) {
+        m.word_base[t] = base;
+        m.bits[t] = bits;  // (replica 0 becomes the union, which the place kernel reads)
+    }
+    uint32_t left = bits, at = base;
+    while (left) {
+        const int b = __builtin_ctz(left);
+        left &= left - 1u;
+        m.listed[at++] = t * 32 + b;
+    }
+    if (t == kPmRankThreads - 1) m.count[1] = base + c;
 }
 
 __global__ __launch_bounds__(256) void score_pages_place(ScoreParams p, PmTables m) {
@@ -1466,7 +1479,10 @@ __global__ __launch_bounds__(256) void score_pages_place(ScoreParams p, PmTables
     const int32_t row_pages = (ctx + 63) / 64;
     const int32_t page = j < row_pages ? page_of(p, row, j) : -1;
     if (page >= 0) {
-        uint32_t* at = m.table + (((int64_t)(page / kPmPages) * p.rows + row) * kPmPages + page % kPmPages);
+        const uint32_t rank =
+            m.compact ? m.word_base[page >> 5] + (uint32_t)__popc(m.bits[page >> 5] & ((1u << (page & 31)) - 1u))
+                      : (uint32_t)page;
+        uint32_t* at = m.table + (((int64_t)(rank / kPmPages) * p.rows + row) * kPmPages + rank % kPmPages);
         if (atomicCAS(at, kPmNone, (uint32_t)j) != kPmNone) m.overflow[atomicAdd(m.count, 1u)] = (uint32_t)(row << 16) | (uint32_t)j;
         return;
     }
@@ -1528,10 +1544,12 @@ __global__ __launch_bounds__(kWave * kPmWaves) void score_pages(ScoreParams p, P
     if (used == 0) return;
     // stage the listed pages: per page eight 1 KiB key chunks and 256 bytes
     // of scales, the 72 loads dealt to the waves in turn
+    const int32_t nlisted = m.compact ? __builtin_amdgcn_readfirstlane((int32_t)m.count[1]) : (int32_t)p.kv_blocks;
     for (int o = wv; o < kPmPages * 9; o += kPmWaves) {
         const int k = o / 9, part = o % 9;
-        const int64_t pg = (int64_t)c * kPmPages + k;
-        const int32_t page = ((used >> k) & 1u) && pg < p.kv_blocks ? (int32_t)pg : -1;
+        const int32_t idx = c * kPmPages + k;
+        const int32_t page = !((used >> k) & 1u) || idx >= nlisted ? -1
+                             : m.compact ? __builtin_amdgcn_readfirstlane(m.listed[min(idx, nlisted - 1)]) : idx;
         const i32x4 rs = page_rsrc(p.kv, page);
         const uint32_t base = lds_addr(pages[k]);
         if (part < 8) {
@@ -1819,12 +1837,6 @@ struct Pages {
         hipLaunchKernelGGL((score_pages<HB, RELU>), g, dim3(kWave * kPmWaves), 0, st, p, m);
     }
 };
-struct RowsFast {  // (the flagged rows of the union form: 17 heads and more)
-    template <int HB, bool RELU>
-    static void launch(dim3 g, hipStream_t st, const ScoreParams& p) {
-        if constexpr (HB >= 2) hipLaunchKernelGGL((score_rows<HB, RELU, true>), g, dim3(kThreads), 0, st, p);
-    }
-};
 
 template <typename K, int HB, typename... X>
 void launch_relu(bool relu, dim3 g, hipStream_t st, const ScoreParams& p, const X&... x) {
@@ -1910,7 +1922,7 @@ extern "C" int v1_score_page_major(int32_t enable, int32_t* previous) {
 extern "C" int64_t v1_score_pages_workspace(int32_t rows, int32_t max_context_len, int64_t kv_blocks) {
     // (overflow entries pack the row and the slot in 16 bits each)
     if (rows < kUnionMinRows || rows > 65535 || max_context_len <= 0 || cdiv(max_context_len, 64) > 65535 ||
-        kv_blocks <= 0)
+        kv_blocks <= 0 || kv_blocks > kPmMaxPool)
         return 0;
     const PmLayout L = pm_layout(rows, max_context_len, kv_blocks);
     return L.total - L.table > kPmMaxTableBytes ? 0 : L.total;
@@ -1988,23 +2000,36 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         }
         return V1_LAUNCHED("score_exact");
     }
-    // Per-row tables of more than 512 rows with at most 32 heads over a pool
-    // small enough for the dense pair table (one request's pages): the
-    // page-major kernels.  Measured against the page-union plan: 4096 rows x
-    // 32 heads (40 history pages + the shared tail union) 0.153 against
-    // 0.182 ms; at 64 heads (1024 rows of 545 of 1057 pages) 0.493 against
-    // 0.463-0.475 ms, so more heads keep the plan.
+    // Per-row tables of more than 512 rows over a pool small enough for the
+    // dense pair table (one request's pages): the page-major kernels.
+    // Measured against the page-union plan: 4096 rows x 32 heads (40 history
+    // pages + the shared tail union) 0.153 against 0.182 ms; 1024 rows x 64
+    // heads listing 545 of 1057 pages spread over a 2116-page pool 0.424
+    // against 0.463-0.48 ms (chunks of listed pages; 0.493 ms in chunks of
+    // consecutive pool pages).
     const int64_t pm_need = v1_score_pages_workspace(a->rows, a->max_context_len, a->kv_blocks);
-    if (g_page_major && hb <= 2 && pm_need > 0 && a->workspace != nullptr && a->workspace_bytes >= pm_need &&
+    if (g_page_major && pm_need > 0 && a->workspace != nullptr && a->workspace_bytes >= pm_need &&
         (reinterpret_cast<uintptr_t>(a->workspace) & 255) == 0) {
         const PmLayout L = pm_layout(a->rows, a->max_context_len, a->kv_blocks);
         uint8_t* ws = static_cast<uint8_t*>(a->workspace);
         const PmTables m{reinterpret_cast<uint32_t*>(ws + L.table), reinterpret_cast<uint32_t*>(ws + L.overflow),
-                         reinterpret_cast<uint32_t*>(ws + L.count), L.table_words, L.chunks};
+                         reinterpret_cast<uint32_t*>(ws + L.count), reinterpret_cast<uint32_t*>(ws + L.bits),
+                         reinterpret_cast<uint32_t*>(ws + L.word_base), reinterpret_cast<int32_t*>(ws + L.listed),
+                         L.table_words, L.chunks, L.words,
+                         // a pool more than twice a row's pages (listed pages spread thin)
+                         a->kv_blocks > 2 * cdiv(a->max_context_len, 64)};
         const int64_t clear_wgs = std::max<int64_t>(1, std::min<int64_t>(cdiv(L.table_words, 256), 4 * (int64_t)v1::device_cus()));
         hipLaunchKernelGGL(score_pages_clear, dim3((uint32_t)clear_wgs), dim3(256), 0, st, m);
         int rc = V1_LAUNCHED("score_pages_clear");
         if (rc != V1_OK) return rc;
+        if (m.compact) {
+            hipLaunchKernelGGL(score_pages_mark, dim3((uint32_t)cdiv(a->rows, 16)), dim3(256), 0, st, p, m);
+            rc = V1_LAUNCHED("score_pages_mark");
+            if (rc != V1_OK) return rc;
+            hipLaunchKernelGGL(score_pages_rank, dim3(1), dim3(kPmRankThreads), 0, st, m);
+            rc = V1_LAUNCHED("score_pages_rank");
+            if (rc != V1_OK) return rc;
+        }
         hipLaunchKernelGGL(score_pages_place, dim3((uint32_t)cdiv(cdiv(a->max_context_len, 64), 256), (uint32_t)a->rows),
                            dim3(256), 0, st, p, m);
         rc = V1_LAUNCHED("score_pages_place");
@@ -2028,7 +2053,7 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         p.pieces = ws;
         p.work = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes);
         p.exact_pages = reinterpret_cast<uint32_t*>(ws + (int64_t)a->rows * kPieceRowBytes + 256);
-        p.exact_words = a->relu ? exact_words(a->max_context_len) : 0;
+        p.exact_words = 0;  // (ReLU taken directly: no exact pass)
         p.groups = (int32_t)groups;
         p.u_cap = L.cap;
         p.u_level_stride = L.level_stride;
@@ -2041,9 +2066,10 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         p.u_items = u.items;
         p.u_level_n = u.level_n;
         const dim3 row_waves((uint32_t)cdiv(a->rows, 4));
-        hipLaunchKernelGGL(score_prep, row_waves, dim3(256), 0, st, a->q, a->weights, a->rows, a->heads, a->relu, ws,
-                           p.work, p.exact_pages, p.exact_words, reinterpret_cast<uint32_t*>(u.level_n),
-                           (int32_t)kUnionLevels);
+        // (records of the weights alone: the union form takes ReLU directly)
+        hipLaunchKernelGGL(score_prep, row_waves, dim3(256), 0, st, a->q, a->weights, a->rows, a->heads,
+                           a->relu ? 2 : 0, ws, p.work, p.exact_pages, p.exact_words,
+                           reinterpret_cast<uint32_t*>(u.level_n), (int32_t)kUnionLevels);
         int rc = V1_LAUNCHED("score_prep");
         if (rc != V1_OK) return rc;
         const int32_t hslots = plan_slots((int32_t)(kQueriesPerGroup * cdiv(a->max_context_len, 64)));
@@ -2063,22 +2089,13 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         launch_hb<SharedUnion>(hb, a->relu != 0, dim3((uint32_t)((hb == 4 ? 1 : 2) * (int64_t)v1::device_cus())), st, p);
         rc = V1_LAUNCHED("score_shared (union)");
         if (rc != V1_OK) return rc;
-        // flagged rows with the plan's arithmetic (every row of the call gets
-        // the same values whichever kernel scores it), on score_rows' grid
+        // flagged rows row by row (the same values, bit for bit), on score_rows' grid
         ScoreParams pr = p;
         pr.row_filter = u.fallback;
         int64_t per_row = std::max<int64_t>(1, std::min<int64_t>(chunks, cdiv(24 * (int64_t)v1::device_cus(), a->rows)));
         if (per_row > 1 && per_row % 2 == 0) --per_row;
-        launch_hb<RowsFast>(hb, a->relu != 0, dim3((uint32_t)per_row, (uint32_t)a->rows), st, pr);
-        rc = V1_LAUNCHED("score_rows (flagged rows)");
-        if (rc != V1_OK || !a->relu) return rc;
-        switch (hb) {
-            case 1: hipLaunchKernelGGL(score_exact<1>, row_waves, dim3(256), 0, st, p); break;
-            case 2: hipLaunchKernelGGL(score_exact<2>, row_waves, dim3(256), 0, st, p); break;
-            case 3: hipLaunchKernelGGL(score_exact<3>, row_waves, dim3(256), 0, st, p); break;
-            default: hipLaunchKernelGGL(score_exact<4>, row_waves, dim3(256), 0, st, p); break;
-        }
-        return V1_LAUNCHED("score_exact");
+        launch_hb<Rows>(hb, a->relu != 0, dim3((uint32_t)per_row, (uint32_t)a->rows), st, pr);
+        return V1_LAUNCHED("score_rows (flagged rows)");
     }
     // About 24 work-groups per CU in all, each striding over its row's
     // chunks, and an odd count per row.  Work-groups are dealt to the 8 XCDs

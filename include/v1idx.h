@@ -186,10 +186,10 @@ int64_t v1_score_workspace(int32_t rows, int32_t max_context_len);
  * per page, and calls without the workspace, score each row on its own. */
 int64_t v1_score_tables_workspace(int32_t rows, int32_t max_context_len);
 /* Workspace bytes for per-row tables scored page-major (0: not taken).  For
- * more than 512 rows over a pool of kv_blocks pages whose dense pair table
- * (rows x kv_blocks x 4 bytes) fits 64 MiB, e.g. a prefill chunk's fine tables
- * over one request's pages: each work-group stages 8 pool pages in LDS once
- * and scores every row of a 64-row block that lists them.  v1_score takes
+ * more than 512 rows over a pool of at most 32768 pages whose dense pair
+ * table (rows x kv_blocks x 4 bytes) fits 64 MiB, e.g. a prefill chunk's fine
+ * tables over one request's pages: each work-group stages 8 listed pool pages
+ * in LDS once and scores every row of a 64-row block that lists them.  v1_score takes
  * this form when its workspace holds this many bytes (checked before the
  * page-union plan of v1_score_tables_workspace); the values are those of the
  * row-by-row kernel, bit for bit.  No counterpart in the reference, which

@@ -253,15 +253,17 @@ def test_union_plan_repeats_and_empty_groups(dev, form, heads):
     assert_scores_rel(got, ref)
 
 
-@pytest.mark.parametrize("heads,relu", [(32, True), (32, False), (20, True), (16, True)])
-def test_page_major_bitwise_equals_row_kernel(dev, heads, relu):
-    """The page-major form (taken for at most 32 heads) gives every row the
-    bits of the row-by-row kernel (the same products in the same order):
-    600 rows scored page-major, then their first 300 alone (a batch of at
-    most 512 rows goes row by row); 20 heads load through the partial head
-    block's range checks."""
-    g = np.random.default_rng(heads * 3 + relu)
-    rows, pool_pages = 600, 120
+@pytest.mark.parametrize("heads,relu,pool_pages", [(64, True, 120), (64, True, 80), (32, True, 120),
+                                                    (32, False, 80), (20, True, 120), (16, True, 80)])
+def test_page_major_bitwise_equals_row_kernel(dev, heads, relu, pool_pages):
+    """The page-major form gives every row the bits of the row-by-row kernel
+    (the same products in the same order): 600 rows scored page-major, then
+    their first 300 alone (a batch of at most 512 rows goes row by row); 20
+    heads load through the partial head block's range checks.  A 120-page
+    pool (more than twice a row's 42 pages) is cut into chunks of listed
+    pages, an 80-page one into chunks of consecutive pool pages."""
+    g = np.random.default_rng(heads * 3 + relu + pool_pages)
+    rows = 600
     q8, w = _queries(g, rows, heads, heads)
     if not relu:
         w *= np.where(g.random(w.shape) < 0.5, -1, 1).astype(np.float32)
