@@ -1372,6 +1372,7 @@ constexpr int64_t kPmMaxTableBytes = 64ll << 20;
 // pool (a fine pool of 2048 page slots holding 1024 built pages).
 constexpr int kPmMaxPool = 32768;          // pool pages (a 1024-word bitmap)
 constexpr int kPmReplicas = 16;            // copies of the bitmap the marks are spread over
+constexpr int kPmMarkRows = 4;             // rows per work-group of the marks
 constexpr int kPmRankThreads = 1024;
 
 struct PmTables {
@@ -1417,8 +1418,9 @@ __global__ __launch_bounds__(256) void score_pages_clear(PmTables m) {
     if (i0 < 2) m.count[i0] = 0u;
 }
 
-// The listed-page bitmap: each work-group ORs the valid pages of 16 rows'
-// tables into an LDS bitmap, then its non-zero words into replica b % 16 of
+// The listed-page bitmap: each work-group ORs the valid pages of
+// kPmMarkRows rows' tables into an LDS bitmap, then its non-zero words into
+// replica b % 16 of
 // the global bitmap (a small pool's few words would otherwise take a global
 // atomic from every work-group on one address); the rank kernel ORs the
 // replicas.
@@ -1427,8 +1429,8 @@ __global__ __launch_bounds__(256) void score_pages_mark(ScoreParams p, PmTables 
     const int t = threadIdx.x;
     for (int k = t; k < m.words; k += 256) lb[k] = 0u;
     __syncthreads();
-    for (int rr = 0; rr < 16; ++rr) {
-        const int64_t row = (int64_t)blockIdx.x * 16 + rr;
+    for (int rr = 0; rr < kPmMarkRows; ++rr) {
+        const int64_t row = (int64_t)blockIdx.x * kPmMarkRows + rr;
         if (row >= p.rows) break;
         const int32_t row_pages = (min(p.ctx[row], p.max_context_len) + 63) / 64;
         for (int32_t j = t; j < row_pages; j += 256) {
@@ -2023,7 +2025,7 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         int rc = V1_LAUNCHED("score_pages_clear");
         if (rc != V1_OK) return rc;
         if (m.compact) {
-            hipLaunchKernelGGL(score_pages_mark, dim3((uint32_t)cdiv(a->rows, 16)), dim3(256), 0, st, p, m);
+            hipLaunchKernelGGL(score_pages_mark, dim3((uint32_t)cdiv(a->rows, kPmMarkRows)), dim3(256), 0, st, p, m);
             rc = V1_LAUNCHED("score_pages_mark");
             if (rc != V1_OK) return rc;
             hipLaunchKernelGGL(score_pages_rank, dim3(1), dim3(kPmRankThreads), 0, st, m);
