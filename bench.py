@@ -37,8 +37,8 @@ PCG64, resident in HBM before timing starts).  Workloads (--config):
 Prints one JSON line: queries/sec, per-stage times, the roofline of the
 dominant kernel and the CPU baseline (the reference's torch expressions on
 the host cores, on a bounded sample of the same workload).  With the default
-config 4 the line also carries "configs": configs 1, 2, 3 and 5 measured the
-same way at their own shapes (--with selects others, "" none), each with its
+config 4 the line also carries "configs": configs 1, 2, 3, 5, 7 and 9 measured
+the same way at their own shapes (--with selects others, "" none), each with its
 rate, step time, stage times, dominant-kernel roofline and a shorter CPU
 sample (--with-cpu-budget seconds).
 """
@@ -117,7 +117,7 @@ def parse():
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work (0 = skip)")
     ap.add_argument("--with", dest="with_configs", default=None, metavar="LIST",
                     help="comma-separated further configs measured after the main one and reported under "
-                         "\"configs\" (default with config 4: 1,2,3,5; \"\" for none)")
+                         "\"configs\" (default with config 4: 1,2,3,5,7,9; \"\" for none)")
     ap.add_argument("--with-cpu-budget", type=float, default=3.0,
                     help="seconds of CPU baseline work per further config")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -973,7 +973,7 @@ def main():
             "dtype": "fp8-e4m3 score / fp32 accumulate / int32 indices / u8 rows", **rec}
     more = args.with_configs
     if more is None:
-        more = "1,2,3,5" if args.config == 4 else ""
+        more = "1,2,3,5,7,9" if args.config == 4 else ""
     configs = [int(c) for c in more.split(",") if c.strip()]
     if configs:
         # the other workloads of the metric, each at its own synthetic shape,
