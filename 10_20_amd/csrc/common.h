@@ -110,11 +110,16 @@ inline uint32_t small_div_magic(uint32_t d) {
 // strict order) held in registers: thread t holds
 // elements t*E .. t*E+E-1 (threads at or past n / E hold none and only join
 // the barriers).  Pairs (e, e ^ j) inside a thread swap registers, pairs
-// inside a wave meet through lane shuffles, and pairs across waves through
+// inside a wave meet through lane permutes, and pairs across waves through
 // LDS, two buffers used in turn with one barrier per such step: of the 66
-// steps of a 2048-key network, 6 cross waves.
+// steps of a 2048-key network, 6 cross waves.  Every pair costs one 64-bit
+// compare; which of the two an element keeps (the larger where its half of
+// the run sorts descending) is fixed per thread for the steps with j >= E,
+// since e & j and e & k then do not depend on the element's index within the
+// thread.
+// (the larger of a, b where keep_max, else the smaller; a == b keeps a)
 __device__ __forceinline__ uint64_t bitonic_keep(uint64_t a, uint64_t b, bool keep_max) {
-    return keep_max ? (a > b ? a : b) : (a > b ? b : a);
+    return ((a < b) == keep_max) ? b : a;
 }
 
 template <int E, int J>
@@ -124,8 +129,9 @@ __device__ __forceinline__ void step_in_thread(uint64_t (&v)[E], int e0, int k, 
         if ((i & J) == 0) {
             const bool desc = last || (((e0 + i) & k) == 0);
             const uint64_t a = v[i], b = v[i + J];
-            v[i] = bitonic_keep(a, b, desc);
-            v[i + J] = bitonic_keep(a, b, !desc);
+            const bool swap = (a < b) == desc;
+            v[i] = swap ? b : a;
+            v[i + J] = swap ? a : b;
         }
     }
 }
@@ -135,6 +141,7 @@ __device__ __forceinline__ void step_in_thread(uint64_t (&v)[E], int e0, int k, 
 template <int E>
 __device__ __forceinline__ void bitonic_desc_regs(uint64_t (&v)[E], int n, uint64_t* buf0, uint64_t* buf1, int group) {
     const int e0 = (int)threadIdx.x * E;
+    const int lane = (int)(threadIdx.x & (kWave - 1));
     const bool live = e0 < n;
     int flip = 0;
     for (int k = 2; k <= group; k <<= 1) {
@@ -145,16 +152,18 @@ __device__ __forceinline__ void bitonic_desc_regs(uint64_t (&v)[E], int n, uint6
                 if (E > 2 && j == 2) step_in_thread<E, (E > 2 ? 2 : 1)>(v, e0, k, last);
                 if (E > 4 && j == 4) step_in_thread<E, (E > 4 ? 4 : 1)>(v, e0, k, last);
                 if (E > 8 && j == 8) step_in_thread<E, (E > 8 ? 8 : 1)>(v, e0, k, last);
-            } else if (j / E < kWave) {
-                const int d = j / E;
+                continue;
+            }
+            // (j >= E: the same for every element of the thread)
+            const bool keep_max = ((e0 & j) == 0) == (last || (e0 & k) == 0);
+            if (j / E < kWave) {
+                const int addr = (lane ^ (j / E)) << 2;  // partner lane, as ds_bpermute's byte address
 #pragma unroll
                 for (int i = 0; i < E; ++i) {
-                    const int e = e0 + i;
                     const uint64_t a = v[i];
-                    const uint32_t blo = (uint32_t)__shfl_xor((int)(uint32_t)a, d, kWave);
-                    const uint32_t bhi = (uint32_t)__shfl_xor((int)(uint32_t)(a >> 32), d, kWave);
-                    const uint64_t b = ((uint64_t)bhi << 32) | blo;
-                    v[i] = bitonic_keep(a, b, ((e & j) == 0) == (last || (e & k) == 0));
+                    const uint32_t blo = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)(uint32_t)a);
+                    const uint32_t bhi = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)(uint32_t)(a >> 32));
+                    v[i] = bitonic_keep(a, ((uint64_t)bhi << 32) | blo, keep_max);
                 }
             } else {
                 uint64_t* w = flip ? buf1 : buf0;
@@ -165,10 +174,7 @@ __device__ __forceinline__ void bitonic_desc_regs(uint64_t (&v)[E], int n, uint6
                 __syncthreads();
                 if (live)
 #pragma unroll
-                    for (int i = 0; i < E; ++i) {
-                        const int e = e0 + i;
-                        v[i] = bitonic_keep(v[i], w[e ^ j], ((e & j) == 0) == (last || (e & k) == 0));
-                    }
+                    for (int i = 0; i < E; ++i) v[i] = bitonic_keep(v[i], w[(e0 + i) ^ j], keep_max);
             }
         }
     }
