@@ -759,7 +759,8 @@ __device__ void select_exact(const Src& src, uint32_t T, SelSmem& sm, const Emit
 // once (kShortPer keys per thread, position 4 * (g * kBlock + t) + e for load
 // g), so no sample, pivot or candidate stream is needed: the radix passes run
 // over the registers, then the ranks.  Rows with fewer than T keys above -inf
-// take the exact steps.  Ends with a barrier.
+// run the exact steps' all-key radix over the registers too.  Ends with a
+// barrier.
 constexpr int kShort = 8192;
 constexpr int kShortPer = kShort / kBlock;  // 16
 static_assert(kShortPer % 4 == 0, "whole 16-byte loads per thread");
@@ -782,14 +783,31 @@ __device__ void select_short(const Src& src, uint32_t T, SelSmem& sm, const Emit
 #pragma unroll
     for (int i = 0; i < kShortPer; ++i) key_stats(ck[i], cmax, cmin, cc);
     block_stats(cmax, cmin, cc, sm);
-    if (cc < T) {
-        __syncthreads();  // every thread has read sm.red
-        select_exact(src, T, sm, emit);
-        return;
-    }
-    uint32_t tau, r;
-    radix_tau(ck, cmax, cmin, T, sm, tau, r);
     auto pos = [&](int i) { return (uint32_t)(4 * ((i >> 2) * kBlock + t) + (i & 3)); };
+    uint32_t tau, r;
+    if (cc < T) {
+        // fewer than T keys above -inf: every key of the row counts (-inf,
+        // NaN), the radix passes of select_exact run over the registers
+        Radix rx;
+        rx.prefix = 0;
+        rx.pmask = 0;
+        rx.remaining = T;
+        rx.shift = 32;
+        while (rx.shift > 0) {
+            __syncthreads();  // (the previous pass's scan, or sm.red, has been read)
+            clear_hist(sm);
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < kShortPer; ++i)
+                if ((int32_t)pos(i) < n && rx.counts(ck[i], false)) atomicAdd(&sm.hist[rx.digit(ck[i])], 1u);
+            __syncthreads();
+            rx.finish(sm);
+        }
+        tau = rx.prefix;
+        r = rx.remaining;
+    } else {
+        radix_tau(ck, cmax, cmin, T, sm, tau, r);
+    }
 #pragma unroll
     for (int i = 0; i < kShortPer; ++i)
         if ((int32_t)pos(i) < n) Ranker::mark(sm, pos(i), ck[i] > tau, ck[i] == tau);
