@@ -790,6 +790,15 @@ def _adversarial_rows(kind, g, cols):
         bits[pos] = 0x7f800001 + g.integers(0, 1 << 22, int(pos.sum())).astype(np.uint32)
         bits[neg] = 0xff800001 + g.integers(0, 1 << 22, int(neg.sum())).astype(np.uint32)
         return r
+    if kind == "sparse_nan":  # fewer keys above -inf than T, with -NaNs below -inf and +NaNs above +inf
+        r = np.full(cols, -np.inf, np.float32)
+        at = g.permutation(cols)
+        r[at[:1200]] = g.standard_normal(min(1200, cols)).astype(np.float32)
+        bits = r.view(np.uint32)
+        neg, pos = at[1200:1400], at[1400:1500]
+        bits[neg] = 0xff800001 + g.integers(0, 1 << 22, neg.size).astype(np.uint32)
+        bits[pos] = 0x7f800001 + g.integers(0, 1 << 22, pos.size).astype(np.uint32)
+        return r
     if kind == "nan_heavy":  # more +NaNs than T: the pivot falls in the NaN key range
         r = g.standard_normal(cols).astype(np.float32)
         bits = r.view(np.uint32)
@@ -800,7 +809,7 @@ def _adversarial_rows(kind, g, cols):
 
 
 @pytest.mark.parametrize("kind", ["plateau", "ascending", "descending", "neg_inf_heavy", "two_values", "tiny_spread",
-                                  "signed_zero", "nan_sprinkled", "nan_heavy"])
+                                  "signed_zero", "nan_sprinkled", "nan_heavy", "sparse_nan"])
 @pytest.mark.parametrize("cols", [2049, 8192, 9000, 32768, 100000])
 def test_topk_adversarial_rows(dev, kind, cols):
     g = np.random.default_rng(cols)
