@@ -2002,15 +2002,18 @@ extern "C" int v1_score(const v1_score_args* a, void* stream) {
         }
         return V1_LAUNCHED("score_exact");
     }
-    // Per-row tables of more than 512 rows over a pool small enough for the
-    // dense pair table (one request's pages): the page-major kernels.
-    // Measured against the page-union plan: 4096 rows x 32 heads (40 history
-    // pages + the shared tail union) 0.153 against 0.182 ms; 1024 rows x 64
-    // heads listing 545 of 1057 pages spread over a 2116-page pool 0.424
-    // against 0.463-0.48 ms (chunks of listed pages; 0.493 ms in chunks of
-    // consecutive pool pages).
+    // Per-row tables of more than 512 rows and more than 16 heads over a pool
+    // small enough for the dense pair table (one request's pages): the
+    // page-major kernels.  Measured against the page-union plan: 4096 rows x
+    // 32 heads (40 history pages + the shared tail union) 0.153 against
+    // 0.182 ms; 1024 rows x 64 heads listing 545 of 1057 pages spread over a
+    // 2116-page pool 0.424 against 0.463-0.48 ms (chunks of listed pages;
+    // 0.493 ms in chunks of consecutive pool pages).  With one head block a
+    // pair is 4 MFMAs and the placement kernels do not pay: 1024 rows x 16
+    // heads of the reference example's fine tables 0.059 ms page-major
+    // against 0.046 ms row by row.
     const int64_t pm_need = v1_score_pages_workspace(a->rows, a->max_context_len, a->kv_blocks);
-    if (g_page_major && pm_need > 0 && a->workspace != nullptr && a->workspace_bytes >= pm_need &&
+    if (g_page_major && hb > 1 && pm_need > 0 && a->workspace != nullptr && a->workspace_bytes >= pm_need &&
         (reinterpret_cast<uintptr_t>(a->workspace) & 255) == 0) {
         const PmLayout L = pm_layout(a->rows, a->max_context_len, a->kv_blocks);
         uint8_t* ws = static_cast<uint8_t*>(a->workspace);

@@ -190,7 +190,7 @@ int64_t v1_score_tables_workspace(int32_t rows, int32_t max_context_len);
  * table (rows x kv_blocks x 4 bytes) fits 64 MiB, e.g. a prefill chunk's fine
  * tables over one request's pages: each work-group stages 8 listed pool pages
  * in LDS once and scores every row of a 64-row block that lists them.  v1_score takes
- * this form when its workspace holds this many bytes (checked before the
+ * this form for more than 16 heads when its workspace holds this many bytes (checked before the
  * page-union plan of v1_score_tables_workspace); the values are those of the
  * row-by-row kernel, bit for bit.  No counterpart in the reference, which
  * scores each row's table on its own (runtime.py:538-548). */
