@@ -254,12 +254,13 @@ def test_union_plan_repeats_and_empty_groups(dev, form, heads):
 
 
 @pytest.mark.parametrize("heads,relu,pool_pages", [(64, True, 120), (64, True, 80), (32, True, 120),
-                                                    (32, False, 80), (20, True, 120), (16, True, 80)])
+                                                    (32, False, 80), (20, True, 120), (17, True, 80)])
 def test_page_major_bitwise_equals_row_kernel(dev, heads, relu, pool_pages):
     """The page-major form gives every row the bits of the row-by-row kernel
     (the same products in the same order): 600 rows scored page-major, then
     their first 300 alone (a batch of at most 512 rows goes row by row); 20
-    heads load through the partial head block's range checks.  A 120-page
+    and 17 heads load through the partial head block's range checks (16
+    heads or fewer stay row by row at any batch size).  A 120-page
     pool (more than twice a row's 42 pages) is cut into chunks of listed
     pages, an 80-page one into chunks of consecutive pool pages."""
     g = np.random.default_rng(heads * 3 + relu + pool_pages)
